@@ -1,0 +1,263 @@
+// extern "C" entry points declared in include/dsl_gemm.h.
+//
+// Every entry validates its arguments on the host before enqueuing anything,
+// never allocates device memory, never synchronises, never exits; failures
+// return a negative status with a thread-local message.
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "dsl_gemm.h"
+#include "launch.h"
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return DSL_OK;
+}
+
+int hip_status(hipError_t e, const char *what) {
+  if (e == hipSuccess) return ok();
+  return fail(DSL_ERR_HIP, "%s: HIP error %d (%s)", what, (int)e, hipGetErrorString(e));
+}
+
+bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Common checks of a bf16 input matrix.
+int check_input(const char *fn, const void *x, int64_t rows, int64_t cols, int64_t sr,
+                int64_t sc) {
+  if (rows < 0 || cols < 0) return fail(DSL_ERR_ARG, "%s: negative shape (%lld, %lld)", fn,
+                                        (long long)rows, (long long)cols);
+  if (rows == 0 || cols == 0) return DSL_OK;
+  if (!x) return fail(DSL_ERR_ARG, "%s: input pointer is NULL", fn);
+  if (!aligned(x, 2)) return fail(DSL_ERR_ARG, "%s: bf16 input must be 2-byte aligned", fn);
+  if (sr <= 0 || sc <= 0)
+    return fail(DSL_ERR_ARG, "%s: strides must be positive (got %lld, %lld)", fn, (long long)sr,
+                (long long)sc);
+  if (rows >= (int64_t)1 << 31 || cols >= (int64_t)1 << 31)
+    return fail(DSL_ERR_ARG, "%s: dimensions must be < 2^31", fn);
+  return DSL_OK;
+}
+
+int check_out(const char *fn, const void *q, const char *name) {
+  if (!q) return fail(DSL_ERR_ARG, "%s: %s is NULL", fn, name);
+  if (!aligned(q, 16)) return fail(DSL_ERR_ARG, "%s: %s must be 16-byte aligned", fn, name);
+  return DSL_OK;
+}
+
+int check_gemm_dims(const char *fn, int64_t m, int64_t n, int64_t k, int64_t ldc, int kmult,
+                    int out_dtype) {
+  if (m < 0 || n < 0 || k <= 0)
+    return fail(DSL_ERR_ARG, "%s: need m >= 0, n >= 0, k > 0 (got %lld, %lld, %lld)", fn,
+                (long long)m, (long long)n, (long long)k);
+  if (m >= (int64_t)1 << 31 || n >= (int64_t)1 << 31 || k >= (int64_t)1 << 31)
+    return fail(DSL_ERR_ARG, "%s: dimensions must be < 2^31", fn);
+  if (k % kmult != 0)
+    return fail(DSL_ERR_ARG, "%s: k=%lld must be a multiple of %d", fn, (long long)k, kmult);
+  if (ldc < n) return fail(DSL_ERR_ARG, "%s: ldc=%lld < n=%lld", fn, (long long)ldc, (long long)n);
+  if (out_dtype != DSL_OUT_BF16 && out_dtype != DSL_OUT_F32)
+    return fail(DSL_ERR_ARG, "%s: unknown out_dtype %d", fn, out_dtype);
+  return DSL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char *dsl_last_error(void) { return g_err.c_str(); }
+
+int dsl_abi_version(void) { return 1; }
+
+size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
+  (void)rows;
+  (void)cols;
+  return (size_t)dsl::kMaxPartials * sizeof(float);
+}
+
+int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
+                         uint8_t *q, float *scale, void *ws, size_t ws_bytes, void *stream) {
+  const char *fn = "dsl_quant_fp8_tensor";
+  int rc = check_input(fn, x, rows, cols, sr, sc);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return ok();
+  if ((rc = check_out(fn, q, "q"))) return rc;
+  if (!scale) return fail(DSL_ERR_ARG, "%s: scale is NULL", fn);
+  if (!ws || ws_bytes < dsl_quant_workspace_bytes(rows, cols))
+    return fail(DSL_ERR_WORKSPACE, "%s: workspace of %zu bytes required", fn,
+                dsl_quant_workspace_bytes(rows, cols));
+  return hip_status(dsl::launch_quant_fp8_tensor(static_cast<const uint16_t *>(x), rows, cols,
+                                                 sr, sc, q, scale, static_cast<float *>(ws),
+                                                 static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+int dsl_quant_fp8_blocks(const void *x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
+                         int64_t gr, int64_t gc, uint8_t *q, float *scales, void *stream) {
+  const char *fn = "dsl_quant_fp8_blocks";
+  int rc = check_input(fn, x, rows, cols, sr, sc);
+  if (rc) return rc;
+  if (gr <= 0 || gc <= 0)
+    return fail(DSL_ERR_ARG, "%s: group sizes must be positive (got %lld x %lld)", fn,
+                (long long)gr, (long long)gc);
+  if (rows == 0 || cols == 0) return ok();
+  if ((rc = check_out(fn, q, "q"))) return rc;
+  if (!scales) return fail(DSL_ERR_ARG, "%s: scales is NULL", fn);
+  return hip_status(dsl::launch_quant_fp8_blocks(static_cast<const uint16_t *>(x), rows, cols,
+                                                 sr, sc, gr, gc, q, scales,
+                                                 static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+int dsl_quant_mxfp4(const void *x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
+                    uint8_t *q, uint8_t *e8m0, void *stream) {
+  const char *fn = "dsl_quant_mxfp4";
+  int rc = check_input(fn, x, rows, cols, sr, sc);
+  if (rc) return rc;
+  if (cols % 32 != 0)
+    return fail(DSL_ERR_ARG, "%s: cols=%lld must be a multiple of 32", fn, (long long)cols);
+  if (rows == 0 || cols == 0) return ok();
+  if ((rc = check_out(fn, q, "q_packed"))) return rc;
+  if (!e8m0) return fail(DSL_ERR_ARG, "%s: e8m0 is NULL", fn);
+  return hip_status(dsl::launch_quant_mxfp4(static_cast<const uint16_t *>(x), rows, cols, sr, sc,
+                                            q, e8m0, static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+int dsl_quant_nvfp4(const void *x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
+                    uint8_t *q, uint8_t *e4m3s, float *gscale, void *ws, size_t ws_bytes,
+                    void *stream) {
+  const char *fn = "dsl_quant_nvfp4";
+  int rc = check_input(fn, x, rows, cols, sr, sc);
+  if (rc) return rc;
+  if (cols % 16 != 0)
+    return fail(DSL_ERR_ARG, "%s: cols=%lld must be a multiple of 16", fn, (long long)cols);
+  if (rows == 0 || cols == 0) return ok();
+  if ((rc = check_out(fn, q, "q_packed"))) return rc;
+  if (!e4m3s || !gscale) return fail(DSL_ERR_ARG, "%s: scale output is NULL", fn);
+  if (!ws || ws_bytes < dsl_quant_workspace_bytes(rows, cols))
+    return fail(DSL_ERR_WORKSPACE, "%s: workspace of %zu bytes required", fn,
+                dsl_quant_workspace_bytes(rows, cols));
+  return hip_status(dsl::launch_quant_nvfp4(static_cast<const uint16_t *>(x), rows, cols, sr, sc,
+                                            q, e4m3s, gscale, static_cast<float *>(ws),
+                                            static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+size_t dsl_gemm_workspace_bytes(int op, int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0) return 0;
+  if (op == DSL_OP_FP8) return dsl::gemm_workspace_bytes(dsl::MODE_FP8_TENSOR, m, n, k);
+  if (op == DSL_OP_FP4) return dsl::gemm_workspace_bytes(dsl::MODE_MXFP4, m, n, k);
+  return 0;
+}
+
+static int run_gemm(const char *fn, int mode, const uint8_t *a, const uint8_t *b, void *c,
+                    int64_t m, int64_t n, int64_t k, int64_t ldc, int out_dtype, const void *sa,
+                    const void *sb, const float *ga, const float *gb, void *ws, size_t ws_bytes,
+                    void *stream) {
+  if (m == 0 || n == 0) return ok();
+  int rc;
+  if ((rc = check_out(fn, a, "a")) || (rc = check_out(fn, b, "b"))) return rc;
+  if (!c) return fail(DSL_ERR_ARG, "%s: c is NULL", fn);
+  if (!aligned(c, out_dtype == DSL_OUT_F32 ? 4 : 2))
+    return fail(DSL_ERR_ARG, "%s: c is misaligned", fn);
+  const size_t need = dsl::gemm_workspace_bytes(mode, m, n, k);
+  if (need && (!ws || ws_bytes < need || !aligned(ws, 16)))
+    return fail(DSL_ERR_WORKSPACE, "%s: workspace of %zu bytes (16-B aligned) required", fn, need);
+  dsl::GemmArgs p;
+  p.a = a;
+  p.b = b;
+  p.c = c;
+  p.M = (int)m;
+  p.N = (int)n;
+  p.K = (int)k;
+  p.Kb = (mode == dsl::MODE_MXFP4 || mode == dsl::MODE_NVFP4) ? (int)(k / 2) : (int)k;
+  p.ldc = ldc;
+  p.sa = sa;
+  p.sb = sb;
+  p.ga = ga;
+  p.gb = gb;
+  p.ws = static_cast<float *>(ws);
+  p.ksplit = 1;
+  p.out_f32 = out_dtype == DSL_OUT_F32;
+  return hip_status(dsl::launch_gemm(mode, p, static_cast<hipStream_t>(stream)), fn);
+}
+
+int dsl_fp8_gemm(const uint8_t *a, const uint8_t *b, void *c, int64_t m, int64_t n, int64_t k,
+                 int64_t ldc, int out_dtype, int scale_mode, const float *scale_a,
+                 const float *scale_b, void *ws, size_t ws_bytes, void *stream) {
+  const char *fn = "dsl_fp8_gemm";
+  int rc = check_gemm_dims(fn, m, n, k, ldc, 16, out_dtype);
+  if (rc) return rc;
+  if (!scale_a || !scale_b) return fail(DSL_ERR_ARG, "%s: scale pointers must not be NULL", fn);
+  if (scale_mode == DSL_SCALE_TENSOR)
+    return run_gemm(fn, dsl::MODE_FP8_TENSOR, a, b, c, m, n, k, ldc, out_dtype, nullptr, nullptr,
+                    scale_a, scale_b, ws, ws_bytes, stream);
+  if (scale_mode == DSL_SCALE_BLOCK128)
+    return run_gemm(fn, dsl::MODE_FP8_BLOCK, a, b, c, m, n, k, ldc, out_dtype, scale_a, scale_b,
+                    nullptr, nullptr, ws, ws_bytes, stream);
+  return fail(DSL_ERR_ARG, "%s: unknown scale_mode %d", fn, scale_mode);
+}
+
+int dsl_fp4_gemm(const uint8_t *a, const uint8_t *b, void *c, int64_t m, int64_t n, int64_t k,
+                 int64_t ldc, int out_dtype, int fmt, const uint8_t *scale_a,
+                 const uint8_t *scale_b, const float *global_a, const float *global_b, void *ws,
+                 size_t ws_bytes, void *stream) {
+  const char *fn = "dsl_fp4_gemm";
+  int rc = check_gemm_dims(fn, m, n, k, ldc, 32, out_dtype);
+  if (rc) return rc;
+  if (!scale_a || !scale_b) return fail(DSL_ERR_ARG, "%s: scale pointers must not be NULL", fn);
+  if (fmt == DSL_FMT_MXFP4)
+    return run_gemm(fn, dsl::MODE_MXFP4, a, b, c, m, n, k, ldc, out_dtype, scale_a, scale_b,
+                    nullptr, nullptr, ws, ws_bytes, stream);
+  if (fmt == DSL_FMT_NVFP4) {
+    if (!global_a || !global_b)
+      return fail(DSL_ERR_ARG, "%s: NVFP4 needs global_a and global_b", fn);
+    return run_gemm(fn, dsl::MODE_NVFP4, a, b, c, m, n, k, ldc, out_dtype, scale_a, scale_b,
+                    global_a, global_b, ws, ws_bytes, stream);
+  }
+  return fail(DSL_ERR_ARG, "%s: unknown fmt %d", fn, fmt);
+}
+
+int dsl_grouped_fp8_gemm(const uint8_t *x, const uint8_t *w, void *y, const int32_t *offsets,
+                         int64_t num_groups, int64_t total_rows, int64_t n, int64_t k,
+                         int64_t ldy, int out_dtype, const float *sx, const float *sw,
+                         void *stream) {
+  const char *fn = "dsl_grouped_fp8_gemm";
+  if (num_groups <= 0 || num_groups > 2048)
+    return fail(DSL_ERR_ARG, "%s: num_groups=%lld must be in [1, 2048]", fn,
+                (long long)num_groups);
+  int rc = check_gemm_dims(fn, total_rows, n, k, ldy, 16, out_dtype);
+  if (rc) return rc;
+  if (total_rows == 0 || n == 0) return ok();
+  if ((rc = check_out(fn, x, "x")) || (rc = check_out(fn, w, "w"))) return rc;
+  if (!y || !offsets || !sx || !sw) return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
+  dsl::GroupedArgs p;
+  p.x = x;
+  p.w = w;
+  p.y = y;
+  p.offsets = offsets;
+  p.G = (int)num_groups;
+  p.rows = (int)total_rows;
+  p.N = (int)n;
+  p.K = (int)k;
+  p.ldy = ldy;
+  p.sx = sx;
+  p.sw = sw;
+  p.out_f32 = out_dtype == DSL_OUT_F32;
+  return hip_status(dsl::launch_grouped_fp8(p, static_cast<hipStream_t>(stream)), fn);
+}
+
+}  // extern "C"

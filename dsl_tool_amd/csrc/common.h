@@ -1,0 +1,111 @@
+// Shared definitions for the gfx950 quantized-GEMM library.
+//
+// Number formats (bit-exact contract, identical on host and device):
+//   E4M3FN  bias 7, max 448, NaN = S.1111.111, RNE, |x| > 464 -> NaN
+//           (the conversion the reference performs with __nv_fp8_e4m3,
+//           cuda/gemm/fp8_gemm.cu:141-142, restated from the OCP FP8 spec).
+//   E2M1    {0,.5,1,1.5,2,3,4,6}, bit 3 = sign (cuda/gemm/fp4_gemm.cu:30-33),
+//           RNE with saturation to +-6, sign of zero kept; two codes per
+//           byte with the even K index in the low nibble (fp4_gemm.cu:45-47).
+//   E8M0    2^(code-127); MXFP4 exponent = clamp(floor(log2 amax)-2,-127,127).
+//
+// MFMA operand layouts (measured on gfx950 with an in-bounds probe):
+//   v_mfma_scale_f32_16x16x128_f8f6f4
+//     A/B lane l -> row (col) l%16, lane group g = l/16.
+//     FP4: the lane's 16 bytes are K elements [32g, 32g+32) of the 128-K
+//          step (even element in the low nibble); E8M0 scale byte of lane l
+//          (op_sel picks the byte of the 32-bit operand) scales that block.
+//     FP8: bytes 0..15 are K [16g, 16g+16), bytes 16..31 are K [64+16g, ..);
+//          with unit scales any K order shared by A and B gives the same
+//          sum, so FP8 here packs 32 contiguous K bytes per lane.
+//     D:   lane l, register i -> C[4*(l/16)+i][l%16].
+//   v_mfma_f32_16x16x32_bf16: lane l -> row l%16, K [(l/16)*8, +8);
+//     D as above.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define DSL_HD __host__ __device__ __forceinline__
+#define DSL_DEV __device__ __forceinline__
+
+typedef int      v8i  __attribute__((ext_vector_type(8)));
+typedef int      v4i  __attribute__((ext_vector_type(4)));
+typedef int      v2i  __attribute__((ext_vector_type(2)));
+typedef float    v4f  __attribute__((ext_vector_type(4)));
+typedef float    v16f __attribute__((ext_vector_type(16)));
+typedef __bf16   v8bf __attribute__((ext_vector_type(8)));
+typedef __bf16   v2bf __attribute__((ext_vector_type(2)));
+
+namespace dsl {
+
+// ------------------------------------------------------------------ bits --
+DSL_HD uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+DSL_HD float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+
+DSL_HD float bf16_to_f32(uint16_t b) { return u2f((uint32_t)b << 16); }
+
+// float32 -> bf16 bits, round-to-nearest-even, NaN stays NaN.
+DSL_HD uint16_t f32_to_bf16(float f) {
+  uint32_t u = f2u(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// ------------------------------------------------------------------ E4M3 --
+DSL_HD uint8_t e4m3_encode(float x) {
+  uint32_t u = f2u(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t mag = u & 0x7fffffffu;
+  if (mag >= 0x7f800000u) return (uint8_t)(sign | 0x7fu);          // inf / nan
+  if (mag >= 0x3c800000u) {                                        // >= 2^-6
+    uint32_t r = (mag + 0x7ffffu + ((mag >> 20) & 1u)) >> 20;      // RNE to 3 bits
+    int code = (int)r - ((127 - 7) << 3);
+    if (code >= 0x7f) return (uint8_t)(sign | 0x7fu);              // > 464 -> NaN
+    return (uint8_t)(sign | (uint32_t)code);
+  }
+  float a = u2f(mag) * 512.0f;                                     // exact
+  return (uint8_t)(sign | (uint32_t)__builtin_rintf(a));           // RNE, 0..8
+}
+
+DSL_HD float e4m3_decode(uint8_t c) {
+  uint32_t s = (uint32_t)(c & 0x80) << 24;
+  uint32_t e = (c >> 3) & 0xF, m = c & 7;
+  if (e == 0) return u2f(s | f2u((float)m * 0.001953125f));        // m * 2^-9
+  if (e == 15 && m == 7) return u2f(s | 0x7fc00000u);
+  return u2f(s | ((e + 120u) << 23) | (m << 20));
+}
+
+// ------------------------------------------------------------------ E2M1 --
+// Count of thresholds not exceeded; NaN exceeds none and saturates to 7.
+DSL_HD uint32_t e2m1_encode(float v) {
+  uint32_t s = (f2u(v) >> 28) & 0x8u;
+  float a = __builtin_fabsf(v);
+  uint32_t c = 7u - (uint32_t)(a <= 5.0f) - (uint32_t)(a < 3.5f) - (uint32_t)(a <= 2.5f)
+             - (uint32_t)(a < 1.75f) - (uint32_t)(a <= 1.25f) - (uint32_t)(a < 0.75f)
+             - (uint32_t)(a <= 0.25f);
+  return s | c;
+}
+
+// ------------------------------------------------------------------ E8M0 --
+// MXFP4 shared exponent: clamp(floor(log2(amax)) - 2, -127, 127); amax == 0
+// gives -127.  Integer exponent extraction (exact for subnormals).
+DSL_HD int mx_exponent(float amax) {
+  uint32_t u = f2u(amax) & 0x7fffffffu;
+  if (u == 0) return -127;
+  int ex = (int)(u >> 23);
+  int fl = ex > 0 ? ex - 127 : (31 - __builtin_clz(u)) - 149;
+  int e = fl - 2;
+  return e < -127 ? -127 : (e > 127 ? 127 : e);
+}
+
+// 2^-e as float for e in [-127, 126].
+DSL_HD float pow2_neg(int e) { return u2f((uint32_t)(127 - e) << 23); }
+
+// ---------------------------------------------------------- constants ----
+constexpr float kE4M3Max = 448.0f;
+constexpr float kScaleFloor = 1e-12f;
+constexpr float kNvGlobalDiv = 2688.0f;   // 448 * 6
+
+}  // namespace dsl

@@ -1,0 +1,177 @@
+// Dense quantized GEMM: C[M,N] = A[M,K] . W[N,K]^T on gfx950 MFMA.
+// Variant selection (tile shape, split-K) lives in launch_gemm below.
+#include <algorithm>
+
+#include "gemm_core.h"
+
+namespace dsl {
+
+template <int MODE, class Cfg>
+__global__ __launch_bounds__(Cfg::NT) void gemm_tiled_kernel(const GemmArgs p) {
+  __shared__ __align__(16) uint8_t smem[Cfg::LDS];
+  const int nbm = (p.M + Cfg::BM - 1) / Cfg::BM, nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
+  int tmi, tni;
+  tile_coords(blockIdx.x, nbm, nbn, tmi, tni);
+  const int m0 = tmi * Cfg::BM, n0 = tni * Cfg::BN;
+
+  TileView tv;
+  tv.a = p.a + (int64_t)m0 * p.Kb;
+  tv.b = p.b + (int64_t)n0 * p.Kb;
+  tv.a_rows = min(Cfg::BM, p.M - m0);
+  tv.b_rows = min(Cfg::BN, p.N - n0);
+  tv.Kb = p.Kb;
+  tv.K = p.K;
+  tv.sa = tv.sb = nullptr;
+  tv.sa_ld = tv.sb_ld = 0;
+  if constexpr (MODE == MODE_MXFP4 || MODE == MODE_NVFP4) {
+    const int64_t ld = MODE == MODE_MXFP4 ? p.K / 32 : p.K / 16;
+    tv.sa = static_cast<const uint8_t *>(p.sa) + (int64_t)m0 * ld;
+    tv.sb = static_cast<const uint8_t *>(p.sb) + (int64_t)n0 * ld;
+    tv.sa_ld = tv.sb_ld = ld;
+  } else if constexpr (MODE == MODE_FP8_BLOCK) {
+    const int64_t nkg = (p.K + 127) / 128;
+    tv.sa = static_cast<const float *>(p.sa) + (int64_t)m0 * nkg;
+    tv.sb = static_cast<const float *>(p.sb) + (int64_t)(n0 / 128) * nkg;
+    tv.sa_ld = tv.sb_ld = nkg;
+  }
+
+  const int nks = (p.Kb + 127) / 128;
+  int ks0 = 0, ks1 = nks;
+  if (p.ksplit > 1) {
+    const int per = (nks + p.ksplit - 1) / p.ksplit;
+    ks0 = blockIdx.y * per;
+    ks1 = min(nks, ks0 + per);
+  }
+
+  v4f acc[Cfg::TM][Cfg::TN];
+  tile_mainloop<MODE, Cfg>(tv, ks0, ks1, smem, acc);
+
+  float s1 = 1.f, s2 = 1.f;
+  if constexpr (MODE == MODE_FP8_TENSOR || MODE == MODE_NVFP4) {
+    s1 = *p.ga;
+    s2 = *p.gb;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+  const int r16 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int tm = 0; tm < Cfg::TM; ++tm)
+#pragma unroll
+    for (int tn = 0; tn < Cfg::TN; ++tn) {
+      const int col = n0 + wn * Cfg::WN + tn * 16 + r16;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = m0 + wm * Cfg::WM + tm * 16 + 4 * g + i;
+        if (row < p.M && col < p.N) {
+          float v = acc[tm][tn][i];
+          if constexpr (MODE == MODE_FP8_TENSOR || MODE == MODE_NVFP4) v = (v * s1) * s2;
+          if (p.ksplit > 1)
+            unsafeAtomicAdd(p.ws + (int64_t)row * p.N + col, v);
+          else if (p.out_f32)
+            static_cast<float *>(p.c)[(int64_t)row * p.ldc + col] = v;
+          else
+            static_cast<uint16_t *>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16(v);
+        }
+      }
+    }
+}
+
+__global__ void fill_zero_kernel(float4 *__restrict__ p, int64_t n4) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+__global__ void splitk_finalize_kernel(const float *__restrict__ ws, void *__restrict__ c, int M,
+                                       int N, int64_t ldc, int out_f32) {
+  const int64_t total = (int64_t)M * N;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / N, col = i - r * N;
+    if (out_f32) static_cast<float *>(c)[r * ldc + col] = ws[i];
+    else static_cast<uint16_t *>(c)[r * ldc + col] = f32_to_bf16(ws[i]);
+  }
+}
+
+// ----------------------------------------------------------------------------
+// Variant selection.
+// ----------------------------------------------------------------------------
+namespace {
+
+struct Plan {
+  int variant;   // 0: 256x256 (8 waves)  1: 128x128 (4 waves)  2: 64x128  3: 16x256
+  int bm, bn;
+  int ksplit;
+};
+
+Plan plan_for(int M, int N, int Kb) {
+  Plan pl;
+  if (M <= 16) { pl.variant = 3; pl.bm = 16; pl.bn = 256; }
+  else if (M <= 64) { pl.variant = 2; pl.bm = 64; pl.bn = 128; }
+  else if (M <= 128 || N <= 128) { pl.variant = 1; pl.bm = 128; pl.bn = 128; }
+  else { pl.variant = 0; pl.bm = 256; pl.bn = 256; }
+  const int tiles = ((M + pl.bm - 1) / pl.bm) * ((N + pl.bn - 1) / pl.bn);
+  const int nks = (Kb + 127) / 128;
+  int ks = 1;
+  if (tiles < 256) {
+    ks = (256 + tiles - 1) / tiles;
+    const int maxk = nks / 4 > 0 ? nks / 4 : 1;    // keep >= 4 stages per split
+    if (ks > maxk) ks = maxk;
+    if (ks > 16) ks = 16;
+    if (ks < 1) ks = 1;
+  }
+  pl.ksplit = ks;
+  return pl;
+}
+
+template <int MODE, class Cfg>
+void launch_variant(const GemmArgs &p, hipStream_t st) {
+  const int tiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * ((p.N + Cfg::BN - 1) / Cfg::BN);
+  dim3 grid(tiles, p.ksplit, 1);
+  gemm_tiled_kernel<MODE, Cfg><<<grid, Cfg::NT, 0, st>>>(p);
+}
+
+template <int MODE>
+void launch_mode(const Plan &pl, const GemmArgs &p, hipStream_t st) {
+  switch (pl.variant) {
+    case 0: launch_variant<MODE, TileCfg<MODE, 256, 256, 2, 4>>(p, st); break;
+    case 1: launch_variant<MODE, TileCfg<MODE, 128, 128, 2, 2>>(p, st); break;
+    case 2: launch_variant<MODE, TileCfg<MODE, 64, 128, 1, 4>>(p, st); break;
+    default: launch_variant<MODE, TileCfg<MODE, 16, 256, 1, 4>>(p, st); break;
+  }
+}
+
+}  // namespace
+
+size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K) {
+  const int Kb = (mode == MODE_MXFP4 || mode == MODE_NVFP4) ? (int)(K / 2) : (int)K;
+  const Plan pl = plan_for((int)M, (int)N, Kb);
+  return pl.ksplit > 1 ? (size_t)((M * N + 3) / 4) * 4 * sizeof(float) : 0;
+}
+
+hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
+  const Plan pl = plan_for(p.M, p.N, p.Kb);
+  p.ksplit = pl.ksplit;
+  if (p.ksplit > 1) {
+    const int64_t n4 = ((int64_t)p.M * p.N + 3) / 4;   // workspace is rounded up to float4
+    fill_zero_kernel<<<(unsigned)std::min<int64_t>((n4 + 255) / 256, 4096), 256, 0, st>>>(
+        reinterpret_cast<float4 *>(p.ws), n4);
+  }
+  switch (mode) {
+    case MODE_FP8_TENSOR: launch_mode<MODE_FP8_TENSOR>(pl, p, st); break;
+    case MODE_FP8_BLOCK: launch_mode<MODE_FP8_BLOCK>(pl, p, st); break;
+    case MODE_MXFP4: launch_mode<MODE_MXFP4>(pl, p, st); break;
+    default: launch_mode<MODE_NVFP4>(pl, p, st); break;
+  }
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  if (p.ksplit > 1) {
+    const int64_t total = (int64_t)p.M * p.N;
+    splitk_finalize_kernel<<<(unsigned)std::min<int64_t>((total + 255) / 256, 8192), 256, 0, st>>>(
+        p.ws, p.c, p.M, p.N, p.ldc, p.out_f32);
+    e = hipGetLastError();
+  }
+  return e;
+}
+
+}  // namespace dsl

@@ -1,0 +1,63 @@
+// Host-side launcher prototypes shared between the kernel translation units
+// and the C ABI (capi.hip).  Launchers assume arguments were validated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dsl {
+
+constexpr int kMaxPartials = 1024;   // pass-1 amax partials (floats)
+
+// ------------------------------------------------------------- quantize --
+hipError_t launch_quant_fp8_tensor(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
+                                   int64_t sc, uint8_t *q, float *scale, float *partial,
+                                   hipStream_t st);
+hipError_t launch_quant_fp8_blocks(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
+                                   int64_t sc, int64_t gr, int64_t gc, uint8_t *q,
+                                   float *scales, hipStream_t st);
+hipError_t launch_quant_mxfp4(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
+                              int64_t sc, uint8_t *q, uint8_t *e8m0, hipStream_t st);
+hipError_t launch_quant_nvfp4(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
+                              int64_t sc, uint8_t *q, uint8_t *e4m3s, float *gscale,
+                              float *partial, hipStream_t st);
+
+// ---------------------------------------------------------------- GEMMs --
+enum GemmMode { MODE_FP8_TENSOR = 0, MODE_FP8_BLOCK = 1, MODE_MXFP4 = 2, MODE_NVFP4 = 3 };
+
+struct GemmArgs {
+  const uint8_t *a;      // [M][Kb] packed, K-major
+  const uint8_t *b;      // [N][Kb] packed, K-major
+  void *c;               // [M][ldc] bf16 or fp32
+  int M, N, K;           // K in elements
+  int Kb;                // bytes per packed row (FP8: K, FP4: K/2)
+  int64_t ldc;
+  const void *sa;        // FP8_BLOCK: float [M][nkg]; MX: uint8 [M][K/32]; NV: uint8 [M][K/16]
+  const void *sb;        // FP8_BLOCK: float [ceil(N/128)][nkg]; MX/NV as sa for N
+  const float *ga;       // FP8_TENSOR: scale_a; NV: global_a
+  const float *gb;       // FP8_TENSOR: scale_b; NV: global_b
+  float *ws;             // split-K fp32 [M][N] accumulation buffer (zeroed by the launcher)
+  int ksplit;            // >= 1
+  int out_f32;
+};
+
+// Picks a kernel variant for the shape and launches it (plus the split-K
+// zero-fill / finalize kernels when ksplit > 1).
+hipError_t launch_gemm(int mode, GemmArgs args, hipStream_t st);
+// Workspace the launcher will need for this shape (0 if none).
+size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K);
+
+struct GroupedArgs {
+  const uint8_t *x;      // [rows][K]
+  const uint8_t *w;      // [G][N][K]
+  void *y;               // [rows][ldy]
+  const int32_t *offsets;// [G+1] device
+  int G, rows, N, K;
+  int64_t ldy;
+  const float *sx;       // [rows]
+  const float *sw;       // [G][N]
+  int out_f32;
+};
+hipError_t launch_grouped_fp8(GroupedArgs args, hipStream_t st);
+
+}  // namespace dsl

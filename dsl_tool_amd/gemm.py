@@ -1,0 +1,319 @@
+"""Quantized GEMM callables registered under the ``hip`` backend.
+
+The three registered entry points keep the reference's calling convention
+(``dispatcher/dispatcher.py:285-294``: tensors positional, scalars keyword):
+
+* ``fp8_gemm(A, B, scale_a=1.0, scale_b=1.0)``  -- ``gemm.fp8_gemm``
+  (reference: triton/gemm/gemm_kernels.py:104-122).  A [M, K], B [K, N]
+  (pass ``W.t()`` for a K-major weight W[N, K]); result ``(A @ B) * sa * sb``.
+* ``fp4_gemm(A, B, fmt="mxfp4")`` -- ``gemm.fp4_gemm``, new name in the
+  reference's ``<category>.<function>`` scheme (dispatcher/registry.py:6-8);
+  semantics of cuda/gemm/fp4_gemm.cu:92-146 with MXFP4 / NVFP4 scales.
+* ``grouped_gemm(A, B, num_groups)`` -- ``gemm.grouped_gemm``
+  (reference: triton/gemm/gemm_kernels.py:164-182).  An int third argument
+  means fixed-size groups A [G, M, K], B [G, K, N]; a 1-D integer tensor of
+  G+1 offsets means variable-size groups over concatenated rows A [T, K]
+  (cuda/gemm/grouped_gemm.cu:26-32, :77-104).
+
+High-precision inputs (bf16 / fp16 / fp32) are quantized on the GPU first
+(the REST/CLI wire format cannot carry fp8 or packed fp4, dispatcher
+schemas); pre-quantized inputs are accepted too (see each docstring).
+Outputs are allocated here with ``torch.empty`` on ``A.device`` and owned by
+the caller; inputs are never modified.  Work is enqueued on the current
+stream without synchronising.  Every path goes through ``libdsl_gemm.so``;
+there is no CPU or eager fallback.
+"""
+from __future__ import annotations
+
+import numbers
+
+import torch
+
+from . import _native as N
+from . import quant as Q
+
+_HIGH = (torch.bfloat16, torch.float16, torch.float32)
+_FP8 = torch.float8_e4m3fn
+
+
+def _out_code(dtype: torch.dtype) -> int:
+    if dtype == torch.bfloat16:
+        return N.OUT_BF16
+    if dtype == torch.float32:
+        return N.OUT_F32
+    raise ValueError(f"unsupported out_dtype {dtype}; use torch.bfloat16 or torch.float32")
+
+
+def _dev_scalar(v, device) -> torch.Tensor:
+    """A 1-element float32 device tensor from a python number or tensor."""
+    if isinstance(v, torch.Tensor):
+        if v.numel() != 1:
+            raise ValueError("expected a single scale value")
+        return v.reshape(1).to(device=device, dtype=torch.float32)
+    return torch.full((1,), float(v), dtype=torch.float32, device=device)
+
+
+def _require_gpu(*ts):
+    dev = ts[0].device
+    for t in ts:
+        if t.device.type != "cuda":
+            raise ValueError(f"tensors must be on a GPU device (got {t.device})")
+        if t.device != dev:
+            raise ValueError("all tensors must be on the same device")
+    return dev
+
+
+def _k_major(b_kn: torch.Tensor) -> torch.Tensor:
+    """[K, N] operand -> contiguous [N, K] (free when B is W.t())."""
+    w = b_kn.t()
+    return w if w.is_contiguous() else w.contiguous()
+
+
+def _u8(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.uint8 else t.view(torch.uint8)
+
+
+def _gemm_ws(op: int, m: int, n: int, k: int, device) -> torch.Tensor | None:
+    nbytes = N.lib().dsl_gemm_workspace_bytes(op, m, n, k)
+    return torch.empty(nbytes // 4, dtype=torch.float32, device=device) if nbytes else None
+
+
+# ----------------------------------------------------------- packed level --
+
+def fp8_gemm_packed(qa, qw, scale_a, scale_b, *, block: bool = False,
+                    out_dtype=torch.bfloat16, out=None):
+    """GEMM on packed E4M3 codes.
+
+    qa [M, K] and qw [N, K] are contiguous uint8 (or float8_e4m3fn) codes.
+    Per-tensor (block=False): scale_a / scale_b are 1-element float32 device
+    tensors.  Block-scaled (block=True): scale_a [M, ceil(K/128)] and
+    scale_b [ceil(N/128), ceil(K/128)] float32.
+    """
+    dev = _require_gpu(qa, qw, scale_a, scale_b)
+    qa, qw = _u8(qa).contiguous(), _u8(qw).contiguous()
+    M, K = qa.shape
+    Nn, K2 = qw.shape
+    if K != K2:
+        raise ValueError(f"K mismatch: A has {K}, W has {K2}")
+    scale_a = scale_a.contiguous().float()
+    scale_b = scale_b.contiguous().float()
+    if block:
+        nkg = -(-K // 128)
+        if tuple(scale_a.shape) != (M, nkg) or tuple(scale_b.shape) != (-(-Nn // 128), nkg):
+            raise ValueError("block scales must be [M, ceil(K/128)] and [ceil(N/128), ceil(K/128)]")
+    c = out if out is not None else torch.empty((M, Nn), dtype=out_dtype, device=dev)
+    ws = _gemm_ws(N.OP_FP8, M, Nn, K, dev)
+    with torch.cuda.device(dev):
+        N.call("dsl_fp8_gemm", N.ptr(qa), N.ptr(qw), N.ptr(c), M, Nn, K, c.stride(0),
+               _out_code(c.dtype), N.SCALE_BLOCK128 if block else N.SCALE_TENSOR,
+               N.ptr(scale_a), N.ptr(scale_b), N.ptr(ws), 0 if ws is None else ws.numel() * 4,
+               N.stream_of(dev))
+    return c
+
+
+def fp4_gemm_packed(qa, sa, qw, sw, *, fmt: str = "mxfp4", global_a=None, global_w=None,
+                    out_dtype=torch.bfloat16, out=None):
+    """GEMM on packed E2M1 codes: qa [M, K/2], qw [N, K/2] uint8 (low nibble =
+    even K).  MXFP4: sa [M, K/32], sw [N, K/32] E8M0 bytes.  NVFP4: sa [M, K/16],
+    sw [N, K/16] E4M3 bytes plus 1-element float32 global scales."""
+    dev = _require_gpu(qa, qw, sa, sw)
+    qa, qw = _u8(qa).contiguous(), _u8(qw).contiguous()
+    sa, sw = _u8(sa).contiguous(), _u8(sw).contiguous()
+    M, Kh = qa.shape
+    Nn, Kh2 = qw.shape
+    if Kh != Kh2:
+        raise ValueError(f"K mismatch: A has {2 * Kh}, W has {2 * Kh2}")
+    K = 2 * Kh
+    if fmt == "mxfp4":
+        code, blk = N.FMT_MXFP4, 32
+    elif fmt == "nvfp4":
+        code, blk = N.FMT_NVFP4, 16
+        if global_a is None or global_w is None:
+            raise ValueError("nvfp4 needs global_a and global_w")
+    else:
+        raise ValueError(f"unknown fp4 format {fmt!r} (expected 'mxfp4' or 'nvfp4')")
+    if tuple(sa.shape) != (M, K // blk) or tuple(sw.shape) != (Nn, K // blk):
+        raise ValueError(f"{fmt} scales must be [M, K/{blk}] and [N, K/{blk}]")
+    ga = _dev_scalar(global_a, dev) if global_a is not None else None
+    gw = _dev_scalar(global_w, dev) if global_w is not None else None
+    c = out if out is not None else torch.empty((M, Nn), dtype=out_dtype, device=dev)
+    ws = _gemm_ws(N.OP_FP4, M, Nn, K, dev)
+    with torch.cuda.device(dev):
+        N.call("dsl_fp4_gemm", N.ptr(qa), N.ptr(qw), N.ptr(c), M, Nn, K, c.stride(0),
+               _out_code(c.dtype), code, N.ptr(sa), N.ptr(sw), N.ptr(ga), N.ptr(gw), N.ptr(ws),
+               0 if ws is None else ws.numel() * 4, N.stream_of(dev))
+    return c
+
+
+def grouped_fp8_gemm_packed(qx, sx, qw, sw, offsets, *, out_dtype=torch.bfloat16, out=None):
+    """Variable-size grouped GEMM on E4M3 codes.
+
+    qx [T, K] rows sorted by group, qw [G, N, K], offsets int32 [G+1] on the
+    device (offsets[0] = 0, offsets[G] = T, non-decreasing), sx [T] per-row
+    scales, sw [G, N] per-channel scales.  Returns y [T, N].
+    """
+    dev = _require_gpu(qx, qw, sx, sw, offsets)
+    qx, qw = _u8(qx).contiguous(), _u8(qw).contiguous()
+    T, K = qx.shape
+    G, Nn, K2 = qw.shape
+    if K != K2:
+        raise ValueError(f"K mismatch: X has {K}, W has {K2}")
+    if offsets.dim() != 1 or offsets.numel() != G + 1:
+        raise ValueError(f"offsets must be 1-D with {G + 1} entries")
+    offsets = offsets.to(torch.int32).contiguous()
+    sx = sx.reshape(-1).float().contiguous()
+    sw = sw.reshape(G, Nn).float().contiguous()
+    if sx.numel() != T:
+        raise ValueError("scale_x must have one entry per row")
+    y = out if out is not None else torch.empty((T, Nn), dtype=out_dtype, device=dev)
+    with torch.cuda.device(dev):
+        N.call("dsl_grouped_fp8_gemm", N.ptr(qx), N.ptr(qw), N.ptr(y), N.ptr(offsets), G, T, Nn,
+               K, y.stride(0), _out_code(y.dtype), N.ptr(sx), N.ptr(sw), N.stream_of(dev))
+    return y
+
+
+# ------------------------------------------------------ registered callables --
+
+def fp8_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=1.0, scale_b=1.0, *,
+             granularity: str = "tensor", out_dtype: torch.dtype = torch.bfloat16):
+    """FP8 E4M3 GEMM ``C = (A @ B) * scale_a * scale_b`` (bf16 by default).
+
+    * A [M, K], B [K, N] in bf16/fp16/fp32: both are quantized on the GPU
+      (granularity "tensor": amax/448 per tensor; "block": 1x128 activation
+      groups and 128x128 weight blocks); scale_a / scale_b stay extra
+      multipliers, as in the reference.
+    * A, B in float8_e4m3fn: scale_a / scale_b are the dequantization scales,
+      either numbers (per-tensor) or tensors [M, ceil(K/128)] and
+      [ceil(N/128), ceil(K/128)] (block-scaled).
+    ``out_dtype=torch.float32`` reproduces the reference's fp32 output.
+    """
+    if A.dim() != 2 or B.dim() != 2:
+        raise ValueError("fp8_gemm expects A [M, K] and B [K, N]")
+    M, K = A.shape
+    K2, Nn = B.shape
+    if K != K2:
+        raise ValueError(f"K mismatch: A is [{M}, {K}], B is [{K2}, {Nn}]")
+    dev = _require_gpu(A, B)
+    if A.dtype in _HIGH and B.dtype in _HIGH:
+        if granularity == "tensor":
+            qa, sa = Q.quant_fp8_tensor(A)
+            qw, sw = Q.quant_fp8_tensor(B.t())
+            block = False
+        elif granularity == "block":
+            qa, sa = Q.quant_fp8_blocks(A, 1, 128)
+            qw, sw = Q.quant_fp8_blocks(B.t(), 128, 128)
+            block = True
+        else:
+            raise ValueError(f"granularity must be 'tensor' or 'block', got {granularity!r}")
+        if not (isinstance(scale_a, numbers.Number) and isinstance(scale_b, numbers.Number)):
+            raise ValueError("with high-precision inputs scale_a/scale_b must be numbers")
+        if scale_a != 1.0:
+            sa = sa * float(scale_a)
+        if scale_b != 1.0:
+            sw = sw * float(scale_b)
+        return fp8_gemm_packed(qa, qw, sa, sw, block=block, out_dtype=out_dtype)
+    if A.dtype == _FP8 and B.dtype == _FP8:
+        qw = _k_major(B)
+        if isinstance(scale_a, torch.Tensor) and scale_a.dim() == 2:
+            if not (isinstance(scale_b, torch.Tensor) and scale_b.dim() == 2):
+                raise ValueError("block-scaled fp8 needs 2-D scale_a and scale_b")
+            return fp8_gemm_packed(A, qw, scale_a.to(dev), scale_b.to(dev), block=True,
+                                   out_dtype=out_dtype)
+        return fp8_gemm_packed(A, qw, _dev_scalar(scale_a, dev), _dev_scalar(scale_b, dev),
+                               block=False, out_dtype=out_dtype)
+    raise TypeError(f"fp8_gemm: unsupported dtypes {A.dtype}, {B.dtype}")
+
+
+def fp4_gemm(A: torch.Tensor, B: torch.Tensor, *, fmt: str = "mxfp4", scale_a=None,
+             scale_b=None, global_a=None, global_b=None,
+             out_dtype: torch.dtype = torch.bfloat16):
+    """FP4 (E2M1) GEMM ``C = A @ B`` with MXFP4 or NVFP4 block scales.
+
+    * A [M, K], B [K, N] in bf16/fp16/fp32: quantized on the GPU with ``fmt``.
+    * Pre-packed: A uint8 [M, K/2] and B uint8 [K/2, N] (the ``.t()`` view of
+      packed weights W [N, K/2]) with scale_a / scale_b bytes ([M, K/32] /
+      [N, K/32] E8M0 for MXFP4, [M, K/16] / [N, K/16] E4M3 for NVFP4) and,
+      for NVFP4, global_a / global_b.
+    """
+    if A.dim() != 2 or B.dim() != 2:
+        raise ValueError("fp4_gemm expects 2-D A and B")
+    _require_gpu(A, B)
+    if fmt not in ("mxfp4", "nvfp4"):
+        raise ValueError(f"unknown fp4 format {fmt!r} (expected 'mxfp4' or 'nvfp4')")
+    if A.dtype in _HIGH and B.dtype in _HIGH:
+        M, K = A.shape
+        K2, Nn = B.shape
+        if K != K2:
+            raise ValueError(f"K mismatch: A is [{M}, {K}], B is [{K2}, {Nn}]")
+        if fmt == "mxfp4":
+            qa, sa = Q.quant_mxfp4(A)
+            qw, sw = Q.quant_mxfp4(B.t())
+            return fp4_gemm_packed(qa, sa, qw, sw, fmt="mxfp4", out_dtype=out_dtype)
+        qa, sa, ga = Q.quant_nvfp4(A)
+        qw, sw, gw = Q.quant_nvfp4(B.t())
+        return fp4_gemm_packed(qa, sa, qw, sw, fmt="nvfp4", global_a=ga, global_w=gw,
+                               out_dtype=out_dtype)
+    if A.dtype == torch.uint8 and B.dtype == torch.uint8:
+        if scale_a is None or scale_b is None:
+            raise ValueError("pre-packed fp4 inputs need scale_a and scale_b")
+        return fp4_gemm_packed(A, scale_a, _k_major(B), scale_b, fmt=fmt, global_a=global_a,
+                               global_w=global_b, out_dtype=out_dtype)
+    raise TypeError(f"fp4_gemm: unsupported dtypes {A.dtype}, {B.dtype}")
+
+
+def grouped_gemm(A: torch.Tensor, B: torch.Tensor, num_groups, *, scale_a=None, scale_b=None,
+                 out_dtype: torch.dtype | None = None):
+    """Grouped FP8 GEMM (MoE experts / LoRA adapters), one W per group.
+
+    * ``num_groups`` an int: fixed-size groups, A [G, M, K], B [G, K, N]
+      -> C [G, M, N] (the reference's batched form).
+    * ``num_groups`` a 1-D integer tensor of G+1 offsets: variable-size
+      groups, A [T, K] with rows sorted by group, B [G, K, N] -> C [T, N];
+      empty groups are allowed.
+    High-precision inputs are quantized to E4M3 with per-row activation and
+    per-channel weight scales.  float8_e4m3fn inputs need scale_a [T] and
+    scale_b [G, N].  The output dtype defaults to A.dtype (bf16 for fp8
+    and fp16 inputs).
+    """
+    if isinstance(num_groups, torch.Tensor):
+        offsets = num_groups
+        if A.dim() != 2 or B.dim() != 3:
+            raise ValueError("variable-size grouped_gemm expects A [T, K] and B [G, K, N]")
+        G = B.shape[0]
+        if offsets.dim() != 1 or offsets.numel() != G + 1:
+            raise ValueError(f"offsets must have num_groups+1 = {G + 1} entries")
+        X = A
+        fixed = None
+    elif isinstance(num_groups, numbers.Integral):
+        G = int(num_groups)
+        if A.dim() != 3 or B.dim() != 3 or A.shape[0] != G or B.shape[0] != G:
+            raise ValueError("fixed-size grouped_gemm expects A [G, M, K], B [G, K, N]")
+        Mg = A.shape[1]
+        X = A.reshape(G * Mg, A.shape[2])
+        offsets = torch.arange(0, G * Mg + 1, Mg, dtype=torch.int32, device=A.device)
+        fixed = Mg
+    else:
+        raise TypeError("num_groups must be an int or a 1-D tensor of group offsets")
+    dev = _require_gpu(A, B, offsets)
+    T, K = X.shape
+    _, K2, Nn = B.shape
+    if K != K2:
+        raise ValueError(f"K mismatch: A has {K}, B has {K2}")
+    if out_dtype is None:
+        out_dtype = torch.float32 if A.dtype == torch.float32 else torch.bfloat16
+    Wt = B.transpose(1, 2).reshape(G * Nn, K)          # W[g, n, k] rows
+    if X.dtype in _HIGH and B.dtype in _HIGH:
+        qx, sx = Q.quant_fp8_blocks(X, 1, K)
+        qw, sw = Q.quant_fp8_blocks(Wt, 1, K)
+    elif X.dtype == _FP8 and B.dtype == _FP8:
+        if scale_a is None or scale_b is None:
+            raise ValueError("fp8 grouped_gemm needs scale_a [T] and scale_b [G, N]")
+        qx, sx = X, scale_a.to(dev)
+        qw, sw = Wt, scale_b.to(dev)
+    else:
+        raise TypeError(f"grouped_gemm: unsupported dtypes {A.dtype}, {B.dtype}")
+    y = grouped_fp8_gemm_packed(qx, sx, qw.reshape(G, Nn, K), sw.reshape(G, Nn), offsets,
+                                out_dtype=out_dtype)
+    if A.dtype == torch.float16:
+        y = y.to(torch.float16)
+    return y.reshape(G, fixed, Nn) if fixed is not None else y

@@ -1,0 +1,154 @@
+/*
+ * dsl_gemm.h -- C ABI of the gfx950 (MI355X) quantized-GEMM library
+ * (libdsl_gemm.so).  Plain pointers and sizes only; no torch or C++ types.
+ *
+ * Conventions for every entry point:
+ *   - all data pointers are device pointers on the current HIP device;
+ *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream);
+ *     work is enqueued asynchronously, nothing synchronises;
+ *   - strides are in elements; packed operand rows are K-major bytes
+ *     (FP8: K bytes per row, FP4: K/2 bytes per row);
+ *   - the return value is DSL_OK (0) or a negative status; the message is
+ *     available from dsl_last_error() (thread-local).  Validation happens
+ *     before any launch, so an error return means nothing was enqueued.
+ *     Nothing in the library calls exit() (the reference's CHECK_CUDA does,
+ *     cuda/gemm/fp8_gemm.cu:17-25);
+ *   - the library never allocates device memory: outputs and workspaces
+ *     are passed in (sizes from the *_workspace_bytes queries).
+ *
+ * Reference interfaces replaced (the reference has no C ABI for this path;
+ * these are the functions the Python callables registered as
+ * gemm.fp8_gemm / gemm.grouped_gemm reach, dispatcher/registry.py:133-141):
+ */
+#ifndef DSL_GEMM_H
+#define DSL_GEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+  DSL_OK = 0,
+  DSL_ERR_ARG = -1,          /* bad shape / stride / alignment / null pointer */
+  DSL_ERR_UNSUPPORTED = -2,  /* valid request this build does not implement   */
+  DSL_ERR_WORKSPACE = -3,    /* workspace missing or too small                */
+  DSL_ERR_HIP = -4           /* HIP runtime error while launching             */
+};
+
+enum { DSL_OUT_BF16 = 0, DSL_OUT_F32 = 1 };
+enum { DSL_SCALE_TENSOR = 0, DSL_SCALE_BLOCK128 = 1 };
+enum { DSL_FMT_MXFP4 = 0, DSL_FMT_NVFP4 = 1 };
+enum { DSL_OP_FP8 = 0, DSL_OP_FP4 = 1, DSL_OP_GROUPED_FP8 = 2 };
+
+/* Last error message of the calling thread ("" when none). */
+const char *dsl_last_error(void);
+
+/* ABI version of this header (bumped on any signature change). */
+int dsl_abi_version(void);
+
+/* ------------------------------------------------------------ quantize --
+ * Input x is a bf16 matrix read as x[r*stride_row + c*stride_col], rows R,
+ * cols C, with C the GEMM reduction axis (A[M,K] directly; the reference's
+ * B[K,N] as its [N,K] view).  Outputs are K-major: q[r*C + c].
+ */
+
+/* Per-tensor E4M3.  scale = max(amax/448, 1e-12); q = e4m3(x / scale).
+ * Replaces quantize_to_fp8_kernel (cuda/gemm/fp8_gemm.cu:118-144).
+ * Writes one float to *scale.  Needs dsl_quant_workspace_bytes(R, C). */
+int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols,
+                         int64_t stride_row, int64_t stride_col,
+                         uint8_t *q, float *scale,
+                         void *workspace, size_t workspace_bytes, void *stream);
+
+/* Block-scaled E4M3 over group_rows x group_cols tiles (1x128 activations,
+ * 128x128 weights, 1xC per-row / per-channel).  scales is
+ * [ceil(R/group_rows)][ceil(C/group_cols)] fp32, each max(amax/448, 1e-12).
+ * Replaces the scale layout read by fp8_gemm_groupwise_kernel
+ * (cuda/gemm/fp8_gemm.cu:67-99), which ships no quantizer of its own. */
+int dsl_quant_fp8_blocks(const void *x, int64_t rows, int64_t cols,
+                         int64_t stride_row, int64_t stride_col,
+                         int64_t group_rows, int64_t group_cols,
+                         uint8_t *q, float *scales, void *stream);
+
+/* MXFP4: per row and 32 K elements, E8M0 = clamp(floor(log2 amax)-2,
+ * -127,127)+127, codes = e2m1_rne_sat(x * 2^-e).  q_packed [R][C/2] (low
+ * nibble = even K), e8m0 [R][C/32].  C % 32 == 0.
+ * Replaces quantize_fp32_to_nvfp4 (cuda/gemm/fp4_gemm.cu:49-90), whose
+ * flat fp32 amax/6 scales are not MXFP4. */
+int dsl_quant_mxfp4(const void *x, int64_t rows, int64_t cols,
+                    int64_t stride_row, int64_t stride_col,
+                    uint8_t *q_packed, uint8_t *e8m0, void *stream);
+
+/* NVFP4: s_g = max(amax_T/2688, 1e-12); per row and 16 K elements
+ * s_b = e4m3((amax_16/6)/s_g); codes = e2m1_rne_sat(x / (f32(s_b)*s_g)),
+ * all-zero codes where that denominator is 0.  q_packed [R][C/2],
+ * e4m3_scales [R][C/16], *global_scale = s_g.  C % 16 == 0.
+ * Same reference function replaced as dsl_quant_mxfp4. */
+int dsl_quant_nvfp4(const void *x, int64_t rows, int64_t cols,
+                    int64_t stride_row, int64_t stride_col,
+                    uint8_t *q_packed, uint8_t *e4m3_scales, float *global_scale,
+                    void *workspace, size_t workspace_bytes, void *stream);
+
+/* Workspace bytes for the two-pass (global amax) quantizers. */
+size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols);
+
+/* --------------------------------------------------------------- GEMMs --
+ * C[m, n] = sum_k A[m, k] * W[n, k] (the reference's A @ B with B = W^T),
+ * A [M][K] and W [N][K] packed K-major, C [M][ldc] in bf16 or fp32.
+ */
+
+/* FP8 E4M3 GEMM.
+ *   DSL_SCALE_TENSOR:   scale_a, scale_b -> one float each (device);
+ *                       C = (acc * sa) * sb  (triton/gemm/gemm_kernels.py:97).
+ *   DSL_SCALE_BLOCK128: scale_a [M][ceil(K/128)] (1x128 groups),
+ *                       scale_b [ceil(N/128)][ceil(K/128)] (128x128 blocks);
+ *                       C = sum_g (sum_{k in g} a*w) * sa[m,g] * sb[n/128,g]
+ *                       (cuda/gemm/fp8_gemm.cu:84-97).
+ * K % 16 == 0.  Replaces fp8_gemm (triton/gemm/gemm_kernels.py:104-122),
+ * fp8_gemm_per_tensor (cuda/gemm/fp8_gemm.cu:102-108) and
+ * fp8_gemm_groupwise (cuda/gemm/fp8_gemm.cu:110-116). */
+int dsl_fp8_gemm(const uint8_t *a, const uint8_t *b, void *c,
+                 int64_t m, int64_t n, int64_t k, int64_t ldc, int out_dtype,
+                 int scale_mode, const float *scale_a, const float *scale_b,
+                 void *workspace, size_t workspace_bytes, void *stream);
+
+/* FP4 (E2M1) GEMM.
+ *   DSL_FMT_MXFP4: scale_a [M][K/32], scale_b [N][K/32] E8M0 bytes, fed to
+ *                  the scaled MFMA; global_a/global_b unused (may be NULL).
+ *   DSL_FMT_NVFP4: scale_a [M][K/16], scale_b [N][K/16] E4M3 bytes,
+ *                  global_a/global_b -> one float each (device).
+ * K % 32 == 0.  Replaces fp4_gemm / fp4_gemm_kernel
+ * (cuda/gemm/fp4_gemm.cu:92-146). */
+int dsl_fp4_gemm(const uint8_t *a, const uint8_t *b, void *c,
+                 int64_t m, int64_t n, int64_t k, int64_t ldc, int out_dtype,
+                 int fmt, const uint8_t *scale_a, const uint8_t *scale_b,
+                 const float *global_a, const float *global_b,
+                 void *workspace, size_t workspace_bytes, void *stream);
+
+/* Grouped FP8 GEMM over variable-size groups (MoE experts / LoRA adapters).
+ * Rows group_offsets[g] .. group_offsets[g+1]-1 of x [total_rows][K]
+ * multiply w[g] (w is [num_groups][N][K]); y [total_rows][ldy].
+ * group_offsets is a device int32 array of num_groups+1 non-decreasing
+ * entries, offsets[0] = 0, offsets[num_groups] = total_rows; empty groups
+ * are skipped on the device.  Per-row scale_x [total_rows] and per-channel
+ * scale_w [num_groups][N]: y = acc * sx[r] * sw[g, n].
+ * Replaces grouped_gemm (triton/gemm/gemm_kernels.py:164-182, fixed size)
+ * and grouped_gemm_variable (cuda/gemm/grouped_gemm.cu:26-32, :150-156). */
+int dsl_grouped_fp8_gemm(const uint8_t *x, const uint8_t *w, void *y,
+                         const int32_t *group_offsets, int64_t num_groups,
+                         int64_t total_rows, int64_t n, int64_t k, int64_t ldy,
+                         int out_dtype, const float *scale_x, const float *scale_w,
+                         void *stream);
+
+/* Workspace bytes dsl_fp8_gemm / dsl_fp4_gemm need for this shape
+ * (op = DSL_OP_FP8 or DSL_OP_FP4; 0 when none is needed). */
+size_t dsl_gemm_workspace_bytes(int op, int64_t m, int64_t n, int64_t k);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DSL_GEMM_H */

@@ -1,0 +1,143 @@
+"""Reference GEMMs for the quantized path (CPU).
+
+TEST INFRASTRUCTURE ONLY -- see ``oracle/__init__.py``.
+
+Orientation: A is [M, K], the weight operand is W[N, K] (K-major); the
+reference's ``B[K, N]`` is ``W.t()`` (triton/gemm/gemm_kernels.py:104-108,
+:117-119 are stride-generic, so passing ``W.t()`` is the same call).
+
+The dense references dequantize both operands to fp32 and multiply with an
+fp32 (or fp64) matmul, then round to bf16 -- the "dequantize -> fp32
+matmul" oracle.  Mathematically this equals the reference's group-partial
+form ``sum_g s_a s_b sum_{k in g} a b`` (cuda/gemm/fp8_gemm.cu:84-97,
+fp4_gemm.cu:111-135); the two differ only by fp32 summation order, which the
+1e-2 tolerance absorbs.  ``tiled_fp8_gemm`` restates the reference's own CPU
+path (tilelang/gemm/gemm_kernels.py:96-113) tile for tile and is used as the
+reference-structured CPU baseline.
+"""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from .formats import e2m1_decode, e4m3_decode, e8m0_decode, unpack_nibbles, round_to_bf16
+from .quant import F32
+
+
+def _mm(a: np.ndarray, w: np.ndarray, f64: bool = False) -> np.ndarray:
+    """a[M,K] @ w[N,K].T on the CPU (torch, so the thread count is explicit)."""
+    dt = torch.float64 if f64 else torch.float32
+    ta = torch.from_numpy(np.ascontiguousarray(a)).to(dt)
+    tw = torch.from_numpy(np.ascontiguousarray(w)).to(dt)
+    return (ta @ tw.T).to(torch.float32).numpy()
+
+
+# ----------------------------- dequantizers -------------------------------
+
+def dequant_fp8_tensor(q, scale):
+    return (e4m3_decode(q) * F32(scale)).astype(F32)
+
+
+def dequant_fp8_blocks(q, scales, group_rows, group_cols):
+    R, C = q.shape
+    full = np.repeat(np.repeat(np.asarray(scales, F32), group_rows, axis=0),
+                     group_cols, axis=1)[:R, :C]
+    return (e4m3_decode(q) * full).astype(F32)
+
+
+def dequant_mxfp4(packed, e8m0):
+    v = e2m1_decode(unpack_nibbles(packed))
+    R, C = v.shape
+    s = np.repeat(e8m0_decode(e8m0), 32, axis=1)[:, :C]
+    return (v * s).astype(F32)
+
+
+def dequant_nvfp4(packed, sb_codes, s_g):
+    v = e2m1_decode(unpack_nibbles(packed))
+    R, C = v.shape
+    s = np.repeat(e4m3_decode(sb_codes), 16, axis=1)[:, :C]
+    return (v * s * F32(s_g)).astype(F32)
+
+
+# ------------------------------ references --------------------------------
+
+def ref_gemm_dequant(a_deq: np.ndarray, w_deq: np.ndarray, f64: bool = False) -> np.ndarray:
+    """fp32 (or fp64) matmul of dequantized operands -> float32 holding bf16."""
+    return round_to_bf16(_mm(a_deq, w_deq, f64))
+
+
+def ref_fp8_per_tensor(qa, sa, qw, sw, f64=False):
+    """C = (sum_k a*w) * sa * sb (triton/gemm/gemm_kernels.py:97 applies the
+    scales after accumulation); bf16 result."""
+    acc = _mm(e4m3_decode(qa), e4m3_decode(qw), f64)
+    return round_to_bf16((acc * F32(sa) * F32(sw)).astype(F32))
+
+
+def ref_fp8_groupwise(qa, sa, qw, sw, f64=False):
+    """Activations 1x128, weights 128x128 (sa [M, K/128], sw [N/128, K/128])."""
+    return ref_gemm_dequant(dequant_fp8_blocks(qa, sa, 1, 128),
+                            dequant_fp8_blocks(qw, sw, 128, 128), f64)
+
+
+def ref_mxfp4(pa, ea, pw, ew, f64=False):
+    return ref_gemm_dequant(dequant_mxfp4(pa, ea), dequant_mxfp4(pw, ew), f64)
+
+
+def ref_nvfp4(pa, sba, ga, pw, sbw, gw, f64=False):
+    return ref_gemm_dequant(dequant_nvfp4(pa, sba, ga), dequant_nvfp4(pw, sbw, gw), f64)
+
+
+def ref_grouped_fp8(qx, sx, qw, sw, offsets, f64=False):
+    """Grouped (MoE) FP8: rows offsets[e]:offsets[e+1] of X multiply W[e].
+
+    Per-row activation scale sx[r], per-channel weight scale sw[e, n]:
+    ``Y[r, n] = sx[r] * sw[e(r), n] * sum_k Q8 Q8``.  Follows the
+    variable-size descriptor semantics of cuda/gemm/grouped_gemm.cu:26-32,
+    :77-104 with the concatenated-rows layout; empty groups produce no rows.
+    """
+    qx = np.asarray(qx)
+    G = len(offsets) - 1
+    N = qw.shape[1]
+    out = np.zeros((qx.shape[0], N), dtype=F32)
+    xd = e4m3_decode(qx)
+    for e in range(G):
+        r0, r1 = int(offsets[e]), int(offsets[e + 1])
+        if r1 == r0:
+            continue
+        acc = _mm(xd[r0:r1], e4m3_decode(qw[e]), f64)
+        out[r0:r1] = acc * np.asarray(sx[r0:r1], F32)[:, None] * np.asarray(sw[e], F32)[None, :]
+    return round_to_bf16(out.astype(F32))
+
+
+def tiled_fp8_gemm(a_codes, w_codes, sa, sw, block_m=64, block_n=64, block_k=32):
+    """The reference's CPU path restated: 64x64x32 tiles, fp32 accumulation
+    over K tiles, scales applied to each finished tile
+    (tilelang/gemm/gemm_kernels.py:96-113).  Returns fp32 [M, N]."""
+    a = torch.from_numpy(e4m3_decode(a_codes))
+    w = torch.from_numpy(e4m3_decode(w_codes))
+    M, K = a.shape
+    N = w.shape[0]
+    c = torch.zeros(M, N, dtype=torch.float32)
+    for bm in range(0, M, block_m):
+        for bn in range(0, N, block_n):
+            acc = torch.zeros(min(block_m, M - bm), min(block_n, N - bn))
+            for bk in range(0, K, block_k):
+                acc += a[bm:bm + block_m, bk:bk + block_k] @ w[bn:bn + block_n, bk:bk + block_k].T
+            c[bm:bm + block_m, bn:bn + block_n] = acc * float(sa) * float(sw)
+    return c.numpy()
+
+
+# ------------------------------ tolerance ---------------------------------
+
+def rel_errors(c: np.ndarray, r: np.ndarray):
+    """(max|C-R| / max|R|, max elementwise rel err over |R| >= 0.1*rms(R))."""
+    c = np.asarray(c, np.float64)
+    r = np.asarray(r, np.float64)
+    denom = np.max(np.abs(r))
+    glob = float(np.max(np.abs(c - r)) / denom) if denom > 0 else float(np.max(np.abs(c)))
+    rms = np.sqrt(np.mean(r * r)) if r.size else 0.0
+    mask = np.abs(r) >= 0.1 * rms
+    if rms == 0 or not mask.any():
+        return glob, 0.0
+    elem = float(np.max(np.abs(c - r)[mask] / np.abs(r)[mask]))
+    return glob, elem

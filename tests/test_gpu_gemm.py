@@ -1,0 +1,182 @@
+"""GPU GEMMs vs the dequantize -> fp32 matmul oracle (tolerance 1e-2).
+
+Each test quantizes on the GPU, checks the codes against the oracle
+bit-for-bit, then compares the GEMM output with the oracle GEMM run on the
+same codes, so a GEMM error can never hide behind a quantization error.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm as OG
+from oracle import quant as OQ
+from dsl_tool_amd import gemm as G
+from dsl_tool_amd import quant as Q
+from dsl_tool_amd import workloads as W
+from tests.util import assert_close, np_f32, np_u8
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _f32(x):
+    return x.float().numpy()
+
+
+# ------------------------------------------------------------ FP8 tensor --
+@pytest.mark.parametrize("m,n,k", [(128, 512, 1024), (37, 200, 272), (16, 256, 4096),
+                                   (300, 640, 512), (1, 16, 16), (513, 257, 144)])
+def test_fp8_per_tensor(m, n, k):
+    a = W.randn_bf16((m, k), 101)
+    w = W.randn_bf16((n, k), 102, 0.02)
+    qa, sa = Q.quant_fp8_tensor(a.to(DEV))
+    qw, sw = Q.quant_fp8_tensor(w.to(DEV))
+    qa_ref, sa_ref = OQ.quant_fp8_per_tensor(_f32(a))
+    qw_ref, sw_ref = OQ.quant_fp8_per_tensor(_f32(w))
+    assert np.array_equal(np_u8(qa), qa_ref) and np.array_equal(np_u8(qw), qw_ref)
+    c = G.fp8_gemm_packed(qa, qw, sa, sw)
+    ref = OG.ref_fp8_per_tensor(qa_ref, sa_ref, qw_ref, sw_ref)
+    assert_close(c, ref, what=f"fp8 tensor {m}x{n}x{k}")
+
+
+def test_fp8_registered_callable_matches_reference_semantics():
+    # reference convention: A [M, K], B [K, N] = W.t(), C = (A @ B) * sa * sb
+    a = W.randn_bf16((64, 512), 103)
+    w = W.randn_bf16((384, 512), 104, 0.02)
+    c = G.fp8_gemm(a.to(DEV), w.to(DEV).t(), 2.0, 0.5)
+    qa, sa = OQ.quant_fp8_per_tensor(_f32(a))
+    qw, sw = OQ.quant_fp8_per_tensor(_f32(w))
+    ref = OG.ref_fp8_per_tensor(qa, sa * np.float32(2.0), qw, sw * np.float32(0.5))
+    assert_close(c, ref, what="fp8_gemm(bf16)")
+    c32 = G.fp8_gemm(a.to(DEV), w.to(DEV).t(), out_dtype=torch.float32)
+    assert c32.dtype == torch.float32
+    ref32 = OG._mm(OG.dequant_fp8_tensor(qa, sa), OG.dequant_fp8_tensor(qw, sw))
+    assert_close(c32, ref32, what="fp8_gemm fp32 out")
+
+
+def test_fp8_prequantized_inputs():
+    a = W.randn_bf16((96, 256), 105)
+    w = W.randn_bf16((128, 256), 106, 0.02)
+    qa, sa = OQ.quant_fp8_per_tensor(_f32(a))
+    qw, sw = OQ.quant_fp8_per_tensor(_f32(w))
+    A8 = torch.from_numpy(qa).view(torch.float8_e4m3fn).to(DEV)
+    B8 = torch.from_numpy(qw).view(torch.float8_e4m3fn).to(DEV).t()   # [K, N] view
+    c = G.fp8_gemm(A8, B8, float(sa), float(sw))
+    assert_close(c, OG.ref_fp8_per_tensor(qa, sa, qw, sw), what="fp8 prequantized")
+
+
+# ------------------------------------------------------------- FP8 block --
+@pytest.mark.parametrize("m,n,k", [(16, 7168 // 8, 4096), (300, 384, 512), (4096 // 16, 256, 1024),
+                                   (5, 200, 272)])
+def test_fp8_block_scaled(m, n, k):
+    a = W.activations(2, m, k, outliers=True)
+    w = W.randn_bf16((n, k), 202, 0.02)
+    qa, sa = Q.quant_fp8_blocks(a.to(DEV), 1, 128)
+    qw, sw = Q.quant_fp8_blocks(w.to(DEV), 128, 128)
+    qa_ref, sa_ref = OQ.quant_fp8_blockwise(_f32(a), 1, 128)
+    qw_ref, sw_ref = OQ.quant_fp8_blockwise(_f32(w), 128, 128)
+    assert np.array_equal(np_u8(qa), qa_ref) and np.array_equal(np_f32(sa), sa_ref)
+    assert np.array_equal(np_u8(qw), qw_ref) and np.array_equal(np_f32(sw), sw_ref)
+    c = G.fp8_gemm_packed(qa, qw, sa, sw, block=True)
+    assert_close(c, OG.ref_fp8_groupwise(qa_ref, sa_ref, qw_ref, sw_ref), what=f"fp8 block {m}x{n}x{k}")
+
+
+def test_fp8_block_via_registered_callable():
+    a = W.activations(2, 64, 512, outliers=True)
+    w = W.randn_bf16((256, 512), 203, 0.02)
+    c = G.fp8_gemm(a.to(DEV), w.to(DEV).t(), granularity="block")
+    qa, sa = OQ.quant_fp8_blockwise(_f32(a), 1, 128)
+    qw, sw = OQ.quant_fp8_blockwise(_f32(w), 128, 128)
+    assert_close(c, OG.ref_fp8_groupwise(qa, sa, qw, sw), what="fp8_gemm block")
+
+
+# ----------------------------------------------------------------- MXFP4 --
+@pytest.mark.parametrize("m,n,k", [(16, 512, 8192), (256, 512, 1024), (300, 384, 512),
+                                   (7, 48, 96), (1, 16, 32)])
+def test_mxfp4(m, n, k):
+    a = W.randn_bf16((m, k), 301)
+    w = W.randn_bf16((n, k), 302, 0.02)
+    qa, ea = Q.quant_mxfp4(a.to(DEV))
+    qw, ew = Q.quant_mxfp4(w.to(DEV))
+    qa_ref, ea_ref = OQ.quant_mxfp4(_f32(a))
+    qw_ref, ew_ref = OQ.quant_mxfp4(_f32(w))
+    assert np.array_equal(np_u8(qa), qa_ref) and np.array_equal(np_u8(ea), ea_ref)
+    assert np.array_equal(np_u8(qw), qw_ref) and np.array_equal(np_u8(ew), ew_ref)
+    c = G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4")
+    assert_close(c, OG.ref_mxfp4(qa_ref, ea_ref, qw_ref, ew_ref), what=f"mxfp4 {m}x{n}x{k}")
+
+
+def test_mxfp4_registered_callable():
+    a = W.randn_bf16((48, 256), 303)
+    w = W.randn_bf16((96, 256), 304, 0.02)
+    c = G.fp4_gemm(a.to(DEV), w.to(DEV).t(), fmt="mxfp4")
+    qa, ea = OQ.quant_mxfp4(_f32(a))
+    qw, ew = OQ.quant_mxfp4(_f32(w))
+    assert_close(c, OG.ref_mxfp4(qa, ea, qw, ew), what="fp4_gemm mxfp4")
+
+
+# ----------------------------------------------------------------- NVFP4 --
+@pytest.mark.parametrize("m,n,k", [(1, 1024, 4096), (256, 512, 1024), (37, 200, 96),
+                                   (16, 48, 32)])
+def test_nvfp4(m, n, k):
+    a = W.randn_bf16((m, k), 401)
+    w = W.randn_bf16((n, k), 402, 0.02)
+    qa, sa, ga = Q.quant_nvfp4(a.to(DEV))
+    qw, sw, gw = Q.quant_nvfp4(w.to(DEV))
+    qa_ref, sa_ref, ga_ref = OQ.quant_nvfp4(_f32(a))
+    qw_ref, sw_ref, gw_ref = OQ.quant_nvfp4(_f32(w))
+    assert np.array_equal(np_u8(qa), qa_ref) and np.array_equal(np_u8(sa), sa_ref)
+    assert np.array_equal(np_u8(qw), qw_ref) and np.array_equal(np_u8(sw), sw_ref)
+    c = G.fp4_gemm_packed(qa, sa, qw, sw, fmt="nvfp4", global_a=ga, global_w=gw)
+    ref = OG.ref_nvfp4(qa_ref, sa_ref, ga_ref, qw_ref, sw_ref, gw_ref)
+    assert_close(c, ref, what=f"nvfp4 {m}x{n}x{k}")
+
+
+# --------------------------------------------------------------- grouped --
+def _grouped_case(counts, n, k, seed):
+    G_ = len(counts)
+    offsets = np.zeros(G_ + 1, np.int32)
+    offsets[1:] = np.cumsum(counts)
+    T = int(offsets[-1])
+    x = W.randn_bf16((max(T, 1), k), seed)[:T]
+    w = W.randn_bf16((G_, n, k), seed + 1, 0.02)
+    return x, w, offsets
+
+
+@pytest.mark.parametrize("counts,n,k", [([5, 0, 130, 64, 0, 1, 300, 17], 384, 256),
+                                        ([0, 0, 40, 0], 160, 512),
+                                        ([1000, 3, 0, 257], 256, 128)])
+def test_grouped_variable(counts, n, k):
+    x, w, offsets = _grouped_case(counts, n, k, 501)
+    G_ = len(counts)
+    qx, sx = Q.quant_fp8_blocks(x.to(DEV), 1, k)
+    qw, sw = Q.quant_fp8_blocks(w.reshape(G_ * n, k).to(DEV), 1, k)
+    qx_ref, sx_ref = OQ.quant_fp8_blockwise(_f32(x), 1, k)
+    qw_ref, sw_ref = OQ.quant_fp8_blockwise(_f32(w.reshape(G_ * n, k)), 1, k)
+    assert np.array_equal(np_u8(qx), qx_ref) and np.array_equal(np_u8(qw), qw_ref)
+    off_d = torch.from_numpy(offsets).to(DEV)
+    y = G.grouped_fp8_gemm_packed(qx, sx, qw.reshape(G_, n, k), sw.reshape(G_, n), off_d)
+    ref = OG.ref_grouped_fp8(qx_ref, sx_ref[:, 0], qw_ref.reshape(G_, n, k),
+                             sw_ref.reshape(G_, n), offsets)
+    assert_close(y, ref, what=f"grouped {counts}")
+
+
+def test_grouped_registered_variable_and_fixed():
+    counts = [7, 0, 60, 33]
+    x, w, offsets = _grouped_case(counts, 128, 256, 601)
+    b = w.transpose(1, 2)                     # reference orientation B [G, K, N]
+    y = G.grouped_gemm(x.to(DEV), b.to(DEV), torch.from_numpy(offsets).to(DEV))
+    qx, sx = OQ.quant_fp8_blockwise(_f32(x), 1, 256)
+    qw, sw = OQ.quant_fp8_blockwise(_f32(w.reshape(-1, 256)), 1, 256)
+    ref = OG.ref_grouped_fp8(qx, sx[:, 0], qw.reshape(4, 128, 256), sw.reshape(4, 128), offsets)
+    assert_close(y, ref, what="grouped_gemm variable")
+    # fixed-size form of the reference: A [G, M, K], B [G, K, N], num_groups int
+    a3 = W.randn_bf16((3, 64, 128), 602)
+    b3 = W.randn_bf16((3, 128, 96), 603, 0.02)
+    y3 = G.grouped_gemm(a3.to(DEV), b3.to(DEV), 3)
+    assert y3.shape == (3, 64, 96) and y3.dtype == torch.bfloat16
+    qx3, sx3 = OQ.quant_fp8_blockwise(_f32(a3.reshape(-1, 128)), 1, 128)
+    qw3, sw3 = OQ.quant_fp8_blockwise(_f32(b3.transpose(1, 2).reshape(-1, 128)), 1, 128)
+    off3 = np.array([0, 64, 128, 192], np.int32)
+    ref3 = OG.ref_grouped_fp8(qx3, sx3[:, 0], qw3.reshape(3, 96, 128), sw3.reshape(3, 96), off3)
+    assert_close(y3.reshape(-1, 96), ref3, what="grouped_gemm fixed")

@@ -1,0 +1,165 @@
+"""GPU quantize/pack kernels vs the CPU oracle: bit-exact codes and scales."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import formats as F
+from oracle import quant as OQ
+from dsl_tool_amd import quant as Q
+from dsl_tool_amd import workloads as W
+from tests.util import np_u8, np_f32
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _f32(x: torch.Tensor) -> np.ndarray:
+    return x.float().numpy()
+
+
+def _all_bf16_upto(limit: float) -> np.ndarray:
+    """Every finite bf16 value with |v| <= limit (both signs, zeros, subnormals)."""
+    v = F.bf16_bits_to_f32(np.arange(65536, dtype=np.uint16))
+    return v[np.isfinite(v) & (np.abs(v) <= limit)]
+
+
+def _rows_with_pin(values: np.ndarray, group: int, pin: float) -> np.ndarray:
+    """Lay values out in rows of `group` elements whose first element is `pin`
+    (which fixes the group's scale); pads with zeros."""
+    per = group - 1
+    n = -(-len(values) // per)
+    body = np.zeros(n * per, np.float32)
+    body[:len(values)] = values
+    rows = np.concatenate([np.full((n, 1), pin, np.float32), body.reshape(n, per)], axis=1)
+    return rows
+
+
+def _to_gpu_bf16(a: np.ndarray) -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a, np.float32)).bfloat16().to(DEV)
+
+
+@pytest.mark.parametrize("shape", [(128, 4096), (37, 272), (1, 16)])
+def test_fp8_tensor_matches_oracle(shape):
+    x = W.randn_bf16(shape, 11)
+    q, s = Q.quant_fp8_tensor(x.to(DEV))
+    q_ref, s_ref = OQ.quant_fp8_per_tensor(_f32(x))
+    assert np_f32(s)[0] == s_ref
+    assert np.array_equal(np_u8(q), q_ref)
+
+
+def test_fp8_tensor_strided_input_matches():
+    # the reference's B[K, N] passed as a contiguous [K, N] tensor: its [N, K]
+    # view has stride (1, N) and takes the strided path
+    b_kn = W.randn_bf16((256, 96), 12, 0.02)
+    q, s = Q.quant_fp8_tensor(b_kn.to(DEV).t())
+    q_ref, s_ref = OQ.quant_fp8_per_tensor(_f32(b_kn.t()))
+    assert np_f32(s)[0] == s_ref
+    assert np.array_equal(np_u8(q), q_ref)
+
+
+def test_fp8_tensor_zero_input_uses_scale_floor():
+    x = torch.zeros((8, 64), dtype=torch.bfloat16, device=DEV)
+    q, s = Q.quant_fp8_tensor(x)
+    assert np_f32(s)[0] == np.float32(1e-12)
+    assert not np_u8(q).any()
+
+
+def test_e4m3_encoder_exhaustive_at_unit_scale():
+    # every bf16 value in [-448, 448], grouped 1x128 with a pinned 448 -> scale 1.0
+    rows = _rows_with_pin(_all_bf16_upto(448.0), 128, 448.0)
+    q, s = Q.quant_fp8_blocks(_to_gpu_bf16(rows), 1, 128)
+    assert (np_f32(s) == 1.0).all()
+    want = torch.from_numpy(rows).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(np_u8(q), want)
+
+
+@pytest.mark.parametrize("gr,gc", [(1, 128), (128, 128), (1, 4096), (1, 64), (16, 48)])
+def test_fp8_blocks_match_oracle(gr, gc):
+    x = W.activations(2, 300, 4096, outliers=True)
+    q, s = Q.quant_fp8_blocks(x.to(DEV), gr, gc)
+    q_ref, s_ref = OQ.quant_fp8_blockwise(_f32(x), gr, gc)
+    assert np.array_equal(np_f32(s), s_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+
+
+def test_fp8_blocks_strided_input_matches():
+    b_kn = W.randn_bf16((384, 200), 13, 0.02)
+    q, s = Q.quant_fp8_blocks(b_kn.to(DEV).t(), 128, 128)
+    q_ref, s_ref = OQ.quant_fp8_blockwise(_f32(b_kn.t()), 128, 128)
+    assert np.array_equal(np_f32(s), s_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+
+
+def test_e2m1_encoder_exhaustive_at_unit_scale():
+    # every bf16 value with |v| < 8 in 32-blocks pinned by 4.0 -> E8M0 127 (2^0)
+    vals = _all_bf16_upto(7.96875)
+    rows = _rows_with_pin(vals, 32, 4.0)
+    q, e = Q.quant_mxfp4(_to_gpu_bf16(rows))
+    assert (np_u8(e) == 127).all()
+    want = F.pack_nibbles(F.e2m1_encode(rows))
+    assert np.array_equal(np_u8(q), want)
+
+
+@pytest.mark.parametrize("shape,seed", [((64, 8192), 21), ((33, 96), 22), ((16, 32), 23)])
+def test_mxfp4_matches_oracle(shape, seed):
+    x = W.randn_bf16(shape, seed)
+    q, e = Q.quant_mxfp4(x.to(DEV))
+    q_ref, e_ref = OQ.quant_mxfp4(_f32(x))
+    assert np.array_equal(np_u8(e), e_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+
+
+def test_mxfp4_wide_dynamic_range_and_zero_blocks():
+    x = W.randn_bf16((32, 256), 24).float()
+    scale = torch.exp2(torch.arange(-60, 68, 4, dtype=torch.float32))[:, None]
+    x = x * scale
+    x[3] = 0.0
+    x[5, :32] = 1e-40      # fp32-subnormal magnitudes (bf16 subnormals)
+    x = x.bfloat16()
+    q, e = Q.quant_mxfp4(x.to(DEV))
+    q_ref, e_ref = OQ.quant_mxfp4(_f32(x))
+    assert np.array_equal(np_u8(e), e_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+
+
+def test_mxfp4_strided_input_matches():
+    b_kn = W.randn_bf16((256, 40), 25, 0.02)
+    q, e = Q.quant_mxfp4(b_kn.to(DEV).t())
+    q_ref, e_ref = OQ.quant_mxfp4(_f32(b_kn.t()))
+    assert np.array_equal(np_u8(e), e_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+
+
+@pytest.mark.parametrize("shape,seed", [((64, 4096), 31), ((3, 48), 32), ((1, 16), 33)])
+def test_nvfp4_matches_oracle(shape, seed):
+    x = W.randn_bf16(shape, seed)
+    q, sb, sg = Q.quant_nvfp4(x.to(DEV))
+    q_ref, sb_ref, sg_ref = OQ.quant_nvfp4(_f32(x))
+    assert np_f32(sg)[0] == sg_ref
+    assert np.array_equal(np_u8(sb), sb_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+
+
+def test_nvfp4_underflowing_blocks_and_zero_tensor():
+    x = W.randn_bf16((8, 64), 34).float()
+    x[0, 0] = 3.0e4          # large amax: tiny blocks' E4M3 scales underflow to 0
+    x[2, 16:32] *= 1e-6
+    x[4] = 0.0
+    x = x.bfloat16()
+    q, sb, sg = Q.quant_nvfp4(x.to(DEV))
+    q_ref, sb_ref, sg_ref = OQ.quant_nvfp4(_f32(x))
+    assert np_f32(sg)[0] == sg_ref
+    assert np.array_equal(np_u8(sb), sb_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+    z = torch.zeros((2, 32), dtype=torch.bfloat16, device=DEV)
+    qz, sbz, sgz = Q.quant_nvfp4(z)
+    assert np_f32(sgz)[0] == np.float32(1e-12) and not np_u8(qz).any() and not np_u8(sbz).any()
+
+
+def test_nvfp4_strided_input_matches():
+    b_kn = W.randn_bf16((128, 24), 35, 0.02)
+    q, sb, sg = Q.quant_nvfp4(b_kn.to(DEV).t())
+    q_ref, sb_ref, sg_ref = OQ.quant_nvfp4(_f32(b_kn.t()))
+    assert np_f32(sg)[0] == sg_ref
+    assert np.array_equal(np_u8(sb), sb_ref)
+    assert np.array_equal(np_u8(q), q_ref)
