@@ -1,0 +1,159 @@
+"""Kernel registry: ``(kernel_name, backend) -> callable``.
+
+Same plugin surface as the reference (dispatcher/registry.py:26-122,
+:329-336): ``KernelEntry``, ``KernelRegistry.register / get / list_kernels /
+list_backends_for / load_all`` and the ``get_registry()`` singleton, with
+names following ``<category>.<function>`` (registry.py:6-8) and keys
+lower-cased.
+
+This build registers one backend, ``hip``: the gfx950 quantized GEMMs of
+``dsl_tool_amd.gemm`` under the reference's names ``gemm.fp8_gemm`` and
+``gemm.grouped_gemm`` plus the new ``gemm.fp4_gemm``.  The callables are
+registered whether or not the HIP library is built; calling one without it
+raises ``DslLibraryError`` (no CPU fallback), which the dispatcher turns into
+the same ``RuntimeError`` the reference raises for a failing kernel.
+
+Unlike the reference (whose docstring promises thread safety without a lock),
+registration and lookup here hold a lock, and the singleton is created
+under it.
+"""
+from __future__ import annotations
+
+import importlib
+import importlib.util
+import logging
+import os
+import threading
+from dataclasses import dataclass, field
+from typing import Callable, Dict, Optional, Tuple
+
+logger = logging.getLogger(__name__)
+
+BACKENDS = ("hip",)
+
+
+@dataclass
+class KernelEntry:
+    """One registered (kernel, backend) pair (reference registry.py:26-34)."""
+    kernel_name: str
+    backend: str
+    fn: Callable
+    description: str = ""
+    input_schema: dict = field(default_factory=dict)
+    output_schema: dict = field(default_factory=dict)
+
+
+class KernelRegistry:
+    def __init__(self) -> None:
+        self._store: Dict[Tuple[str, str], KernelEntry] = {}
+        self._lock = threading.RLock()
+
+    # ------------------------------------------------------------ register --
+    def register(self, kernel_name: str, backend: str, fn: Callable, description: str = "",
+                 input_schema: Optional[dict] = None,
+                 output_schema: Optional[dict] = None) -> None:
+        name, be = kernel_name.lower(), backend.lower()
+        entry = KernelEntry(name, be, fn, description, dict(input_schema or {}),
+                            dict(output_schema or {}))
+        with self._lock:
+            self._store[(name, be)] = entry
+        logger.debug("registered %s [%s]", name, be)
+
+    def get(self, kernel_name: str, backend: str) -> Optional[KernelEntry]:
+        with self._lock:
+            return self._store.get((kernel_name.lower(), backend.lower()))
+
+    def list_kernels(self) -> list[dict]:
+        with self._lock:
+            entries = list(self._store.values())
+        rows = [{"kernel_name": e.kernel_name, "backend": e.backend,
+                 "description": e.description} for e in entries]
+        return sorted(rows, key=lambda r: (r["kernel_name"], r["backend"]))
+
+    def list_backends_for(self, kernel_name: str) -> list[str]:
+        kn = kernel_name.lower()
+        with self._lock:
+            return sorted(b for (k, b) in self._store if k == kn)
+
+    # -------------------------------------------------------------- loading --
+    def _try_load_attr_from_file(self, file_path: str, attr: str) -> Optional[Callable]:
+        """Load ``attr`` from a Python file given by absolute path (the
+        reference's discovery hook, registry.py:99-111), for callers that
+        register their own kernel files.  Failures are logged and give None."""
+        try:
+            mod_name = "_dsl_kernel_file_" + os.path.splitext(os.path.basename(file_path))[0]
+            spec = importlib.util.spec_from_file_location(mod_name, file_path)
+            if spec is None or spec.loader is None:
+                return None
+            mod = importlib.util.module_from_spec(spec)
+            spec.loader.exec_module(mod)
+            return getattr(mod, attr, None)
+        except Exception as exc:   # noqa: BLE001 -- a broken plugin file must not break startup
+            logger.warning("could not load %s:%s: %s", file_path, attr, exc)
+            return None
+
+    def load_all(self, root: Optional[str] = None) -> None:
+        """Register every backend this build ships (only ``hip``)."""
+        self._register_hip(root)
+
+    def _register_hip(self, root: Optional[str] = None) -> None:
+        del root  # the hip kernels are a package module, not files under a root
+        gemm = importlib.import_module("dsl_tool_amd.gemm")
+        for name, attr, desc in HIP_GEMM_ENTRIES:
+            self.register(name, "hip", getattr(gemm, attr), desc,
+                          input_schema=gemm_input_schema(name),
+                          output_schema=gemm_output_schema(name))
+
+
+HIP_GEMM_ENTRIES = (
+    ("gemm.fp8_gemm", "fp8_gemm",
+     "FP8 E4M3 GEMM (per-tensor or 1x128/128x128 block scales), gfx950 scaled MFMA"),
+    ("gemm.fp4_gemm", "fp4_gemm",
+     "FP4 E2M1 GEMM: MXFP4 (E8M0 / 32, scaled MFMA) or NVFP4 (E4M3 / 16 + fp32 global)"),
+    ("gemm.grouped_gemm", "grouped_gemm",
+     "Grouped FP8 GEMM for MoE / LoRA: fixed [G,M,K] or variable-size groups by offsets"),
+)
+
+
+def gemm_input_schema(kernel_name: str) -> dict:
+    """Documentation schema (the reference's _gemm_input_schema,
+    registry.py:274-283, extended with this build's keyword arguments)."""
+    s = {"A": "Tensor[M, K] bf16/fp16/fp32 (or pre-quantized, see kwargs)",
+         "B": "Tensor[K, N] (pass W.t() for a K-major weight W[N, K])"}
+    if kernel_name.endswith("fp8_gemm"):
+        s.update({"scale_a": "float | Tensor[M, ceil(K/128)] fp32",
+                  "scale_b": "float | Tensor[ceil(N/128), ceil(K/128)] fp32",
+                  "granularity": "str 'tensor' | 'block' (bf16 inputs)",
+                  "out_dtype": "torch.bfloat16 (default) | torch.float32"})
+    elif kernel_name.endswith("fp4_gemm"):
+        s.update({"fmt": "str 'mxfp4' (default) | 'nvfp4'",
+                  "scale_a": "uint8 Tensor (pre-packed inputs only)",
+                  "scale_b": "uint8 Tensor (pre-packed inputs only)",
+                  "global_a": "float (nvfp4, pre-packed)", "global_b": "float (nvfp4, pre-packed)"})
+    elif kernel_name.endswith("grouped_gemm"):
+        s = {"A": "Tensor[G, M, K] (fixed) | Tensor[T, K] rows sorted by group (variable)",
+             "B": "Tensor[G, K, N]",
+             "num_groups": "int G (fixed) | int32 Tensor[G+1] group offsets (variable)"}
+    return s
+
+
+def gemm_output_schema(kernel_name: str) -> dict:
+    if kernel_name.endswith("grouped_gemm"):
+        return {"C": "Tensor[G, M, N] | Tensor[T, N], bf16 (fp32 for fp32 inputs)"}
+    return {"C": "Tensor[M, N] bf16 (out_dtype=torch.float32 for the reference's fp32)"}
+
+
+_registry: Optional[KernelRegistry] = None
+_registry_lock = threading.Lock()
+
+
+def get_registry(auto_load: bool = True) -> KernelRegistry:
+    """The process-wide registry, created (and loaded) on first use."""
+    global _registry
+    with _registry_lock:
+        if _registry is None:
+            reg = KernelRegistry()
+            if auto_load:
+                reg.load_all()
+            _registry = reg
+    return _registry

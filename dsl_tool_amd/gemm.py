@@ -237,9 +237,9 @@ def fp4_gemm(A: torch.Tensor, B: torch.Tensor, *, fmt: str = "mxfp4", scale_a=No
     """
     if A.dim() != 2 or B.dim() != 2:
         raise ValueError("fp4_gemm expects 2-D A and B")
-    _require_gpu(A, B)
     if fmt not in ("mxfp4", "nvfp4"):
         raise ValueError(f"unknown fp4 format {fmt!r} (expected 'mxfp4' or 'nvfp4')")
+    _require_gpu(A, B)
     if A.dtype in _HIGH and B.dtype in _HIGH:
         M, K = A.shape
         K2, Nn = B.shape

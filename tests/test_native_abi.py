@@ -1,0 +1,123 @@
+"""CPU: the C-ABI library loads, exports every function include/dsl_gemm.h
+declares, and rejects bad arguments with a status code before it would
+launch anything (no GPU is touched by any call here)."""
+import ctypes
+import os
+
+import pytest
+
+from dsl_tool_amd import _native as N
+
+LIB = N.LIB_PATH
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.fail(f"{LIB} is not built; run `python -m dsl_tool_amd.build`")
+    return N.lib()
+
+
+def test_library_exports_every_header_function(lib):
+    declared = N.header_functions()
+    assert declared, "no dsl_* functions found in include/dsl_gemm.h"
+    raw = ctypes.CDLL(LIB)
+    for name in declared:
+        assert hasattr(raw, name), f"{name} declared in dsl_gemm.h but not exported"
+    assert set(declared) == set(N.SIGNATURES), "ctypes signature table out of sync with header"
+
+
+def test_abi_version(lib):
+    assert lib.dsl_abi_version() == N.ABI_VERSION
+
+
+def _err(lib):
+    return lib.dsl_last_error().decode()
+
+
+def test_fp8_gemm_argument_validation(lib):
+    # k not a multiple of 16
+    rc = lib.dsl_fp8_gemm(None, None, None, 16, 16, 15, 16, 0, 0, None, None, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "multiple of 16" in _err(lib)
+    # ldc < n
+    rc = lib.dsl_fp8_gemm(None, None, None, 16, 32, 16, 16, 0, 0, None, None, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "ldc" in _err(lib)
+    # missing scales
+    rc = lib.dsl_fp8_gemm(None, None, None, 16, 16, 16, 16, 0, 0, None, None, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "scale" in _err(lib)
+    # unknown scale mode (pointers are never dereferenced on the host)
+    fake = 1 << 20
+    rc = lib.dsl_fp8_gemm(fake, fake, fake, 16, 16, 16, 16, 0, 7, fake, fake, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "scale_mode" in _err(lib)
+    # misaligned operand
+    rc = lib.dsl_fp8_gemm(fake + 1, fake, fake, 16, 16, 16, 16, 0, 0, fake, fake, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "aligned" in _err(lib)
+    # empty problem is a no-op success
+    assert lib.dsl_fp8_gemm(None, None, None, 0, 16, 16, 16, 0, 0, fake, fake, None, 0, None) == 0
+
+
+def test_fp8_gemm_workspace_is_required_when_split_k_is_planned(lib):
+    need = lib.dsl_gemm_workspace_bytes(N.OP_FP8, 16, 8192, 8192)
+    assert need > 0
+    fake = 1 << 20
+    rc = lib.dsl_fp8_gemm(fake, fake, fake, 16, 8192, 8192, 8192, 0, 0, fake, fake, None,
+                          need - 4, None)
+    assert rc == N.DSL_ERR_WORKSPACE
+
+
+def test_fp4_gemm_argument_validation(lib):
+    fake = 1 << 20
+    rc = lib.dsl_fp4_gemm(fake, fake, fake, 4, 4, 48, 4, 0, N.FMT_MXFP4, fake, fake, None, None,
+                          None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "multiple of 32" in _err(lib)
+    rc = lib.dsl_fp4_gemm(fake, fake, fake, 4, 4, 64, 4, 0, N.FMT_NVFP4, fake, fake, None, None,
+                          None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "global" in _err(lib)
+    rc = lib.dsl_fp4_gemm(fake, fake, fake, 4, 4, 64, 4, 0, 9, fake, fake, None, None,
+                          None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "fmt" in _err(lib)
+    rc = lib.dsl_fp4_gemm(fake, fake, fake, 4, 4, 64, 4, 5, N.FMT_MXFP4, fake, fake, None, None,
+                          None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "out_dtype" in _err(lib)
+
+
+def test_grouped_gemm_argument_validation(lib):
+    fake = 1 << 20
+    rc = lib.dsl_grouped_fp8_gemm(fake, fake, fake, fake, 0, 8, 16, 16, 16, 0, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "num_groups" in _err(lib)
+    rc = lib.dsl_grouped_fp8_gemm(fake, fake, fake, fake, 4096, 8, 16, 16, 16, 0, fake, fake,
+                                  None)
+    assert rc == N.DSL_ERR_ARG
+    rc = lib.dsl_grouped_fp8_gemm(fake, fake, fake, None, 4, 8, 16, 16, 16, 0, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "NULL" in _err(lib)
+
+
+def test_quantizer_argument_validation(lib):
+    fake = 1 << 20
+    rc = lib.dsl_quant_mxfp4(fake, 4, 48, 48, 1, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "multiple of 32" in _err(lib)
+    rc = lib.dsl_quant_nvfp4(fake, 4, 40, 40, 1, fake, fake, fake, fake, 1 << 20, None)
+    assert rc == N.DSL_ERR_ARG and "multiple of 16" in _err(lib)
+    rc = lib.dsl_quant_fp8_tensor(fake, 4, 64, 64, 1, fake, fake, fake, 4, None)
+    assert rc == N.DSL_ERR_WORKSPACE
+    rc = lib.dsl_quant_fp8_blocks(fake, 4, 64, 64, 1, 0, 128, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "group" in _err(lib)
+    rc = lib.dsl_quant_fp8_blocks(fake + 1, 4, 64, 64, 1, 1, 128, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "aligned" in _err(lib)
+    rc = lib.dsl_quant_fp8_blocks(fake, 4, 64, -3, 1, 1, 128, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "stride" in _err(lib)
+    # an empty input is a successful no-op
+    assert lib.dsl_quant_mxfp4(None, 0, 64, 64, 1, None, None, None) == 0
+
+
+def test_error_message_is_cleared_on_success(lib):
+    lib.dsl_quant_mxfp4(1 << 20, 4, 48, 48, 1, 1 << 20, 1 << 20, None)
+    assert _err(lib)
+    assert lib.dsl_quant_mxfp4(None, 0, 64, 64, 1, None, None, None) == 0
+    assert _err(lib) == ""
+
+
+def test_python_wrappers_raise_dslerror(lib):
+    with pytest.raises(N.DslError) as ei:
+        N.call("dsl_quant_mxfp4", 1 << 20, 4, 48, 48, 1, 1 << 20, 1 << 20, None)
+    assert ei.value.status == N.DSL_ERR_ARG
