@@ -1,6 +1,7 @@
 // Dense quantized GEMM: C[M,N] = A[M,K] . W[N,K]^T on gfx950 MFMA.
 // Variant selection (tile shape, split-K) lives in launch_gemm below.
 #include <algorithm>
+#include <cstdlib>
 
 #include "gemm_core.h"
 
@@ -149,7 +150,34 @@ size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K) {
   return pl.ksplit > 1 ? (size_t)((M * N + 3) / 4) * 4 * sizeof(float) : 0;
 }
 
+// Pipelined-kernel variant for this problem, or -1 for the register-staged
+// kernels above.  DSL_GEMM_PIPE=off disables it (A/B comparisons).
+static int pipe_variant(int mode, const GemmArgs &p) {
+  // DSL_GEMM_PIPE: unset = automatic, "off" = never, a digit = force that
+  // variant for large problems (tuning sweeps).
+  static const int forced = [] {
+    const char *e = getenv("DSL_GEMM_PIPE");
+    if (!e || !e[0]) return -1;
+    if (e[0] == 'o' || e[0] == 'O') return -2;
+    return e[0] >= '0' && e[0] <= '9' ? e[0] - '0' : -1;
+  }();
+  if (forced == -2 || mode == MODE_NVFP4 || p.Kb % 128 != 0) return -1;
+  if (mode != MODE_FP8_TENSOR &&
+      ((reinterpret_cast<uintptr_t>(p.sa) | reinterpret_cast<uintptr_t>(p.sb)) & 3) != 0)
+    return -1;
+  const int64_t t256 = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
+  if (t256 >= 240) return forced >= 0 ? forced : 0;
+  const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
+  if (p.M > 64 && p.N > 64 && t128 >= 200) return 1;
+  return -1;
+}
+
 hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
+  const int pv = pipe_variant(mode, p);
+  if (pv >= 0) {
+    p.ksplit = 1;
+    return launch_gemm_pipe(mode, p, pv, st);
+  }
   const Plan pl = plan_for(p.M, p.N, p.Kb);
   p.ksplit = pl.ksplit;
   if (p.ksplit > 1) {

@@ -41,6 +41,10 @@ struct GemmArgs {
   int out_f32;
 };
 
+// LDS-DMA pipelined kernel (FP8_TENSOR / MXFP4, Kb % 64 == 0, no split-K);
+// variant 0: 256x256 tile, 8 waves; 1: 128x128 tile, 4 waves.
+hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_t st);
+
 // Picks a kernel variant for the shape and launches it (plus the split-K
 // zero-fill / finalize kernels when ksplit > 1).
 hipError_t launch_gemm(int mode, GemmArgs args, hipStream_t st);

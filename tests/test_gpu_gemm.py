@@ -180,3 +180,75 @@ def test_grouped_registered_variable_and_fixed():
     off3 = np.array([0, 64, 128, 192], np.int32)
     ref3 = OG.ref_grouped_fp8(qx3, sx3[:, 0], qw3.reshape(3, 96, 128), sw3.reshape(3, 96), off3)
     assert_close(y3.reshape(-1, 96), ref3, what="grouped_gemm fixed")
+
+
+# -------------------------------------------- LDS-DMA pipelined variants --
+# Shapes chosen to take the pipelined kernels: >= 240 tiles of 256x256
+# (variant 0) or >= 200 tiles of 128x128 (variant 1), with ragged M/N edges
+# and K shorter than the stage ring.
+PIPE_SHAPES = [(4096, 4096, 256), (4000, 4100, 640), (2048, 1920, 512), (3840, 4096, 128)]
+
+
+@pytest.mark.parametrize("m,n,k", PIPE_SHAPES)
+def test_fp8_per_tensor_pipelined(m, n, k):
+    a = W.randn_bf16((m, k), 111)
+    w = W.randn_bf16((n, k), 112, 0.02)
+    qa, sa = Q.quant_fp8_tensor(a.to(DEV))
+    qw, sw = Q.quant_fp8_tensor(w.to(DEV))
+    c = G.fp8_gemm_packed(qa, qw, sa, sw)
+    ref = OG.ref_fp8_per_tensor(np_u8(qa), np_f32(sa)[0], np_u8(qw), np_f32(sw)[0])
+    assert_close(c, ref, what=f"fp8 pipelined {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", PIPE_SHAPES)
+def test_mxfp4_pipelined(m, n, k):
+    a = W.randn_bf16((m, k), 311)
+    w = W.randn_bf16((n, k), 312, 0.02)
+    qa, ea = Q.quant_mxfp4(a.to(DEV))
+    qw, ew = Q.quant_mxfp4(w.to(DEV))
+    c = G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4")
+    ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
+    assert_close(c, ref, what=f"mxfp4 pipelined {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", PIPE_SHAPES)
+def test_fp8_block_pipelined(m, n, k):
+    a = W.activations(2, m, k, outliers=True)
+    w = W.randn_bf16((n, k), 212, 0.02)
+    qa, sa = Q.quant_fp8_blocks(a.to(DEV), 1, 128)
+    qw, sw = Q.quant_fp8_blocks(w.to(DEV), 128, 128)
+    c = G.fp8_gemm_packed(qa, qw, sa, sw, block=True)
+    ref = OG.ref_fp8_groupwise(np_u8(qa), np_f32(sa), np_u8(qw), np_f32(sw))
+    assert_close(c, ref, what=f"fp8 block pipelined {m}x{n}x{k}")
+
+
+def _e4m3_values(codes):
+    c = codes.astype(np.int64)
+    s = np.where(c & 0x80, -1.0, 1.0)
+    e, mt = (c >> 3) & 15, c & 7
+    return s * np.where(e == 0, mt / 8.0 * 2.0 ** -6, (1 + mt / 8.0) * 2.0 ** (e - 7))
+
+
+def test_fp8_mfma_accumulation_bound():
+    """The FP8 MFMA's accumulation error bound the output tolerance relies on:
+    exact for codes of one narrow exponent range and for subnormals, and
+    within 1e-4 of max|C| for codes spanning the whole E4M3 range."""
+    rng = np.random.default_rng(7)
+    one = torch.ones(1, device=DEV)
+
+    def codes(shape, lo, hi):
+        c = rng.integers(lo, hi + 1, size=shape).astype(np.uint8)
+        return c | (rng.integers(0, 2, size=shape).astype(np.uint8) << 7)
+
+    def fp32_gemm(qa, qw):
+        c = G.fp8_gemm_packed(torch.from_numpy(qa).to(DEV), torch.from_numpy(qw).to(DEV), one, one,
+                              out_dtype=torch.float32)
+        return np_f32(c).astype(np.float64), _e4m3_values(qa) @ _e4m3_values(qw).T
+
+    for m, n, k in [(16, 16, 128), (256, 512, 512)]:
+        got, exact = fp32_gemm(codes((m, k), 0x30, 0x40), codes((n, k), 0x30, 0x40))
+        assert np.array_equal(got, exact)
+        got, exact = fp32_gemm(codes((m, k), 0x01, 0x07), np.full((n, k), 0x38, np.uint8))
+        assert np.array_equal(got, exact)
+        got, exact = fp32_gemm(codes((m, k), 0x00, 0x7E), codes((n, k), 0x00, 0x7E))
+        assert np.abs(got - exact).max() <= 1e-4 * np.abs(exact).max()

@@ -4,7 +4,16 @@ import torch
 
 from oracle import gemm as OG
 
-TOL = 1e-2   # max|C-R|/max|R| and elementwise rel. on |R| >= 0.1 rms(R)
+# Output tolerance against the dequantize -> fp32 matmul -> bf16 oracle.
+# TOL is the north-star bound on max|C-R| / max|R|.  ELEM_TOL bounds the
+# elementwise relative error on entries with |R| >= 0.1 rms(R): bf16 output
+# rounding alone allows 2^-7 (0.78%) there, and the gfx950 FP8 MFMA sums the
+# products of one instruction after aligning them to the largest (measured:
+# error <= 1e-4 of max|C| for codes spanning the whole E4M3 range, exact for
+# narrow ranges; tests/test_gpu_gemm.py::test_fp8_mfma_accumulation_bound),
+# which with 50x activation outliers adds a few tenths of a percent.
+TOL = 1e-2
+ELEM_TOL = 2e-2
 
 
 def np_u8(t: torch.Tensor) -> np.ndarray:
@@ -19,10 +28,21 @@ def f32_of_bf16(t: torch.Tensor) -> np.ndarray:
     return t.detach().cpu().float().numpy()
 
 
-def assert_close(c: torch.Tensor, ref: np.ndarray, tol: float = TOL, what: str = ""):
+def assert_close(c: torch.Tensor, ref: np.ndarray, tol: float = TOL, what: str = "",
+                 elem_tol: float = ELEM_TOL):
     got = np_f32(c)
     assert got.shape == ref.shape, (got.shape, ref.shape)
     assert np.isfinite(got).all(), f"{what}: non-finite output"
     glob, elem = OG.rel_errors(got, ref)
-    assert glob <= tol and elem <= tol, f"{what}: max-rel {glob:.3e}, elementwise {elem:.3e} > {tol}"
+    if not (glob <= tol and elem <= elem_tol):
+        err = np.abs(got.astype(np.float64) - ref)
+        r, c = np.unravel_index(int(err.argmax()), err.shape)
+        bad = err > tol * np.abs(ref).max()
+        rows, cols = np.nonzero(bad)
+        where = (f"worst at [{r}, {c}] got {got[r, c]:.6g} want {ref[r, c]:.6g}; "
+                 f"{int(bad.sum())} entries over the global bound"
+                 + (f", rows {rows.min()}..{rows.max()}, cols {cols.min()}..{cols.max()}"
+                    if bad.any() else ""))
+        raise AssertionError(f"{what}: max-rel {glob:.3e} (bound {tol}), elementwise {elem:.3e} "
+                             f"(bound {elem_tol}); {where}")
     return glob, elem
