@@ -2,6 +2,7 @@
 // Variant selection (tile shape, split-K) lives in launch_gemm below.
 #include <algorithm>
 #include <cstdlib>
+#include <cstring>
 
 #include "gemm_core.h"
 
@@ -144,42 +145,74 @@ void launch_mode(const Plan &pl, const GemmArgs &p, hipStream_t st) {
 
 }  // namespace
 
-size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K) {
-  const int Kb = (mode == MODE_MXFP4 || mode == MODE_NVFP4) ? (int)(K / 2) : (int)K;
-  const Plan pl = plan_for((int)M, (int)N, Kb);
-  return pl.ksplit > 1 ? (size_t)((M * N + 3) / 4) * 4 * sizeof(float) : 0;
+// True when environment variable `name` is "0", "off" or "false" (any case).
+static bool env_off(const char *name) {
+  const char *e = getenv(name);
+  if (!e) return false;
+  char buf[8] = {0};
+  for (int i = 0; i < 7 && e[i]; ++i) buf[i] = (char)((e[i] >= 'A' && e[i] <= 'Z') ? e[i] + 32 : e[i]);
+  return strcmp(buf, "0") == 0 || strcmp(buf, "off") == 0 || strcmp(buf, "false") == 0;
 }
 
-// Pipelined-kernel variant for this problem, or -1 for the register-staged
-// kernels above.  DSL_GEMM_PIPE=off disables it (A/B comparisons).
-static int pipe_variant(int mode, const GemmArgs &p) {
-  // DSL_GEMM_PIPE: unset = automatic, "off" = never, a digit = force that
-  // variant for large problems (tuning sweeps).
-  static const int forced = [] {
+// Kernel path for a problem.  The choice depends on the shape and on the
+// alignment of the scale pointers only, so the workspace query (which sees
+// no pointers and assumes aligned scales) and the launch agree whenever the
+// scales are aligned; with misaligned scales the launch may fall back to
+// the register-staged kernels, split-K only if a workspace was passed.
+//   DSL_GEMM_DECODE = 0/off    never use the skinny-M kernel
+//   DSL_GEMM_PIPE   = 0/off    never use the LDS-DMA pipelined kernels
+//   DSL_GEMM_PIPE   = 1..9     force that pipelined variant for large problems
+enum { PATH_DECODE = 0, PATH_PIPE = 1, PATH_TILED = 2 };
+struct Route {
+  int path;
+  int variant;    // PATH_PIPE variant
+  Plan tiled;     // PATH_TILED plan
+};
+
+static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc16) {
+  static const bool decode_on = !env_off("DSL_GEMM_DECODE");
+  static const int pipe_forced = [] {
+    if (env_off("DSL_GEMM_PIPE")) return -2;
     const char *e = getenv("DSL_GEMM_PIPE");
-    if (!e || !e[0]) return -1;
-    if (e[0] == 'o' || e[0] == 'O') return -2;
-    return e[0] >= '0' && e[0] <= '9' ? e[0] - '0' : -1;
+    return (e && e[0] >= '1' && e[0] <= '9' && !e[1]) ? e[0] - '0' : -1;
   }();
-  if (forced == -2 || mode == MODE_NVFP4 || p.Kb % 128 != 0) return -1;
-  if (mode != MODE_FP8_TENSOR &&
-      ((reinterpret_cast<uintptr_t>(p.sa) | reinterpret_cast<uintptr_t>(p.sb)) & 3) != 0)
-    return -1;
-  const int64_t t256 = (int64_t)((p.M + 255) / 256) * ((p.N + 255) / 256);
-  if (t256 >= 240) return forced >= 0 ? forced : 0;
-  const int64_t t128 = (int64_t)((p.M + 127) / 128) * ((p.N + 127) / 128);
-  if (p.M > 64 && p.N > 64 && t128 >= 200) return 1;
-  return -1;
+  Route r{PATH_TILED, -1, plan_for(M, N, Kb)};
+  if (decode_on && decode_supported(mode, M, K, Kb, sc4, sc16)) {
+    r.path = PATH_DECODE;
+    return r;
+  }
+  const bool pipe_ok = pipe_forced != -2 && mode != MODE_NVFP4 && Kb % 128 == 0 &&
+                       (mode == MODE_FP8_TENSOR || sc4);
+  if (pipe_ok) {
+    const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+    if (t256 >= 240) {
+      r.path = PATH_PIPE;
+      r.variant = pipe_forced >= 0 ? pipe_forced : 0;
+    } else if (M > 64 && N > 64 && t128 >= 200) {
+      r.path = PATH_PIPE;
+      r.variant = 1;
+    }
+  }
+  return r;
+}
+
+size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K) {
+  const int Kb = (mode == MODE_MXFP4 || mode == MODE_NVFP4) ? (int)(K / 2) : (int)K;
+  const Route r = route_for(mode, (int)M, (int)N, (int)K, Kb, true, true);
+  return (r.path == PATH_TILED && r.tiled.ksplit > 1)
+             ? (size_t)((M * N + 3) / 4) * 4 * sizeof(float)
+             : 0;
 }
 
 hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
-  const int pv = pipe_variant(mode, p);
-  if (pv >= 0) {
-    p.ksplit = 1;
-    return launch_gemm_pipe(mode, p, pv, st);
-  }
-  const Plan pl = plan_for(p.M, p.N, p.Kb);
-  p.ksplit = pl.ksplit;
+  const uintptr_t sc = reinterpret_cast<uintptr_t>(p.sa) | reinterpret_cast<uintptr_t>(p.sb);
+  const Route r = route_for(mode, p.M, p.N, p.K, p.Kb, (sc & 3) == 0, (sc & 15) == 0);
+  p.ksplit = 1;
+  if (r.path == PATH_DECODE) return launch_gemm_decode(mode, p, st);
+  if (r.path == PATH_PIPE) return launch_gemm_pipe(mode, p, r.variant, st);
+  const Plan pl = r.tiled;
+  p.ksplit = p.ws ? pl.ksplit : 1;
   if (p.ksplit > 1) {
     const int64_t n4 = ((int64_t)p.M * p.N + 3) / 4;   // workspace is rounded up to float4
     fill_zero_kernel<<<(unsigned)std::min<int64_t>((n4 + 255) / 256, 4096), 256, 0, st>>>(

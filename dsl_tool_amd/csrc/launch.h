@@ -45,6 +45,12 @@ struct GemmArgs {
 // variant 0: 256x256 tile, 8 waves; 1: 128x128 tile, 4 waves.
 hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_t st);
 
+// Skinny-M kernel (M <= 32, Kb % 1024 == 0; FP8_TENSOR, FP8_BLOCK with
+// 4-byte aligned scales, MXFP4 with 16-byte aligned scale rows): one
+// launch, no workspace.
+bool decode_supported(int mode, int M, int K, int Kb, bool scales4, bool scales16);
+hipError_t launch_gemm_decode(int mode, const GemmArgs &p, hipStream_t st);
+
 // Picks a kernel variant for the shape and launches it (plus the split-K
 // zero-fill / finalize kernels when ksplit > 1).
 hipError_t launch_gemm(int mode, GemmArgs args, hipStream_t st);

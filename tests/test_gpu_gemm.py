@@ -252,3 +252,41 @@ def test_fp8_mfma_accumulation_bound():
         assert np.array_equal(got, exact)
         got, exact = fp32_gemm(codes((m, k), 0x00, 0x7E), codes((n, k), 0x00, 0x7E))
         assert np.abs(got - exact).max() <= 1e-4 * np.abs(exact).max()
+
+
+# ------------------------------------------------ skinny-M decode kernel --
+DECODE_SHAPES = [(1, 1000, 4096), (7, 2048, 1024), (16, 7168, 4096), (32, 1040, 2048)]
+
+
+@pytest.mark.parametrize("m,n,k", DECODE_SHAPES)
+def test_fp8_per_tensor_decode(m, n, k):
+    a = W.randn_bf16((m, k), 121)
+    w = W.randn_bf16((n, k), 122, 0.02)
+    qa, sa = Q.quant_fp8_tensor(a.to(DEV))
+    qw, sw = Q.quant_fp8_tensor(w.to(DEV))
+    c = G.fp8_gemm_packed(qa, qw, sa, sw)
+    ref = OG.ref_fp8_per_tensor(np_u8(qa), np_f32(sa)[0], np_u8(qw), np_f32(sw)[0])
+    assert_close(c, ref, what=f"fp8 decode {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", DECODE_SHAPES)
+def test_fp8_block_decode(m, n, k):
+    a = W.activations(2, m, k, outliers=True)
+    w = W.randn_bf16((n, k), 222, 0.02)
+    qa, sa = Q.quant_fp8_blocks(a.to(DEV), 1, 128)
+    qw, sw = Q.quant_fp8_blocks(w.to(DEV), 128, 128)
+    c = G.fp8_gemm_packed(qa, qw, sa, sw, block=True)
+    ref = OG.ref_fp8_groupwise(np_u8(qa), np_f32(sa), np_u8(qw), np_f32(sw))
+    assert_close(c, ref, what=f"fp8 block decode {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 1000, 4096), (7, 2048, 1024), (16, 8192, 8192),
+                                   (32, 1040, 2048)])
+def test_mxfp4_decode(m, n, k):
+    a = W.randn_bf16((m, k), 321)
+    w = W.randn_bf16((n, k), 322, 0.02)
+    qa, ea = Q.quant_mxfp4(a.to(DEV))
+    qw, ew = Q.quant_mxfp4(w.to(DEV))
+    c = G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4")
+    ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
+    assert_close(c, ref, what=f"mxfp4 decode {m}x{n}x{k}")

@@ -56,11 +56,18 @@ def test_fp8_gemm_argument_validation(lib):
     assert lib.dsl_fp8_gemm(None, None, None, 0, 16, 16, 16, 0, 0, fake, fake, None, 0, None) == 0
 
 
-def test_fp8_gemm_workspace_is_required_when_split_k_is_planned(lib):
-    need = lib.dsl_gemm_workspace_bytes(N.OP_FP8, 16, 8192, 8192)
-    assert need > 0
+def test_workspace_query_matches_the_planned_path(lib):
+    # skinny M with K a multiple of 1024 takes the single-pass decode kernel
+    assert lib.dsl_gemm_workspace_bytes(N.OP_FP8, 16, 8192, 8192) == 0
+    assert lib.dsl_gemm_workspace_bytes(N.OP_FP4, 16, 8192, 8192) == 0
+    # large problems take the pipelined kernels, which need none either
+    assert lib.dsl_gemm_workspace_bytes(N.OP_FP8, 8192, 8192, 8192) == 0
+    # a skinny problem the decode kernel does not cover plans split-K and
+    # then requires the workspace it reports
+    need = lib.dsl_gemm_workspace_bytes(N.OP_FP8, 16, 8192, 8208)
+    assert need >= 16 * 8192 * 4
     fake = 1 << 20
-    rc = lib.dsl_fp8_gemm(fake, fake, fake, 16, 8192, 8192, 8192, 0, 0, fake, fake, None,
+    rc = lib.dsl_fp8_gemm(fake, fake, fake, 16, 8192, 8208, 8192, 0, 0, fake, fake, None,
                           need - 4, None)
     assert rc == N.DSL_ERR_WORKSPACE
 
