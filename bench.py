@@ -18,7 +18,14 @@ Cache cannot serve them, and are timed as a captured HIP graph of K launches
 so host launch latency does not enter the kernel time.
 
 ``cpu_baseline`` times the CPU oracle (dequantize -> fp32 torch matmul) on
-the headline workload with a bounded row sample, on the host's cores.
+the headline workload, on the host's cores.
+
+``roofline.traffic`` is the headline kernel's HBM bytes per launch from two
+``rocprofv3 --pmc`` runs (FETCH_SIZE, then WRITE_SIZE) of
+``python3 bench.py --profile-traffic``, each scaled by the same counter's
+reading for a plain 256 MiB device copy in that run; the summary lives in
+``profiles/fp8_block_m4096_traffic.txt`` and is read from there (null when
+the file is absent).
 
 Only one GPU: ``--gpus N`` with N > 1 exits with a message.
 """
@@ -39,6 +46,8 @@ PEAK_FP4_TFLOPS = 10100.0     # MI355X dense fp4 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 HEADLINE = "fp8_block_m4096"
 MALL_BYTES = 256 << 20
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fp8_block_m4096_traffic.txt")
+COPY_BYTES = 256 << 20          # calibration copy for the HBM byte counters
 
 
 def log(msg: str) -> None:
@@ -221,6 +230,41 @@ def time_case(case, steps, warmup, dev, graph):
     return start.elapsed_time(end) / steps
 
 
+def read_traffic(path: str = TRAFFIC_FILE):
+    """HBM bytes per headline launch recorded by the counter runs, or None."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip())
+    except OSError:
+        return None
+    return None
+
+
+def profile_traffic(steps: int) -> int:
+    """Workload for the FETCH_SIZE / WRITE_SIZE counter runs: a plain device
+    copy of COPY_BYTES (the calibration), then `steps` headline launches."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize(dev)
+    case = build_cases([HEADLINE], dev)[HEADLINE]
+    s = torch.cuda.Stream(device=dev)
+    with torch.cuda.stream(s):
+        for i in range(steps):
+            rc = case.launch(i, s.cuda_stream)
+            if rc != 0:
+                raise RuntimeError(f"headline launch failed with status {rc}")
+    torch.cuda.synchronize(dev)
+    log(f"profile-traffic: 3 copies of {COPY_BYTES} bytes, {steps} headline launches")
+    return 0
+
+
 def cpu_baseline(sample_rows: int):
     """The oracle (dequantize -> fp32 CPU matmul -> bf16) on the headline
     workload restricted to its first `sample_rows` activation rows."""
@@ -255,6 +299,8 @@ def main(argv=None):
                     help="comma list of extra cases, 'all' or 'none' (headline always runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-rows", type=int, default=4096)
+    ap.add_argument("--profile-traffic", action="store_true",
+                    help="run only the copy calibration and headline launches for rocprofv3 --pmc")
     args = ap.parse_args(argv)
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the quantized GEMM "
@@ -269,6 +315,8 @@ def main(argv=None):
     torch.cuda.set_device(dev)
     from dsl_tool_amd import _native as N
     N.lib()
+    if args.profile_traffic:
+        return profile_traffic(args.steps)
 
     extra = ALL_CASES[1:] if args.cases == "all" else (
         [] if args.cases == "none" else [c for c in args.cases.split(",") if c and c != HEADLINE])
@@ -316,7 +364,7 @@ def main(argv=None):
                    "cus": props.multi_processor_count},
         "roofline": {"bound": "mfma", "achieved": h["tflops"], "peak": PEAK_FP8_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(h["tflops"] / PEAK_FP8_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": read_traffic()},
         "cpu_baseline": cpu,
         "cases": results,
     }

@@ -158,8 +158,15 @@ int dsl_quant_nvfp4(const void *x, int64_t rows, int64_t cols, int64_t sr, int64
 
 size_t dsl_gemm_workspace_bytes(int op, int64_t m, int64_t n, int64_t k) {
   if (m <= 0 || n <= 0 || k <= 0) return 0;
-  if (op == DSL_OP_FP8) return dsl::gemm_workspace_bytes(dsl::MODE_FP8_TENSOR, m, n, k);
-  if (op == DSL_OP_FP4) return dsl::gemm_workspace_bytes(dsl::MODE_MXFP4, m, n, k);
+  // the op does not say which scale mode / FP4 format follows, so report
+  // the larger of the two plans
+  auto mx = [](size_t a, size_t b) { return a > b ? a : b; };
+  if (op == DSL_OP_FP8)
+    return mx(dsl::gemm_workspace_bytes(dsl::MODE_FP8_TENSOR, m, n, k),
+              dsl::gemm_workspace_bytes(dsl::MODE_FP8_BLOCK, m, n, k));
+  if (op == DSL_OP_FP4)
+    return mx(dsl::gemm_workspace_bytes(dsl::MODE_MXFP4, m, n, k),
+              dsl::gemm_workspace_bytes(dsl::MODE_NVFP4, m, n, k));
   return 0;
 }
 

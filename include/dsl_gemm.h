@@ -144,7 +144,11 @@ int dsl_grouped_fp8_gemm(const uint8_t *x, const uint8_t *w, void *y,
                          void *stream);
 
 /* Workspace bytes dsl_fp8_gemm / dsl_fp4_gemm need for this shape
- * (op = DSL_OP_FP8 or DSL_OP_FP4; 0 when none is needed). */
+ * (op = DSL_OP_FP8 or DSL_OP_FP4; the larger of the plans of the op's two
+ * scale modes / FP4 formats; 0 when none is needed).  The kernel choice
+ * depends on the shape and on the scale pointers' alignment; with scale
+ * arrays that are not 16-byte aligned a launch may fall back to a kernel
+ * that runs without split-K rather than ask for more workspace. */
 size_t dsl_gemm_workspace_bytes(int op, int64_t m, int64_t n, int64_t k);
 
 #ifdef __cplusplus
