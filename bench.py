@@ -171,6 +171,7 @@ def build_cases(names, dev):
                                             W.activations(2, 4096, 4096, outliers=True),
                                             W.weights(2, 7168, 4096)),
         "fp8_block_m16": lambda: fp8_case("fp8_block_m16", 16, 7168, 4096, True),
+        "fp8_tensor_m4096": lambda: fp8_case("fp8_tensor_m4096", 4096, 7168, 4096, False),
         "fp8_tensor_cfg1": lambda: fp8_case("fp8_tensor_cfg1", 128, 4096, 4096, False),
         "fp8_tensor_8192": lambda: fp8_case("fp8_tensor_8192", 8192, 8192, 8192, False),
         "mxfp4_8192": lambda: fp4_case("mxfp4_8192", 8192, 8192, 8192, "mxfp4"),
@@ -184,7 +185,8 @@ def build_cases(names, dev):
     return cases
 
 
-ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_cfg1", "fp8_tensor_8192",
+ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor_cfg1",
+             "fp8_tensor_8192",
              "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe"]
 
 

@@ -290,3 +290,30 @@ def test_mxfp4_decode(m, n, k):
     c = G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4")
     ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
     assert_close(c, ref, what=f"mxfp4 decode {m}x{n}x{k}")
+
+
+def test_grouped_moe_skewed_counts_pipelined():
+    # Zipf-skewed expert counts (two empty experts), K % 64 == 0 -> pipelined kernel
+    counts = W.moe_counts(num_experts=16, tokens=512, top_k=4, n_empty=2, seed=777).tolist()
+    n, k = 512, 2048
+    x, w, offsets = _grouped_case(counts, n, k, 701)
+    G_ = len(counts)
+    qx, sx = Q.quant_fp8_blocks(x.to(DEV), 1, k)
+    qw, sw = Q.quant_fp8_blocks(w.reshape(G_ * n, k).to(DEV), 1, k)
+    y = G.grouped_fp8_gemm_packed(qx, sx, qw.reshape(G_, n, k), sw.reshape(G_, n),
+                                  torch.from_numpy(offsets).to(DEV))
+    ref = OG.ref_grouped_fp8(np_u8(qx), np_f32(sx)[:, 0], np_u8(qw).reshape(G_, n, k),
+                             np_f32(sw).reshape(G_, n), offsets)
+    assert_close(y, ref, what=f"grouped MoE {counts}")
+
+
+def test_grouped_register_staged_fallback_k_not_multiple_of_64():
+    counts = [9, 0, 70, 33]
+    x, w, offsets = _grouped_case(counts, 96, 272, 711)
+    qx, sx = Q.quant_fp8_blocks(x.to(DEV), 1, 272)
+    qw, sw = Q.quant_fp8_blocks(w.reshape(4 * 96, 272).to(DEV), 1, 272)
+    y = G.grouped_fp8_gemm_packed(qx, sx, qw.reshape(4, 96, 272), sw.reshape(4, 96),
+                                  torch.from_numpy(offsets).to(DEV))
+    ref = OG.ref_grouped_fp8(np_u8(qx), np_f32(sx)[:, 0], np_u8(qw).reshape(4, 96, 272),
+                             np_f32(sw).reshape(4, 96), offsets)
+    assert_close(y, ref, what="grouped fallback")
