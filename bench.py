@@ -43,6 +43,7 @@ if ROOT not in sys.path:
 
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 PEAK_FP4_TFLOPS = 10100.0     # MI355X dense fp4 MFMA
+PEAK_FP16_TFLOPS = 2500.0     # MI355X dense fp16 MFMA (the NVFP4 kernels dequantize to fp16)
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 HEADLINE = "fp8_block_m4096"
 MALL_BYTES = 256 << 20
@@ -142,10 +143,11 @@ def build_cases(names, dev):
                                   N.OUT_BF16, code, sa.data_ptr(), s_.data_ptr(), gap, gwp,
                                   ws.data_ptr(), nb, stream)
         nbytes = qa.numel() + sa.numel() + wbytes + 2 * m * n
-        ridge = PEAK_FP4_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+        peak = PEAK_FP4_TFLOPS if fmt == "mxfp4" else PEAK_FP16_TFLOPS
+        ridge = peak * 1e12 / (PEAK_HBM_GBS * 1e9)
         bound = "hbm" if 2 * m * n * k / nbytes < ridge else "mfma"
-        return Case(name, 2.0 * m * n * k, nbytes, PEAK_FP4_TFLOPS, bound, launch, rot,
-                    f"{fmt} M={m} N={n} K={k}")
+        return Case(name, 2.0 * m * n * k, nbytes, peak, bound, launch, rot,
+                    f"{fmt} M={m} N={n} K={k}" + ("" if fmt == "mxfp4" else " (fp16 MFMA peak)"))
 
     def grouped_case(name):
         x, w, offsets, counts = W.moe_problem()

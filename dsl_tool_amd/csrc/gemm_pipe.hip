@@ -20,7 +20,8 @@ void gemm_pipe_kernel(const GemmArgs p) {
   pipe_mainloop<Cfg>(p, m0, n0, smem, wave, lane, acc);
 
   float s1 = 1.f, s2 = 1.f;
-  if constexpr (MODE_FP8_TENSOR == Cfg::MODE) {
+  constexpr bool GLOBAL = Cfg::MODE == MODE_FP8_TENSOR || Cfg::MODE == MODE_NVFP4;
+  if constexpr (GLOBAL) {
     s1 = *p.ga;
     s2 = *p.gb;
   }
@@ -35,7 +36,7 @@ void gemm_pipe_kernel(const GemmArgs p) {
         const int row = m0 + wm * Cfg::WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
         if (row >= p.M) continue;
         float v = acc[i][j][r];
-        if constexpr (MODE_FP8_TENSOR == Cfg::MODE) v = (v * s1) * s2;
+        if constexpr (GLOBAL) v = (v * s1) * s2;
         if (p.out_f32) static_cast<float *>(p.c)[(int64_t)row * p.ldc + col] = v;
         else static_cast<uint16_t *>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16(v);
       }
@@ -157,6 +158,13 @@ hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_
       case 2: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 256, 2, 4, 2, 128>>(p, st);
       case 3: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 128, 4, 2, 3, 128>>(p, st);
       default: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 128, 128, 2, 2, 4, 64>>(p, st);
+    }
+  }
+  if (mode == MODE_NVFP4) {
+    switch (variant) {
+      case 1: return launch_pipe_cfg<PipeCfg<MODE_NVFP4, 128, 128, 2, 2, 4, 64, 2>>(p, st);
+      case 2: return launch_pipe_cfg<PipeCfg<MODE_NVFP4, 256, 256, 2, 4, 4, 64>>(p, st);
+      default: return launch_pipe_cfg<PipeCfg<MODE_NVFP4, 256, 256, 2, 4, 2, 128>>(p, st);
     }
   }
   switch (variant) {

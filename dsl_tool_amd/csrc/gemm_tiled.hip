@@ -181,8 +181,7 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
     r.path = PATH_DECODE;
     return r;
   }
-  const bool pipe_ok = pipe_forced != -2 && mode != MODE_NVFP4 && Kb % 128 == 0 &&
-                       (mode == MODE_FP8_TENSOR || sc4);
+  const bool pipe_ok = pipe_forced != -2 && Kb % 128 == 0 && (mode == MODE_FP8_TENSOR || sc4);
   if (pipe_ok) {
     const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
     const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);

@@ -88,12 +88,17 @@ struct PipeCfg {
   static constexpr int OCC = OCC_ > 0 ? OCC_ : (NW >= 8 ? 2 : 1);   // waves per SIMD
   static constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
   static constexpr bool MX = MODE == MODE_MXFP4;
+  static constexpr bool NV = MODE == MODE_NVFP4;
+  static constexpr bool FP4 = MX || NV;
   static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;     // one 128-K scale group per stage
   static constexpr int CH = SKB / 16, RPI = 1024 / SKB;     // chunks per row, rows per DMA
-  static constexpr int KSTEPS = MX ? SKB / 32 : SKB / 64;   // 32x32x64 MFMA steps per stage
-  static constexpr int SCW = MX ? SKB / 64 : (BLOCK ? 1 : 0);  // scale words per row per stage
+  // MFMA steps per stage: 32x32x64 for FP8 / MXFP4; for NVFP4 a "step" is a
+  // quad of four 32x32x16 fp16 MFMAs over 64 elements (32 bytes)
+  static constexpr int KSTEPS = MX ? SKB / 32 : (NV ? SKB / 32 : SKB / 64);
+  // scale words (4 bytes) per row per stage: E8M0 per 32, E4M3 per 16, fp32 per 128-K group
+  static constexpr int SCW = MX ? SKB / 64 : (NV ? SKB / 32 : (BLOCK ? 1 : 0));
   static constexpr int A_BYTES = BM * SKB, B_BYTES = BN * SKB;
-  static constexpr int SA_BYTES = BM * 4 * SCW, SB_BYTES = MX ? BN * 4 * SCW : 0;
+  static constexpr int SA_BYTES = BM * 4 * SCW, SB_BYTES = FP4 ? BN * 4 * SCW : 0;
   static constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES + SB_BYTES;
   static constexpr int LDS = NS * STAGE;
   static constexpr int A_DMA = A_BYTES / 1024, B_DMA = B_BYTES / 1024;
@@ -156,10 +161,14 @@ struct Ring {
           src[j] = reinterpret_cast<const uint8_t *>(static_cast<const float *>(p.sa) +
                                                      (int64_t)grow * (p.K / 128));
           step[j] = 4;
-        } else {                           // E8M0 [row][K/32]: SKB/16 bytes per row per stage
+        } else if constexpr (Cfg::MX) {    // E8M0 [row][K/32]: SKB/16 bytes per row per stage
           src[j] = static_cast<const uint8_t *>(isA ? p.sa : p.sb) + (int64_t)grow * (p.K / 32) +
                    word * 4;
           step[j] = SKB / 16;
+        } else {                           // E4M3 [row][K/16]: SKB/8 bytes per row per stage
+          src[j] = static_cast<const uint8_t *>(isA ? p.sa : p.sb) + (int64_t)grow * (p.K / 16) +
+                   word * 4;
+          step[j] = SKB / 8;
         }
         dst[j] = Cfg::A_BYTES + Cfg::B_BYTES + (isA ? 0 : Cfg::SA_BYTES) +
                  (word * rows + rblk * 64) * 4;
@@ -188,7 +197,7 @@ DSL_DEV void mma_kstep(const uint8_t *st, int k, int wm, int wn, int r32, int h,
                        v16f (&acc)[Cfg::TM][Cfg::TN]) {
   constexpr int SKB = Cfg::SKB;
   const uint8_t *sA = st, *sB = st + Cfg::A_BYTES;
-  if constexpr (!Cfg::MX) {
+  if constexpr (!Cfg::FP4) {
     auto ld = [&](const uint8_t *base, int row) {
       const int s = pipe::swz<SKB>(row), c0 = 4 * k + 2 * h;
       const v4i lo = *reinterpret_cast<const v4i *>(base + row * SKB + ((c0 ^ s) << 4));
@@ -206,6 +215,49 @@ DSL_DEV void mma_kstep(const uint8_t *st, int k, int wm, int wn, int r32, int h,
       for (int j = 0; j < Cfg::TN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(af[i], bf[j], acc[i][j], 0, 0,
                                                                     0, 0, 0, 0);
+  } else if constexpr (Cfg::NV) {
+    // NVFP4 quad k: lane half h holds the 32 elements [64k + 32h, +32) of its
+    // row (one 16-byte chunk), taken as four 8-element K-steps i; K-step i
+    // of both operands covers elements 64k + 32h + 8i.. for lane half h, so
+    // A and W see the same K order and each lane's 8 elements lie in one
+    // 16-element E4M3 block (2h + i/2 of the quad's four).  Elements are
+    // dequantized to fp16 exactly (E2M1 x E4M3 has <= 5 significant bits)
+    // and multiplied by fp16 MFMAs; the fp32 global scales apply in the
+    // epilogue.  Scales: [word][row] u32 after the data tiles, word k holds
+    // the quad's four E4M3 bytes.
+    const uint8_t *sSa = st + Cfg::A_BYTES + Cfg::B_BYTES;
+    const uint8_t *sSb = sSa + Cfg::SA_BYTES;
+    v4i araw[Cfg::TM], braw[Cfg::TN];
+    _Float16 asc[Cfg::TM][2], bsc[Cfg::TN][2];
+#pragma unroll
+    for (int t = 0; t < Cfg::TN; ++t) {
+      const int row = wn * Cfg::WN + t * 32 + r32;
+      braw[t] = *reinterpret_cast<const v4i *>(sB + row * SKB + (((2 * k + h) ^ pipe::swz<SKB>(row)) << 4));
+      const uint32_t w = *reinterpret_cast<const uint32_t *>(sSb + (k * Cfg::BN + row) * 4);
+      bsc[t][0] = e4m3_to_f16((w >> (16 * h)) & 0xFF);
+      bsc[t][1] = e4m3_to_f16((w >> (16 * h + 8)) & 0xFF);
+    }
+#pragma unroll
+    for (int t = 0; t < Cfg::TM; ++t) {
+      const int row = wm * Cfg::WM + t * 32 + r32;
+      araw[t] = *reinterpret_cast<const v4i *>(sA + row * SKB + (((2 * k + h) ^ pipe::swz<SKB>(row)) << 4));
+      const uint32_t w = *reinterpret_cast<const uint32_t *>(sSa + (k * Cfg::BM + row) * 4);
+      asc[t][0] = e4m3_to_f16((w >> (16 * h)) & 0xFF);
+      asc[t][1] = e4m3_to_f16((w >> (16 * h + 8)) & 0xFF);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v8h af[Cfg::TM], bf[Cfg::TN];
+#pragma unroll
+      for (int t = 0; t < Cfg::TN; ++t) bf[t] = fp4x8_to_f16((uint32_t)braw[t][i], bsc[t][i >> 1]);
+#pragma unroll
+      for (int t = 0; t < Cfg::TM; ++t) af[t] = fp4x8_to_f16((uint32_t)araw[t][i], asc[t][i >> 1]);
+#pragma unroll
+      for (int a = 0; a < Cfg::TM; ++a)
+#pragma unroll
+        for (int b = 0; b < Cfg::TN; ++b)
+          acc[a][b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[a], bf[b], acc[a][b], 0, 0, 0);
+    }
   } else {
     // scales: [word][row] u32 after the two data tiles; byte j of the permuted
     // word is the E8M0 of block 2*j + h of the word's 4 blocks of this row

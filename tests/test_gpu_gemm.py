@@ -317,3 +317,14 @@ def test_grouped_register_staged_fallback_k_not_multiple_of_64():
     ref = OG.ref_grouped_fp8(np_u8(qx), np_f32(sx)[:, 0], np_u8(qw).reshape(4, 96, 272),
                              np_f32(sw).reshape(4, 96), offsets)
     assert_close(y, ref, what="grouped fallback")
+
+
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 256), (2048, 1920, 512), (4000, 4100, 768)])
+def test_nvfp4_pipelined(m, n, k):
+    a = W.randn_bf16((m, k), 411)
+    w = W.randn_bf16((n, k), 412, 0.02)
+    qa, sa, ga = Q.quant_nvfp4(a.to(DEV))
+    qw, sw, gw = Q.quant_nvfp4(w.to(DEV))
+    c = G.fp4_gemm_packed(qa, sa, qw, sw, fmt="nvfp4", global_a=ga, global_w=gw)
+    ref = OG.ref_nvfp4(np_u8(qa), np_u8(sa), np_f32(ga)[0], np_u8(qw), np_u8(sw), np_f32(gw)[0])
+    assert_close(c, ref, what=f"nvfp4 pipelined {m}x{n}x{k}")
