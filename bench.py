@@ -168,6 +168,55 @@ def build_cases(names, dev):
         return Case(name, flops, nbytes, PEAK_FP8_TFLOPS, "mfma", launch, 1,
                     f"grouped fp8 MoE E={E} T={T} N={Nn} K={K} ({E - nonempty} empty)")
 
+    def quant_case(name, kind, r, k):
+        """One quantize/pack pass over a bf16 [r, k] operand resident in HBM."""
+        x = rnd((r, k), 5, 0.02)
+        ws = torch.empty(L.dsl_quant_workspace_bytes(r, k) // 4, dtype=torch.float32, device=dev)
+        if kind == "fp8_block128":
+            q = torch.empty((r, k), dtype=torch.uint8, device=dev)
+            sc = torch.empty((-(-r // 128), -(-k // 128)), dtype=torch.float32, device=dev)
+            out_b, passes = r * k + sc.numel() * 4, 1
+
+            def launch(i, stream):
+                return L.dsl_quant_fp8_blocks(x.data_ptr(), r, k, k, 1, 128, 128, q.data_ptr(),
+                                              sc.data_ptr(), stream)
+        elif kind == "fp8_row128":
+            q = torch.empty((r, k), dtype=torch.uint8, device=dev)
+            sc = torch.empty((r, -(-k // 128)), dtype=torch.float32, device=dev)
+            out_b, passes = r * k + sc.numel() * 4, 1
+
+            def launch(i, stream):
+                return L.dsl_quant_fp8_blocks(x.data_ptr(), r, k, k, 1, 1, 128, q.data_ptr(),
+                                              sc.data_ptr(), stream)
+        elif kind == "fp8_tensor":
+            q = torch.empty((r, k), dtype=torch.uint8, device=dev)
+            sc = torch.empty(1, dtype=torch.float32, device=dev)
+            out_b, passes = r * k + 4, 2
+
+            def launch(i, stream):
+                return L.dsl_quant_fp8_tensor(x.data_ptr(), r, k, k, 1, q.data_ptr(), sc.data_ptr(),
+                                              ws.data_ptr(), ws.numel() * 4, stream)
+        elif kind == "mxfp4":
+            q = torch.empty((r, k // 2), dtype=torch.uint8, device=dev)
+            sc = torch.empty((r, k // 32), dtype=torch.uint8, device=dev)
+            out_b, passes = r * k // 2 + r * k // 32, 1
+
+            def launch(i, stream):
+                return L.dsl_quant_mxfp4(x.data_ptr(), r, k, k, 1, q.data_ptr(), sc.data_ptr(),
+                                         stream)
+        else:
+            q = torch.empty((r, k // 2), dtype=torch.uint8, device=dev)
+            sc = torch.empty((r, k // 16), dtype=torch.uint8, device=dev)
+            g = torch.empty(1, dtype=torch.float32, device=dev)
+            out_b, passes = r * k // 2 + r * k // 16 + 4, 2
+
+            def launch(i, stream):
+                return L.dsl_quant_nvfp4(x.data_ptr(), r, k, k, 1, q.data_ptr(), sc.data_ptr(),
+                                         g.data_ptr(), ws.data_ptr(), ws.numel() * 4, stream)
+        nbytes = passes * 2 * r * k + out_b
+        return Case(name, 0.0, nbytes, PEAK_FP8_TFLOPS, "hbm", launch, 1,
+                    f"quantize {kind} [{r}, {k}] bf16 ({passes} read pass{'es' if passes > 1 else ''})")
+
     builders = {
         "fp8_block_m4096": lambda: fp8_case("fp8_block_m4096", 4096, 7168, 4096, True,
                                             W.activations(2, 4096, 4096, outliers=True),
@@ -181,6 +230,11 @@ def build_cases(names, dev):
         "nvfp4_m1": lambda: fp4_case("nvfp4_m1", 1, 14336, 4096, "nvfp4"),
         "nvfp4_m2048": lambda: fp4_case("nvfp4_m2048", 2048, 14336, 4096, "nvfp4"),
         "grouped_moe": lambda: grouped_case("grouped_moe"),
+        "quant_fp8_block128_w": lambda: quant_case("quant_fp8_block128_w", "fp8_block128", 7168, 4096),
+        "quant_fp8_row128_a": lambda: quant_case("quant_fp8_row128_a", "fp8_row128", 4096, 4096),
+        "quant_fp8_tensor_w": lambda: quant_case("quant_fp8_tensor_w", "fp8_tensor", 4096, 4096),
+        "quant_mxfp4_w": lambda: quant_case("quant_mxfp4_w", "mxfp4", 8192, 8192),
+        "quant_nvfp4_w": lambda: quant_case("quant_nvfp4_w", "nvfp4", 14336, 4096),
     }
     for nm in names:
         cases[nm] = builders[nm]()
@@ -189,7 +243,9 @@ def build_cases(names, dev):
 
 ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor_cfg1",
              "fp8_tensor_8192",
-             "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe"]
+             "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe",
+             "quant_fp8_block128_w", "quant_fp8_row128_a", "quant_fp8_tensor_w", "quant_mxfp4_w",
+             "quant_nvfp4_w"]
 
 
 def time_case(case, steps, warmup, dev, graph):
@@ -335,7 +391,7 @@ def main(argv=None):
         case = build_cases([nm], dev)[nm]
         graph = case.bound == "hbm"
         ms = time_case(case, args.steps, args.warmup, dev, graph=graph)
-        tflops = case.flops / (ms * 1e-3) / 1e12
+        tflops = case.flops / (ms * 1e-3) / 1e12 if case.flops else 0.0
         gbs = case.nbytes / (ms * 1e-3) / 1e9
         results[nm] = {"us": round(ms * 1e3, 2), "tflops": round(tflops, 1),
                        "frac_mfma": round(tflops / case.peak_tflops, 4),

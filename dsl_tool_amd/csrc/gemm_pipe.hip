@@ -1,5 +1,7 @@
 // Dense pipelined GEMM kernels for gfx950 (FP8 per-tensor, FP8 block-scaled,
 // MXFP4); the mainloop, DMA ring and LDS layout are described in pipe_core.h.
+#include <type_traits>
+
 #include "pipe_core.h"
 
 namespace dsl {
@@ -24,6 +26,29 @@ void gemm_pipe_kernel(const GemmArgs p) {
   if constexpr (GLOBAL) {
     s1 = *p.ga;
     s2 = *p.gb;
+  }
+  using Out = pipe::OutStage<Cfg::BM, Cfg::BN>;
+  if constexpr (Cfg::BM * Cfg::BN * 2 <= Cfg::LDS) {
+    if (!p.out_f32) {
+      // bf16: stage the tile in the idle ring, then write whole rows
+      uint16_t *stg = reinterpret_cast<uint16_t *>(smem);
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+        for (int j = 0; j < Cfg::TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int row = wm * Cfg::WM + i * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+            const int col = wn * Cfg::WN + j * 32 + r32;
+            float v = acc[i][j][r];
+            if constexpr (GLOBAL) v = (v * s1) * s2;
+            stg[Out::off(row, col)] = f32_to_bf16(v);
+          }
+      __syncthreads();
+      Out::template store<Cfg::NT>(p, m0, n0, stg);
+      return;
+    }
   }
 #pragma unroll
   for (int i = 0; i < Cfg::TM; ++i)
@@ -117,6 +142,26 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     }
   }
 
+  using Out = pipe::OutStage<Cfg::BM, Cfg::BN>;
+  if constexpr (Cfg::BM * Cfg::BN * 2 <= Cfg::LDS) {
+    if (!p.out_f32) {
+      uint16_t *stg = reinterpret_cast<uint16_t *>(smem);
+      __syncthreads();
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = wm * Cfg::WM + i * 16 + 4 * g + r;
+            const int col = wn * Cfg::WN + j * 16 + r16;
+            stg[Out::off(row, col)] = f32_to_bf16(acc[i][j][r]);
+          }
+      __syncthreads();
+      Out::template store<Cfg::NT>(p, m0, n0, stg);
+      return;
+    }
+  }
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -133,29 +178,287 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     }
 }
 
+// Block-scaled FP8 (1x128 activation groups, 128x128 weight blocks) on the
+// prefetch schedule: 64-byte stages, two per 128-K group, 32x32x64 MFMAs
+// with the operands swapped so that each lane owns one output row.  Instead
+// of a separate partial sum per group, the accumulator is kept in units of
+// the current group's scale s_g(m) = sa[m][g] * sb[n/128][g]: MFMAs add the
+// group's raw products, and at each group boundary the accumulator is
+// multiplied by s_g / s_g+1; the epilogue multiplies by the last group's
+// scale.  This equals the sum over groups of partial(g) * s_g of
+// cuda/gemm/fp8_gemm.cu:84-97 up to fp32 rounding.
+//
+// Activation scales sa[M][K/128] travel in their own LDS ring of two slots,
+// each holding one set of 4 groups for the tile's BM rows ([row][4 groups],
+// 16 bytes per row, so one 16-byte DMA per lane reads a row's 4 groups).
+// Wave 0 issues exactly one scale DMA with every stage: with stage s it
+// loads row block t = (s+6) % 8 (t < 4) of set (s+6) / 8, else a dummy copy
+// into a 1 KB scratch area, so its vmcnt count per stage stays fixed.  Set q
+// is first read in the step that consumes stage 8q-1 (whose wait covers all
+// loads issued with stages <= 8q) and its slot was last read in the step of
+// stage 8q-11 (before the step that issues stage 8q-6 with a 4-stage ring);
+// set 0 goes out before the prologue.  The weight scale of a wave's
+// 128-column block is picked per group with readlane from one VGPR.
+template <class Cfg>
+struct BlockScales {
+  static_assert(Cfg::NS <= 4, "the scale ring schedule assumes a ring of at most 4 stages");
+  uint32_t sa_lds;        // LDS address of the scale ring
+  int nsets;              // ceil(K/128 / 4)
+  DSL_DEV void init(const GemmArgs &p, uint32_t lds0) {
+    sa_lds = lds0 + Cfg::NS * Cfg::STAGE;
+    nsets = (p.K / 128 + 3) / 4;
+  }
+  // the scale DMA of row block t of set q (a dummy copy if t >= 4 or q is
+  // past the last set)
+  DSL_DEV void issue(const GemmArgs &p, int m0, int lane, int q, int t) const {
+    const int nkg = p.K / 128;
+    const bool real = t < 4 && q < nsets;
+    const int tb = real ? t : 0, qb = real ? q : 0;
+    int row = m0 + tb * 64 + lane;
+    row = row < p.M ? row : p.M - 1;
+    const float *src = static_cast<const float *>(p.sa) + (int64_t)row * nkg + qb * 4;
+    const uint32_t dst = real ? sa_lds + (uint32_t)((q & 1) * Cfg::SA_SET + t * 1024)
+                              : sa_lds + 2 * Cfg::SA_SET;
+    pipe::dma16(src, dst);
+  }
+  DSL_DEV void issue_for_stage(const GemmArgs &p, int m0, int lane, int s) const {
+    issue(p, m0, lane, (s + 6) >> 3, (s + 6) & 7);
+  }
+  // sa[row][g] from the ring (row within the tile)
+  static DSL_DEV float get(const uint8_t *smem, int row, int g) {
+    const float *ring = reinterpret_cast<const float *>(smem + Cfg::NS * Cfg::STAGE);
+    return ring[((g >> 2) & 1) * (Cfg::SA_SET / 4) + row * 4 + (g & 3)];
+  }
+};
+
+template <class Cfg, bool ISSUE>
+DSL_DEV void block_pf_step(int ks, int nks, bool rescale, int g_next, float sb_next,
+                           const GemmArgs &p, int m0, bool sa_wave, const BlockScales<Cfg> &bs,
+                           const pipe::Ring<Cfg> &ring, uint32_t lds0, const uint8_t *smem,
+                           const StageFrag<Cfg> &cur, StageFrag<Cfg> &nxt, int wm, int wn,
+                           int lane, float (&sc)[Cfg::TM], v16f (&acc)[Cfg::TM][Cfg::TN]) {
+  constexpr int NS = Cfg::NS, D = Cfg::D, TM = Cfg::TM, TN = Cfg::TN;
+  const int r32 = lane & 31, h = lane >> 5;
+  // wave 0 issues one scale DMA per stage on top of the ring's D; in the
+  // steady state (ISSUE) NS-2 stages follow stage ks+1, in the tail fewer
+  if constexpr (ISSUE) {
+    pipe::wait_stages_of<D + 1, NS - 2>(NS - 2, sa_wave);
+  } else {
+    const int last = (ks + NS - 1 < nks - 1) ? ks + NS - 1 : nks - 1;
+    pipe::wait_stages_of<D + 1, NS - 2>(last - (ks + 1), sa_wave);
+  }
+  pipe::wait_lds();
+  __syncthreads();
+  const uint8_t *stn = smem + ((ks + 1) % NS) * Cfg::STAGE;
+  nxt.f[0].load_b(stn, 0, wn, r32, h);
+  float sn[TM];
+  if (rescale) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      sn[i] = BlockScales<Cfg>::get(smem, wm * Cfg::WM + i * 32 + r32, g_next) * sb_next;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  float rt[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    cur.f[0].mma_row_t(i, acc);
+    if constexpr (ISSUE) {
+      if (i == 0 && sa_wave) bs.issue_for_stage(p, m0, lane, ks + NS);
+#pragma unroll
+      for (int j = i * D / TM; j < (i + 1) * D / TM; ++j) ring.issue_one(j, ks + NS, lds0);
+    }
+    nxt.f[0].load_a(stn, 0, i, wm, r32, h);
+    if (rescale) {
+      if (i == 1) {
+#pragma unroll
+        for (int t = 0; t < TM; ++t) {
+          rt[t] = sc[t] * __builtin_amdgcn_rcpf(sn[t]);
+          sc[t] = sn[t];
+        }
+      }
+      // row i-1 has had its last MFMA of the group issued one row ago
+      if (i >= 1) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i - 1][j] *= rt[i - 1];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (rescale) {
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[TM - 1][j] *= rt[TM - 1];
+  }
+}
+
+// Preconditions (checked by the launcher): K % 512 == 0, K / 128 <=
+// kBlockPfMaxGroups, sa 16-byte aligned.
+constexpr int kBlockPfMaxGroups = 512;
+
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT) __attribute__((amdgpu_waves_per_eu(Cfg::OCC, Cfg::OCC)))
+void gemm_pipe_block_pf_kernel(const GemmArgs p) {
+  static_assert(Cfg::BLOCK && Cfg::PF && Cfg::SKB == 64 && Cfg::KSTEPS == 1, "block prefetch cfg");
+  static_assert(Cfg::TM >= 2 && Cfg::WN <= 128 && 128 % Cfg::WN == 0, "block-scale tiling");
+  static_assert(Cfg::SC_DMA == 0 && Cfg::BM == 4 * 64, "scale ring: four 64-row blocks");
+  constexpr int NS = Cfg::NS, D = Cfg::D, TM = Cfg::TM, TN = Cfg::TN;
+  __shared__ __align__(16) uint8_t smem[Cfg::LDS];
+  const int nbm = (p.M + Cfg::BM - 1) / Cfg::BM, nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
+  int tmi, tni;
+  tile_coords(blockIdx.x, nbm, nbn, tmi, tni);
+  const int m0 = tmi * Cfg::BM, n0 = tni * Cfg::BN;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+  const int r32 = lane & 31, h = lane >> 5;
+  const bool sa_wave = wave == 0;
+  const uint32_t lds0 = pipe::lds_addr(smem);
+  pipe::Ring<Cfg> ring;
+  ring.init(p, m0, n0, wave, lane);
+  BlockScales<Cfg> bs;
+  bs.init(p, lds0);
+  const int nks = p.Kb / Cfg::SKB, nkg = p.K / 128;   // nks even, >= 2
+  int sbrow = (n0 + wn * Cfg::WN) / 128;
+  const int sblim = (p.N + 127) / 128 - 1;
+  sbrow = sbrow > sblim ? sblim : sbrow;
+  // Weight scales of the tile's 128-column blocks go to LDS once, before
+  // the first DMA: a global load inside the loop would be a vector load
+  // (the DMA asm may write memory, so the compiler does not use the scalar
+  // cache), and waiting for it would also drain the DMA ring.
+  constexpr int NBB = Cfg::BN / 128 > 0 ? Cfg::BN / 128 : 1;
+  __shared__ float sb_lds[NBB][kBlockPfMaxGroups];
+  {
+    const int nb0 = n0 / 128;
+    for (int idx = threadIdx.x; idx < NBB * nkg; idx += Cfg::NT) {
+      const int b = idx / nkg, g = idx - b * nkg;
+      const int row = nb0 + b < sblim ? nb0 + b : sblim;
+      sb_lds[b][g] = static_cast<const float *>(p.sb)[(int64_t)row * nkg + g];
+    }
+  }
+  const float *sbw = sb_lds[sbrow - n0 / 128 < NBB ? sbrow - n0 / 128 : NBB - 1];
+  auto sb_of = [&](int g) { return sbw[g]; };
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // prologue: scale set 0, then stages 0..NS-1 (each with its scale DMA)
+  if (sa_wave) {
+#pragma unroll
+    for (int t = 0; t < 4; ++t) bs.issue(p, m0, lane, 0, t);
+  }
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    if (s < nks) {
+      if (sa_wave) bs.issue_for_stage(p, m0, lane, s);
+      ring.issue(s, lds0);
+    }
+  pipe::wait_stages_of<D + 1, NS - 1>((nks < NS ? nks : NS) - 1, sa_wave);
+  __syncthreads();
+  StageFrag<Cfg> f0, f1;
+  f0.load(smem, wm, wn, r32, h);
+  float sc[TM];   // s_g(row) of the group the accumulator is expressed in
+  {
+    const float sb0 = sb_of(0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+      sc[i] = BlockScales<Cfg>::get(smem, wm * Cfg::WM + i * 32 + r32, 0) * sb0;
+  }
+  // one pair of steps per group: the second step moves to the next group.
+  // NS and nks are even, so both steps of a pair either issue their next
+  // stage (steady state) or not (tail); keeping that a compile-time choice
+  // leaves no branch between the MFMAs and the rescale that follows them.
+  static_assert(NS % 2 == 0, "pairs of steps agree on issuing");
+  auto pair = [&](auto issue_tag, int ks) {
+    constexpr bool ISSUE = decltype(issue_tag)::value;
+    const int gn = ks / 2 + 1;
+    const float sb_next = sb_of(gn);
+    block_pf_step<Cfg, ISSUE>(ks, nks, false, 0, 0.f, p, m0, sa_wave, bs, ring, lds0, smem, f0,
+                              f1, wm, wn, lane, sc, acc);
+    block_pf_step<Cfg, ISSUE>(ks + 1, nks, true, gn, sb_next, p, m0, sa_wave, bs, ring, lds0,
+                              smem, f1, f0, wm, wn, lane, sc, acc);
+  };
+  int ks = 0;
+  for (; ks + NS < nks && ks + 2 < nks; ks += 2) pair(std::true_type{}, ks);
+  for (; ks + 2 < nks; ks += 2) pair(std::false_type{}, ks);
+  block_pf_step<Cfg, false>(ks, nks, false, 0, 0.f, p, m0, sa_wave, bs, ring, lds0, smem, f0, f1,
+                            wm, wn, lane, sc, acc);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) f1.f[0].mma_row_t(i, acc);
+
+  using Out = pipe::OutStage<Cfg::BM, Cfg::BN>;
+  if (!p.out_f32) {
+    uint16_t *stg = reinterpret_cast<uint16_t *>(smem);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int row = wm * Cfg::WM + i * 32 + r32;
+          const int col = wn * Cfg::WN + j * 32 + 8 * q + 4 * h;
+          const uint32_t lo = (uint32_t)f32_to_bf16(acc[i][j][4 * q] * sc[i]) |
+                              ((uint32_t)f32_to_bf16(acc[i][j][4 * q + 1] * sc[i]) << 16);
+          const uint32_t hi = (uint32_t)f32_to_bf16(acc[i][j][4 * q + 2] * sc[i]) |
+                              ((uint32_t)f32_to_bf16(acc[i][j][4 * q + 3] * sc[i]) << 16);
+          *reinterpret_cast<uint2 *>(stg + Out::off(row, col)) = make_uint2(lo, hi);
+        }
+    __syncthreads();
+    Out::template store<Cfg::NT>(p, m0, n0, stg);
+    return;
+  }
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int row = m0 + wm * Cfg::WM + i * 32 + r32;
+    if (row >= p.M) continue;
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int col = n0 + wn * Cfg::WN + j * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+        if (col < p.N) static_cast<float *>(p.c)[(int64_t)row * p.ldc + col] = acc[i][j][r] * sc[i];
+      }
+  }
+}
+
 template <class Cfg>
 static hipError_t launch_pipe_cfg(const GemmArgs &p, hipStream_t st) {
   const int tiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * ((p.N + Cfg::BN - 1) / Cfg::BN);
-  if constexpr (Cfg::BLOCK) gemm_pipe_block_kernel<Cfg><<<tiles, Cfg::NT, 0, st>>>(p);
+  if constexpr (Cfg::BLOCK && Cfg::PF) gemm_pipe_block_pf_kernel<Cfg><<<tiles, Cfg::NT, 0, st>>>(p);
+  else if constexpr (Cfg::BLOCK) gemm_pipe_block_kernel<Cfg><<<tiles, Cfg::NT, 0, st>>>(p);
   else gemm_pipe_kernel<Cfg><<<tiles, Cfg::NT, 0, st>>>(p);
   return hipGetLastError();
 }
 
-// Dense FP8 (per-tensor) / MXFP4 GEMM through the LDS-DMA pipeline.
-// Preconditions (checked by the caller): Kb % 128 == 0, mode FP8_TENSOR,
-// FP8_BLOCK or MXFP4, ksplit == 1, 4-byte aligned scales.
+// Dense FP8 (per-tensor, block-scaled), MXFP4 and NVFP4 GEMM through the
+// LDS-DMA pipeline.  Preconditions (checked by the caller): Kb % 128 == 0,
+// ksplit == 1, 4-byte aligned scales.  Variant 0 is the default for large
+// grids, 1 the 128x128 tile for mid-sized ones; the others are kept as
+// alternatives for tuning (DSL_GEMM_PIPE).
 hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_t st) {
   if (mode == MODE_FP8_BLOCK) {
+    const bool ring_ok = p.K % 512 == 0 && p.K / 128 <= kBlockPfMaxGroups &&
+                         (reinterpret_cast<uintptr_t>(p.sa) & 15) == 0;
     switch (variant) {
-      case 0: return launch_pipe_cfg<PipeCfg<MODE_FP8_BLOCK, 256, 256, 2, 4, 2, 128>>(p, st);
+      case 0:
+        // prefetch kernel with the activation-scale ring: K % 512 == 0, at
+        // most kBlockPfMaxGroups groups, 16-byte aligned sa
+        if (ring_ok)
+          return launch_pipe_cfg<PipeCfg<MODE_FP8_BLOCK, 256, 256, 2, 4, 4, 64, 0, 1>>(p, st);
+        return launch_pipe_cfg<PipeCfg<MODE_FP8_BLOCK, 256, 256, 2, 4, 2, 128>>(p, st);
       case 2: return launch_pipe_cfg<PipeCfg<MODE_FP8_BLOCK, 256, 256, 4, 2, 2, 128>>(p, st);
+      case 3: return launch_pipe_cfg<PipeCfg<MODE_FP8_BLOCK, 256, 256, 2, 4, 2, 128>>(p, st);
       default: return launch_pipe_cfg<PipeCfg<MODE_FP8_BLOCK, 128, 128, 2, 2, 2, 128, 2>>(p, st);
     }
   }
   if (mode == MODE_FP8_TENSOR) {
     switch (variant) {
-      case 0: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 256, 2, 4, 4, 64>>(p, st);
-      case 2: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 256, 2, 4, 2, 128>>(p, st);
+      case 0: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 256, 2, 4, 4, 64, 0, 1>>(p, st);
+      case 2: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 256, 2, 4, 4, 64>>(p, st);
       case 3: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 128, 4, 2, 3, 128>>(p, st);
       default: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 128, 128, 2, 2, 4, 64>>(p, st);
     }

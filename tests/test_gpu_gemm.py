@@ -222,6 +222,41 @@ def test_fp8_block_pipelined(m, n, k):
     assert_close(c, ref, what=f"fp8 block pipelined {m}x{n}x{k}")
 
 
+# K % 512 == 0: the block-scaled kernel with the activation-scale ring (two
+# slots of four 128-K groups), over 2, 3 and 9 scale sets, ragged M/N.
+BLOCK_RING_SHAPES = [(4096, 3840, 1024), (4000, 4100, 1536), (3840, 4096, 4608)]
+
+
+@pytest.mark.parametrize("m,n,k", BLOCK_RING_SHAPES)
+def test_fp8_block_scale_ring(m, n, k):
+    a = W.activations(3, m, k, outliers=True)
+    w = W.randn_bf16((n, k), 213, 0.02)
+    qa, sa = Q.quant_fp8_blocks(a.to(DEV), 1, 128)
+    qw, sw = Q.quant_fp8_blocks(w.to(DEV), 128, 128)
+    c = G.fp8_gemm_packed(qa, qw, sa, sw, block=True)
+    ref = OG.ref_fp8_groupwise(np_u8(qa), np_f32(sa), np_u8(qw), np_f32(sw))
+    assert_close(c, ref, what=f"fp8 block scale ring {m}x{n}x{k}")
+
+
+def test_fp8_block_zero_groups():
+    """All-zero activation groups get the scale floor (1e-12): the kernel's
+    per-group accumulator rescaling then moves through ratios of ~1e10 and
+    back, and must still match the group-sum oracle."""
+    m, n, k = 4096, 3840, 2048
+    a = W.activations(4, m, k, outliers=False)
+    a[::3, 256:384] = 0          # group 2 of every third row
+    a[1::7, 1024:1152] = 0       # group 8 of every seventh row
+    a[:5, :] = 0                 # whole rows
+    w = W.randn_bf16((n, k), 214, 0.02)
+    qa, sa = Q.quant_fp8_blocks(a.to(DEV), 1, 128)
+    qw, sw = Q.quant_fp8_blocks(w.to(DEV), 128, 128)
+    assert float(sa.min()) == pytest.approx(1e-12)
+    c = G.fp8_gemm_packed(qa, qw, sa, sw, block=True)
+    ref = OG.ref_fp8_groupwise(np_u8(qa), np_f32(sa), np_u8(qw), np_f32(sw))
+    assert_close(c, ref, what="fp8 block zero groups")
+    assert torch.count_nonzero(c[:5]) == 0
+
+
 def _e4m3_values(codes):
     c = codes.astype(np.int64)
     s = np.where(c & 0x80, -1.0, 1.0)
