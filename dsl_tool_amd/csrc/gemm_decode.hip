@@ -1,38 +1,61 @@
-// Skinny-M ("decode") quantized GEMM for gfx950: C[M,N] = A[M,K] . W[N,K]^T
-// with M <= 32, bound by streaming W from HBM.
+// Skinny-M ("decode") quantized GEMMs for gfx950: C[M,N] = A[M,K] . W[N,K]^T
+// with few activation rows, bound by streaming W from HBM.
 //
-// One workgroup owns 16 rows of W (one MFMA tile of output columns) over
-// the whole of K; its NW waves split K into contiguous ranges.  Each wave
-// copies its 16 rows x K-range slab of W into a private LDS region with
-// direct-to-LDS loads (one instruction = one row's next 1 KB, i.e. eight
-// whole 128-byte lines, so every line is requested once and the copy runs
-// at streaming efficiency), loads its activation fragments straight into
-// registers (A is tiny and L2-resident), waits for its own loads only, and
-// runs the MFMAs from LDS.  The waves' partial tiles are summed through LDS
-// and written as bf16 / fp32 by the workgroup: one launch, no workspace, no
-// atomics.  A K-range longer than one LDS chunk is processed chunk by chunk.
+// gemm_decode_kernel (FP8 per-tensor, FP8 1x128/128x128 block, MXFP4; M <= 32)
+//   One workgroup owns 32 rows of W (two 16-row MFMA tiles) over the whole
+//   of K; its four waves split K into contiguous ranges of whole 1 KB chunks
+//   (1 KB of every row: 1024 FP8 or 2048 FP4 elements).  A wave streams a
+//   sequence of "items" through two LDS regions: for each of its chunks, the
+//   activation tiles (16 rows x 1 KB each) and then the two W tiles.  Each
+//   item is 16 direct-to-LDS loads (one row's 1 KB per instruction, i.e.
+//   eight whole 128-byte lines) plus, for block-scaled FP8 and MXFP4, one
+//   more load of the item's scales.  Item i goes into region i % 2 as soon
+//   as item i-2 has left it, so two items (32 KB) are always in flight per
+//   wave and every wave waits for its own loads only (no barrier until the
+//   final reduction).  Activation tiles are moved into registers and reused
+//   for both W tiles, which halves the activation traffic of a 16-row
+//   layout; W loads carry the non-temporal hint so the stream of W lines
+//   does not evict the activations from L2.  The waves' partial tiles are
+//   summed through LDS: one launch, no workspace, no atomics.
 //
-// MFMA: v_mfma_scale_f32_16x16x128_f8f6f4.  Lane l supplies row l%16 of its
-// operand; lane group g = l/16 supplies a quarter of the step's K.  Output
-// register i of lane l is C[4*g + i][l%16].
-//   FP8 tensor / block: group g holds the 16-byte chunks g and 4+g of the
-//     step's 128 K bytes (the same K order for A and W, so the sum is
-//     unchanged; for block scales the step is exactly one 128-K scale group),
-//     so each activation load instruction reads 64 contiguous bytes per row.
-//   MXFP4: K is taken in 512-element superblocks of 4 steps; at step j of a
-//     superblock group g holds the 32-element block 4g+j, so a lane's data
-//     for the superblock is 64 contiguous bytes and its 4 E8M0 scale bytes
-//     are one aligned u32 (opsel j picks the byte).  A and W use the same
-//     permutation of K, which leaves every block paired with its own scale.
-// LDS slab: row r's 16-byte chunk c lives in slot c ^ r (r < 16), so the 16
-// lanes reading one logical chunk of the 16 rows hit 16 distinct bank groups.
+//   MFMA: v_mfma_scale_f32_16x16x128_f8f6f4.  Lane l supplies row l%16 of
+//   its operand; lane group g = l/16 supplies a quarter of the step's K.
+//   Output register i of lane l is C[4*g + i][l%16] (rows: activations,
+//   columns: W rows).
+//     FP8 tensor / block: a step is 128 K bytes; group g holds the 16-byte
+//       chunks g and 4+g of the step (the same K order for A and W, so the
+//       sum is unchanged; for block scales a step is exactly one 128-K scale
+//       group, folded as acc += part * sa[m][grp] * sb[n/128][grp], the
+//       group-partial form of cuda/gemm/fp8_gemm.cu:84-97).
+//     MXFP4: K is taken in 512-element superblocks of 4 steps; at step j of
+//       a superblock group g holds the 32-element block 4g+j, so a lane's data
+//       for the superblock is 64 contiguous bytes and its 4 E8M0 scale bytes
+//       are one aligned u32 (opsel j picks the byte).  A and W use the same
+//       permutation of K, which leaves every block paired with its own scale.
+//   LDS: row r's 16-byte chunk c lives in slot c ^ r (r < 16), so the 16
+//   lanes reading one logical chunk of the 16 rows hit 16 distinct bank
+//   groups.
+//
+// gemv_nvfp4_kernel (NVFP4, M <= 4)
+//   One wave owns RPW consecutive W rows over all of K.  Lane l holds bytes
+//   [16l, 16l+16) of every 1 KB chunk of a row (32 E2M1 codes = two 16-element
+//   E4M3 blocks), so each load instruction reads one row's 1 KB
+//   contiguously.  The E4M3 scales of the wave's rows are contiguous in
+//   memory and arrive in LDS by 1 KB direct loads (a 2-byte load per lane
+//   would cost a whole instruction per 128 bytes); the activations and their
+//   scales are loaded once per workgroup into LDS and dequantized exactly to
+//   fp16 (E2M1 x E4M3 has at most 5 significant bits), held in registers for
+//   all of K.  W codes are converted to fp16 with unit scale and multiplied
+//   by fp16 dot products with fp32 accumulation per 16-element block; each
+//   block's E4M3 scale (hardware OCP E4M3 -> f32 conversion, exact) applies
+//   once per block.  Each row's 64 lane partials are summed across the wave;
+//   the fp32 global scales apply last, as in the dense NVFP4 kernel.
+#include <type_traits>
+#include <utility>
+
 #include "gemm_core.h"
 
 #pragma clang diagnostic ignored "-Winline-asm"
-
-#ifndef DSL_DECODE_TN
-#define DSL_DECODE_TN 1
-#endif
 
 namespace dsl {
 
@@ -48,176 +71,223 @@ DSL_DEV void dma16(const void *src, uint32_t lds) {
                "s"(lds)
                : "memory", "m0");
 }
+// Same, with the non-temporal hint (streamed data, read once).
+DSL_DEV void dma16_nt(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src),
+               "s"(lds)
+               : "memory", "m0");
+}
+// s_waitcnt vmcnt(N) / lgkmcnt(0) as compiler memory barriers: LDS reads of
+// a region may not move above the wait for its loads, nor DMA into a region
+// above the wait for its reads.
+template <int N>
+DSL_DEV void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+DSL_DEV void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+// f(integral_constant<int, K>) for K = B .. E-1, in order
+template <int B, int E, class F>
+DSL_DEV void static_for(F &&f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 }  // namespace dec
 
-template <int MODE_, int TMA_, int NW_, int TN_ = 1>
+template <int MODE_, int TMA_>
 struct DecodeCfg {
   static constexpr int MODE = MODE_;
-  static constexpr int TMA = TMA_;       // 16-row activation tiles (M <= 16*TMA)
-  static constexpr int TN = TN_;         // 16-row W tiles per workgroup (and per wave)
-  static constexpr int NW = NW_, NT = NW * 64;
+  static constexpr int TMA = TMA_;                  // 16-row activation tiles (M <= 16*TMA)
+  static constexpr int TN = 2;                      // 16-row W tiles per workgroup
+  static constexpr int NW = 4, NT = NW * 64;        // waves split K
   static constexpr bool MX = MODE == MODE_MXFP4;
-  static constexpr int STEP_BYTES = MX ? 64 : 128;    // bytes of one W row per MFMA step
-  static constexpr int CHUNK = 1024;                  // W bytes per row per LDS chunk
-  static constexpr int CSTEPS = CHUNK / STEP_BYTES;   // MFMA steps per chunk
-  static constexpr int SLAB = TN * (16 * CHUNK + (MX ? 16 * (CHUNK / 16) : 0));   // + E8M0
+  static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;
+  static constexpr int CHUNK = 1024;                // bytes of one row per item
+  static constexpr int AUX = (MX || BLOCK) ? 1024 : 0;   // scale bytes per item (DMA target)
+  static constexpr int DPI = 16 + (AUX ? 1 : 0);    // DMA instructions per item
+  static constexpr int REGION = 16 * CHUNK + AUX;
+  static constexpr int P = TMA + TN;                // items per chunk
+  static_assert(2 * NW * REGION + NW * TN * TMA * 1024 <= 160 * 1024, "LDS budget");
+};
+
+// Register state of one wave: activation fragments of the current chunk,
+// their block scales, and the accumulators.
+template <class Cfg>
+struct DecodeRegs {
+  static constexpr int TMA = Cfg::TMA;
+  v8i af[TMA][8];               // FP8: 8 steps of 32 bytes per lane
+  v4f sa[TMA][8];               // FP8 block: sa[4g+i][group] of the 8 groups
+  v4i ad[TMA][4][4];            // MXFP4: 4 superblocks x 4 steps of 16 bytes
+  int as[TMA][4];               // MXFP4: E8M0 u32 per superblock
+  v4f acc[Cfg::TN][TMA];
 };
 
 template <class Cfg>
 __global__ __launch_bounds__(Cfg::NT) void gemm_decode_kernel(const GemmArgs p) {
-  constexpr int TMA = Cfg::TMA, NW = Cfg::NW, CHUNK = Cfg::CHUNK, CSTEPS = Cfg::CSTEPS;
-  constexpr int TN = Cfg::TN;
-  constexpr int TSLAB = Cfg::SLAB / TN;  // one 16-row tile's slab
-  __shared__ __align__(16) uint8_t slab[NW][Cfg::SLAB];
+  constexpr int TMA = Cfg::TMA, TN = Cfg::TN, NW = Cfg::NW, P = Cfg::P, DPI = Cfg::DPI;
+  constexpr int CHUNK = Cfg::CHUNK;
+  __shared__ __align__(16) uint8_t region[NW][2][Cfg::REGION];
   __shared__ __align__(16) float red[NW][TN][TMA][64][4];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, g = lane >> 4;
   const int nb0 = blockIdx.x * 16 * TN;
-
-  // contiguous K-range of this wave, in whole chunks
   const int nchunks = p.Kb / CHUNK;
-  const int c_begin = (int)((int64_t)nchunks * wave / NW);
-  const int c_end = (int)((int64_t)nchunks * (wave + 1) / NW);
+  const int c_begin = nchunks * wave / NW, c_end = nchunks * (wave + 1) / NW;
+  const int nitems = (c_end - c_begin) * P;
+  const uint32_t R0 = dec::lds_addr(region[wave][0]), R1 = dec::lds_addr(region[wave][1]);
+  const int nkg = p.K / 128;              // FP8 block: scale groups per row
+  const int64_t sld = p.K / 32;           // MXFP4: E8M0 bytes per row
 
-  uint8_t *ws = slab[wave];
-  const uint32_t ws_lds = dec::lds_addr(ws);
-  const int64_t sld = p.K / 32;          // E8M0 bytes per row (MX)
-
-  v4f acc_all[TN][TMA];
+  // item it: chunk c_begin + it / P; kind it % P (< TMA: activation tile,
+  // else W tile kind - TMA); region it % 2
+  auto issue = [&](int it) {
+    const int ch = c_begin + it / P, kind = it % P;
+    const uint32_t dst = (it & 1) ? R1 : R0;
+    const int64_t kb0 = (int64_t)ch * CHUNK;
+    const bool isA = kind < TMA;
+    const int rbase = isA ? kind * 16 : nb0 + (kind - TMA) * 16;
+    const int rlim = isA ? p.M - 1 : p.N - 1;
+    const uint8_t *src = isA ? p.a : p.b;
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-    for (int t = 0; t < TMA; ++t) acc_all[tn][t] = (v4f){0.f, 0.f, 0.f, 0.f};
-
-  for (int ch = c_begin; ch < c_end; ++ch) {
-    const int64_t kb0 = (int64_t)ch * CHUNK;           // first W byte of the chunk
-    // ---- W slabs: TN x 16 rows x CHUNK bytes (+ MX scales), swizzled
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int nrow = min(nb0 + tn * 16 + r, p.N - 1);   // rows past N re-read the last row
-        const int c = lane ^ r;                          // logical chunk stored in slot `lane`
-        dec::dma16(p.b + (int64_t)nrow * p.Kb + kb0 + c * 16, ws_lds + tn * TSLAB + r * CHUNK);
-      }
-      if constexpr (Cfg::MX) {
-        // CHUNK*2 elements / 32 = 64 scale bytes per row: lane -> row lane/4, 16 bytes lane%4
-        const int nrow = min(nb0 + tn * 16 + (lane >> 2), p.N - 1);
-        dec::dma16(static_cast<const uint8_t *>(p.sb) + (int64_t)nrow * sld + kb0 / 16 +
-                       (lane & 3) * 16,
-                   ws_lds + tn * TSLAB + 16 * CHUNK);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int row = min(rbase + r, rlim);          // rows past the edge re-read the last row
+      const uint8_t *s = src + (int64_t)row * p.Kb + kb0 + ((lane ^ r) << 4);
+      if (isA) dec::dma16(s, dst + r * CHUNK);
+      else dec::dma16_nt(s, dst + r * CHUNK);
     }
+    if constexpr (Cfg::MX) {
+      // 16 rows x 64 E8M0 bytes: lane -> row lane/4, 16 bytes lane%4
+      const int row = min(rbase + (lane >> 2), rlim);
+      const uint8_t *sc = static_cast<const uint8_t *>(isA ? p.sa : p.sb);
+      dec::dma16(sc + row * sld + kb0 / 16 + ((lane & 3) << 4), dst + 16 * CHUNK);
+    } else if constexpr (Cfg::BLOCK) {
+      // activation tile: sa[row][8 groups of the chunk], 32 bytes per row
+      // (lanes 32..63 repeat lanes 0..31); W tile: sb[n/128][8 groups]
+      const float *sc;
+      if (isA) {
+        const int row = min(rbase + ((lane >> 1) & 15), rlim);
+        sc = static_cast<const float *>(p.sa) + (int64_t)row * nkg;
+      } else {
+        const int sbrow = min(nb0, p.N - 1) / 128;   // both W tiles lie in one 128-row block
+        sc = static_cast<const float *>(p.sb) + (int64_t)sbrow * nkg;
+      }
+      dec::dma16(sc + ch * 8 + ((lane & 1) << 2), dst + 16 * CHUNK);
+    }
+  };
 
-    // ---- activation fragments for the chunk, straight into registers
-    if constexpr (!Cfg::MX) {
-      v8i af[CSTEPS][TMA];
+  DecodeRegs<Cfg> st;
 #pragma unroll
-      for (int s = 0; s < CSTEPS; ++s)
+  for (int t = 0; t < TN; ++t)
 #pragma unroll
-        for (int t = 0; t < TMA; ++t) {
-          const uint8_t *ap = p.a + (int64_t)min(t * 16 + r16, p.M - 1) * p.Kb + kb0 + s * 128 +
-                              g * 16;
-          const v4i lo = reinterpret_cast<const v4i *>(ap)[0];
-          const v4i hi = reinterpret_cast<const v4i *>(ap)[4];
-          af[s][t] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    for (int a = 0; a < TMA; ++a) st.acc[t][a] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  auto chunk16 = [&](const uint8_t *base, int c) {      // row r16's logical chunk c
+    return *reinterpret_cast<const v4i *>(base + r16 * CHUNK + ((c ^ r16) << 4));
+  };
+
+  // consume item of kind KIND from `base`
+  auto consume = [&](auto kind_tag, const uint8_t *base) {
+    constexpr int KIND = decltype(kind_tag)::value;
+    const uint8_t *aux = base + 16 * CHUNK;
+    if constexpr (KIND < TMA) {
+      if constexpr (Cfg::MX) {
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) st.ad[KIND][b][j] = chunk16(base, b * 16 + 4 * g + j);
+          st.as[KIND][b] = *reinterpret_cast<const int *>(aux + r16 * 64 + b * 16 + g * 4);
         }
-      float sbv[TN][CSTEPS];
-      v4f sa4[CSTEPS][TMA];
-      if constexpr (Cfg::MODE == MODE_FP8_BLOCK) {
-        const int nkg = p.K / 128, kg0 = (int)(kb0 / 128);
+      } else {
 #pragma unroll
-        for (int tn = 0; tn < TN; ++tn) {
-          const int sbrow = min(nb0 + tn * 16, p.N - 1) / 128;
-          const float *sbp = static_cast<const float *>(p.sb) + (int64_t)sbrow * nkg + kg0;
-#pragma unroll
-          for (int s = 0; s < CSTEPS; ++s) sbv[tn][s] = sbp[s];
+        for (int s = 0; s < 8; ++s) {
+          const v4i lo = chunk16(base, s * 8 + g), hi = chunk16(base, s * 8 + g + 4);
+          st.af[KIND][s] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
-        const float *sa = static_cast<const float *>(p.sa);
-#pragma unroll
-        for (int t = 0; t < TMA; ++t)
+        if constexpr (Cfg::BLOCK) {
+          const float *sa = reinterpret_cast<const float *>(aux);   // [16 rows][8 groups]
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float *rp = sa + (int64_t)min(t * 16 + 4 * g + i, p.M - 1) * nkg + kg0;
+            const v4f q0 = *reinterpret_cast<const v4f *>(sa + (4 * g + i) * 8);
+            const v4f q1 = *reinterpret_cast<const v4f *>(sa + (4 * g + i) * 8 + 4);
 #pragma unroll
-            for (int s = 0; s < CSTEPS; ++s) sa4[s][t][i] = rp[s];
-          }
-      }
-      __builtin_amdgcn_s_waitcnt(0);                   // this wave's DMA and loads
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const uint8_t *wt = ws + tn * TSLAB;
-        v4f (&acc)[TMA] = acc_all[tn];
-#pragma unroll
-        for (int s = 0; s < CSTEPS; ++s) {
-          const int c0 = s * 8 + g;
-          const v4i lo = *reinterpret_cast<const v4i *>(wt + r16 * CHUNK + ((c0 ^ r16) << 4));
-          const v4i hi = *reinterpret_cast<const v4i *>(wt + r16 * CHUNK + (((c0 + 4) ^ r16) << 4));
-          const v8i wf = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-#pragma unroll
-          for (int t = 0; t < TMA; ++t) {
-            if constexpr (Cfg::MODE == MODE_FP8_TENSOR) {
-              acc[t] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[s][t], wf, acc[t], 0,
-                                                                        0, 0, 0, 0, 0);
-            } else {
-              const v4f zero = {0.f, 0.f, 0.f, 0.f};
-              const v4f part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af[s][t], wf,
-                                                                                zero, 0, 0, 0,
-                                                                                0, 0, 0);
-              acc[t] = part * (sa4[s][t] * sbv[tn][s]) + acc[t];
+            for (int s = 0; s < 4; ++s) {
+              st.sa[KIND][s][i] = q0[s];
+              st.sa[KIND][s + 4][i] = q1[s];
             }
           }
         }
       }
     } else {
-      constexpr int NSB = CSTEPS / 4;                  // superblocks per chunk
-      v4i ad[NSB][TMA][4];
-      int as[NSB][TMA];
+      constexpr int T = KIND - TMA;
+      if constexpr (Cfg::MX) {
 #pragma unroll
-      for (int b = 0; b < NSB; ++b)
-#pragma unroll
-        for (int t = 0; t < TMA; ++t) {
-          const int arow = min(t * 16 + r16, p.M - 1);
-          const v4i *ap = reinterpret_cast<const v4i *>(p.a + (int64_t)arow * p.Kb + kb0 +
-                                                        b * 256 + g * 64);
-#pragma unroll
-          for (int j = 0; j < 4; ++j) ad[b][t][j] = ap[j];
-          as[b][t] = *reinterpret_cast<const int *>(static_cast<const uint8_t *>(p.sa) +
-                                                    (int64_t)arow * sld + kb0 / 16 + b * 16 + g * 4);
-        }
-      __builtin_amdgcn_s_waitcnt(0);
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const uint8_t *wt = ws + tn * TSLAB;
-        const uint8_t *wsc = wt + 16 * CHUNK;
-        v4f (&acc)[TMA] = acc_all[tn];
-#pragma unroll
-        for (int b = 0; b < NSB; ++b) {
-          const int wsv = *reinterpret_cast<const int *>(wsc + r16 * 64 + b * 16 + g * 4);
+        for (int b = 0; b < 4; ++b) {
+          const int wsv = *reinterpret_cast<const int *>(aux + r16 * 64 + b * 16 + g * 4);
           v4i wd[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j)
-            wd[j] = *reinterpret_cast<const v4i *>(wt + r16 * CHUNK +
-                                                   (((b * 16 + 4 * g + j) ^ r16) << 4));
+          for (int j = 0; j < 4; ++j) wd[j] = chunk16(base, b * 16 + 4 * g + j);
 #pragma unroll
-          for (int t = 0; t < TMA; ++t) {
-            acc[t] = mfma_mx<0>(ad[b][t][0], wd[0], acc[t], as[b][t], wsv);
-            acc[t] = mfma_mx<1>(ad[b][t][1], wd[1], acc[t], as[b][t], wsv);
-            acc[t] = mfma_mx<2>(ad[b][t][2], wd[2], acc[t], as[b][t], wsv);
-            acc[t] = mfma_mx<3>(ad[b][t][3], wd[3], acc[t], as[b][t], wsv);
+          for (int a = 0; a < TMA; ++a) {
+            st.acc[T][a] = mfma_mx<0>(st.ad[a][b][0], wd[0], st.acc[T][a], st.as[a][b], wsv);
+            st.acc[T][a] = mfma_mx<1>(st.ad[a][b][1], wd[1], st.acc[T][a], st.as[a][b], wsv);
+            st.acc[T][a] = mfma_mx<2>(st.ad[a][b][2], wd[2], st.acc[T][a], st.as[a][b], wsv);
+            st.acc[T][a] = mfma_mx<3>(st.ad[a][b][3], wd[3], st.acc[T][a], st.as[a][b], wsv);
+          }
+        }
+      } else {
+        v4f sb0, sb1;
+        if constexpr (Cfg::BLOCK) {
+          sb0 = *reinterpret_cast<const v4f *>(aux);
+          sb1 = *reinterpret_cast<const v4f *>(aux + 16);
+        }
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const v4i lo = chunk16(base, s * 8 + g), hi = chunk16(base, s * 8 + g + 4);
+          const v8i wf = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+          for (int a = 0; a < TMA; ++a) {
+            if constexpr (Cfg::BLOCK) {
+              const v4f zero = {0.f, 0.f, 0.f, 0.f};
+              const v4f part = mfma_fp8(st.af[a][s], wf, zero);
+              const float sbv = s < 4 ? sb0[s & 3] : sb1[s & 3];
+              st.acc[T][a] = part * (st.sa[a][s] * sbv) + st.acc[T][a];
+            } else {
+              st.acc[T][a] = mfma_fp8(st.af[a][s], wf, st.acc[T][a]);
+            }
           }
         }
       }
     }
+  };
+
+  if (nitems > 0) issue(0);
+  if (nitems > 1) issue(1);
+  for (int base_it = 0; base_it < nitems; base_it += P) {
+    // the P items of one chunk; item it = base_it + k sits in region it % 2
+    auto step = [&](auto kind_tag) {
+      constexpr int K = decltype(kind_tag)::value;
+      const int it = base_it + K;
+      // item it has landed once at most the one item issued after it is outstanding
+      if (it + 1 < nitems) dec::wait_vm<DPI>();
+      else dec::wait_vm<0>();
+      const uint8_t *base = region[wave][it & 1];
+      consume(kind_tag, base);
+      dec::wait_lds();                 // region free: every LDS read of it has returned
+      if (it + 2 < nitems) issue(it + 2);
+    };
+    dec::static_for<0, P>(step);
   }
 
   // ---- sum the waves' partial tiles and write the 16*TN columns
 #pragma unroll
-  for (int tn = 0; tn < TN; ++tn)
+  for (int t = 0; t < TN; ++t)
 #pragma unroll
-    for (int t = 0; t < TMA; ++t) *reinterpret_cast<v4f *>(red[wave][tn][t][lane]) = acc_all[tn][t];
+    for (int a = 0; a < TMA; ++a) *reinterpret_cast<v4f *>(red[wave][t][a][lane]) = st.acc[t][a];
   __syncthreads();
   float s1 = 1.f, s2 = 1.f;
   if constexpr (Cfg::MODE == MODE_FP8_TENSOR) {
@@ -225,23 +295,179 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_decode_kernel(const GemmArgs p) 
     s2 = *p.gb;
   }
   for (int o = threadIdx.x; o < TN * TMA * 256; o += Cfg::NT) {
-    // output o: W tile tn, A tile t, lane ln, register i ->
-    // row 16t + 4*(ln/16) + i, col 16tn + ln%16
-    const int tn = o / (TMA * 256), t = (o >> 8) % TMA, ln = (o >> 2) & 63, i = o & 3;
-    const int row = t * 16 + 4 * (ln >> 4) + i, col = nb0 + tn * 16 + (ln & 15);
+    // output o: W tile t, activation tile a, lane ln, register i ->
+    // row 16a + 4*(ln/16) + i, col nb0 + 16t + ln%16
+    const int t = o / (TMA * 256), a = (o >> 8) % TMA, ln = (o >> 2) & 63, i = o & 3;
+    const int row = a * 16 + 4 * (ln >> 4) + i, col = nb0 + t * 16 + (ln & 15);
     if (row >= p.M || col >= p.N) continue;
     float v = 0.f;
 #pragma unroll
-    for (int w = 0; w < NW; ++w) v += red[w][tn][t][ln][i];
+    for (int w = 0; w < NW; ++w) v += red[w][t][a][ln][i];
     if constexpr (Cfg::MODE == MODE_FP8_TENSOR) v = (v * s1) * s2;
     if (p.out_f32) static_cast<float *>(p.c)[(int64_t)row * p.ldc + col] = v;
     else static_cast<uint16_t *>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16(v);
   }
 }
 
+// ------------------------------------------------------- NVFP4 GEMV (M <= 4)
+// 32 E2M1 codes (16 bytes) with their two E4M3 block scales (low byte: the
+// first 16 codes) as 16 pairs of fp16 (exact: at most 5 significant bits).
+DSL_DEV void nv_dequant32(const v4i &q, uint32_t sc2, v2h (&out)[16]) {
+  const _Float16 s0 = e4m3_to_f16(sc2 & 0xFF), s1 = e4m3_to_f16((sc2 >> 8) & 0xFF);
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const v8h h = fp4x8_to_f16((uint32_t)q[w], w < 2 ? s0 : s1);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[4 * w + e] = (v2h){h[2 * e], h[2 * e + 1]};
+  }
+}
+
+// acc += sum over the 32 elements of a[e] * (E2M1 code e x its block scale):
+// per 16-element block, the dot products of the raw codes (converted to fp16
+// with unit scale) accumulate in fp32 and the block scale, decoded exactly
+// by the hardware OCP E4M3 -> f32 conversion, applies once.
+template <int B>
+DSL_DEV float nv_dot16(const v2h (&a)[16], const v4i &q, uint32_t sc2, float acc) {
+  float part = 0.f;
+#pragma unroll
+  for (int w = 0; w < 2; ++w) {
+    const uint32_t word = (uint32_t)q[2 * B + w];
+    const v2h *ap = &a[8 * B + 4 * w];
+    part = __builtin_amdgcn_fdot2(ap[0], __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 0), part, false);
+    part = __builtin_amdgcn_fdot2(ap[1], __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 1), part, false);
+    part = __builtin_amdgcn_fdot2(ap[2], __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 2), part, false);
+    part = __builtin_amdgcn_fdot2(ap[3], __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(word, 1.0f, 3), part, false);
+  }
+  return __builtin_fmaf(__builtin_amdgcn_cvt_f32_fp8((int)sc2, B), part, acc);
+}
+DSL_DEV float nv_dot32(const v2h (&a)[16], const v4i &q, uint32_t sc2, float acc) {
+  return nv_dot16<1>(a, q, sc2, nv_dot16<0>(a, q, sc2, acc));
+}
+
+DSL_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int MM, int NCH, int RPW>
+__global__ __launch_bounds__(256) void gemv_nvfp4_kernel(const GemmArgs p) {
+  constexpr int SROW = NCH * 128;                 // E4M3 scale bytes per row
+  constexpr int WSB = RPW * SROW;                 // a wave's W scale bytes (contiguous rows)
+  constexpr int WSD = (WSB + 1023) / 1024;        // its 1 KB scale DMAs
+  constexpr int AD = MM * NCH;                    // activation data DMAs (1 KB each)
+  constexpr int ASD = (MM * SROW + 1023) / 1024;  // activation scale DMAs
+  __shared__ __align__(16) uint8_t a_lds[MM][NCH * 1024];
+  __shared__ __align__(16) uint8_t as_lds[ASD * 1024];
+  __shared__ __align__(16) uint8_t ws_lds[4][WSD * 1024];
+  const int lane = threadIdx.x & 63;
+  const int wv = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int n0 = (blockIdx.x * 4 + wv) * RPW;
+  const bool live = n0 < p.N;
+  const int64_t sbytes = (int64_t)p.N * SROW;     // size of the W scale matrix
+
+  // wave 0: the activations (data and scales) for the whole workgroup
+  if (wv == 0) {
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      const int row = min(m, p.M - 1);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        dec::dma16(p.a + (int64_t)row * p.Kb + c * 1024 + lane * 16,
+                   dec::lds_addr(&a_lds[m][c * 1024]));
+    }
+#pragma unroll
+    for (int j = 0; j < ASD; ++j) {
+      // activation scale rows are contiguous; pieces past them re-read the last 16 bytes
+      const int off = min(j * 1024 + lane * 16, p.M * SROW - 16);
+      dec::dma16(static_cast<const uint8_t *>(p.sa) + off, dec::lds_addr(&as_lds[j * 1024]));
+    }
+  }
+  // this wave's W scales (RPW contiguous rows), then its W rows into registers
+  v4i wq[RPW][NCH];
+  if (live) {
+#pragma unroll
+    for (int j = 0; j < WSD; ++j) {
+      const int64_t off = min((int64_t)n0 * SROW + j * 1024 + lane * 16, sbytes - 16);
+      dec::dma16(static_cast<const uint8_t *>(p.sb) + off, dec::lds_addr(&ws_lds[wv][j * 1024]));
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const int row = min(n0 + r, p.N - 1);
+#pragma unroll
+      for (int c = 0; c < NCH; ++c)
+        wq[r][c] = __builtin_nontemporal_load(
+            reinterpret_cast<const v4i *>(p.b + (int64_t)row * p.Kb + c * 1024 + lane * 16));
+    }
+  }
+  // the direct-to-LDS loads were issued before the W rows: they have landed
+  // once at most the RPW*NCH row loads are outstanding
+  if (live) dec::wait_vm<RPW * NCH>();
+  else dec::wait_vm<0>();
+  __syncthreads();
+  if (!live) return;
+  v2h a[MM][NCH][16];
+#pragma unroll
+  for (int m = 0; m < MM; ++m)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const v4i q = *reinterpret_cast<const v4i *>(&a_lds[m][c * 1024 + lane * 16]);
+      const uint32_t s2 = *reinterpret_cast<const uint16_t *>(&as_lds[m * SROW + c * 128 + lane * 2]);
+      nv_dequant32(q, s2, a[m][c]);
+    }
+  uint32_t ws[RPW][NCH];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r)
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+      ws[r][c] = *reinterpret_cast<const uint16_t *>(&ws_lds[wv][r * SROW + c * 128 + lane * 2]);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    float acc[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) acc[m] = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int m = 0; m < MM; ++m) acc[m] = nv_dot32(a[m][c], wq[r][c], ws[r][c], acc[m]);
+    const int col = n0 + r;
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      float v = wave_sum(acc[m]);
+      if (lane == m && m < p.M && col < p.N) {
+        v = (v * (*p.ga)) * (*p.gb);
+        if (p.out_f32) static_cast<float *>(p.c)[(int64_t)m * p.ldc + col] = v;
+        else static_cast<uint16_t *>(p.c)[(int64_t)m * p.ldc + col] = f32_to_bf16(v);
+      }
+    }
+  }
+}
+
+template <int MM, int NCH>
+static hipError_t launch_gemv_nv(const GemmArgs &p, hipStream_t st) {
+  if constexpr (MM * NCH > 8) {
+    return hipErrorInvalidValue;          // excluded by decode_supported (register budget)
+  } else {
+    constexpr int RPW = 4;
+    const int waves = (p.N + RPW - 1) / RPW;
+    gemv_nvfp4_kernel<MM, NCH, RPW><<<(waves + 3) / 4, 256, 0, st>>>(p);
+    return hipGetLastError();
+  }
+}
+
+template <int MM>
+static hipError_t launch_gemv_nv_m(const GemmArgs &p, hipStream_t st) {
+  switch (p.Kb / 1024) {
+    case 1: return launch_gemv_nv<MM, 1>(p, st);
+    case 2: return launch_gemv_nv<MM, 2>(p, st);
+    case 4: return launch_gemv_nv<MM, 4>(p, st);
+    default: return launch_gemv_nv<MM, 8>(p, st);
+  }
+}
+
 template <int MODE, int TMA>
 static hipError_t launch_decode_tma(const GemmArgs &p, hipStream_t st) {
-  using Cfg = DecodeCfg<MODE, TMA, 4, DSL_DECODE_TN>;
+  using Cfg = DecodeCfg<MODE, TMA>;
   const int grid = (p.N + 16 * Cfg::TN - 1) / (16 * Cfg::TN);
   gemm_decode_kernel<Cfg><<<grid, Cfg::NT, 0, st>>>(p);
   return hipGetLastError();
@@ -254,10 +480,18 @@ static hipError_t launch_decode_mode(const GemmArgs &p, hipStream_t st) {
 }
 
 bool decode_supported(int mode, int M, int K, int Kb, bool scales4, bool scales16) {
-  if (M > 32 || M < 1 || Kb % 1024 != 0) return false;
+  if (M < 1 || Kb % 1024 != 0) return false;
+  if (mode == MODE_NVFP4) {
+    // GEMV: activations stay in registers for all of K (M * chunks <= 8);
+    // scale rows move by 16-byte direct-to-LDS loads
+    const int nch = Kb / 1024;
+    return scales16 && M <= 4 && (nch == 1 || nch == 2 || nch == 4 || nch == 8) && M * nch <= 8;
+  }
+  if (M > 32) return false;
   if (mode == MODE_FP8_TENSOR) return true;
-  if (mode == MODE_FP8_BLOCK) return scales4;
-  if (mode == MODE_MXFP4) return scales16 && (K / 32) % 16 == 0;
+  // block scales and E8M0 rows move by 16-byte direct loads
+  if (mode == MODE_FP8_BLOCK) return scales16 && K % 512 == 0;
+  if (mode == MODE_MXFP4) return scales16 && K % 512 == 0;
   return false;
 }
 
@@ -265,7 +499,14 @@ hipError_t launch_gemm_decode(int mode, const GemmArgs &p, hipStream_t st) {
   switch (mode) {
     case MODE_FP8_TENSOR: return launch_decode_mode<MODE_FP8_TENSOR>(p, st);
     case MODE_FP8_BLOCK: return launch_decode_mode<MODE_FP8_BLOCK>(p, st);
-    default: return launch_decode_mode<MODE_MXFP4>(p, st);
+    case MODE_MXFP4: return launch_decode_mode<MODE_MXFP4>(p, st);
+    default:
+      switch (p.M) {
+        case 1: return launch_gemv_nv_m<1>(p, st);
+        case 2: return launch_gemv_nv_m<2>(p, st);
+        case 3: return launch_gemv_nv_m<3>(p, st);
+        default: return launch_gemv_nv_m<4>(p, st);
+      }
   }
 }
 

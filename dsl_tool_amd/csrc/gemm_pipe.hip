@@ -459,6 +459,7 @@ hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_
     switch (variant) {
       case 0: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 256, 2, 4, 4, 64, 0, 1>>(p, st);
       case 2: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 256, 2, 4, 4, 64>>(p, st);
+      case 4: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 256, 2, 2, 4, 64, 1, 1>>(p, st);
       case 3: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 128, 4, 2, 3, 128>>(p, st);
       default: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 128, 128, 2, 2, 4, 64>>(p, st);
     }
@@ -473,6 +474,8 @@ hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_
   switch (variant) {
     case 0: return launch_pipe_cfg<PipeCfg<MODE_MXFP4, 256, 256, 2, 4, 4, 64>>(p, st);
     case 2: return launch_pipe_cfg<PipeCfg<MODE_MXFP4, 256, 256, 2, 4, 2, 128>>(p, st);
+    case 4: return launch_pipe_cfg<PipeCfg<MODE_MXFP4, 256, 256, 2, 2, 4, 64, 1, 1>>(p, st);
+    case 5: return launch_pipe_cfg<PipeCfg<MODE_MXFP4, 256, 256, 2, 4, 4, 64, 0, 1>>(p, st);
     default: return launch_pipe_cfg<PipeCfg<MODE_MXFP4, 128, 128, 2, 2, 4, 64>>(p, st);
   }
 }

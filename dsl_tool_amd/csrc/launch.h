@@ -45,9 +45,10 @@ struct GemmArgs {
 // variant 0: 256x256 tile, 8 waves; 1: 128x128 tile, 4 waves.
 hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_t st);
 
-// Skinny-M kernel (M <= 32, Kb % 1024 == 0; FP8_TENSOR, FP8_BLOCK with
-// 4-byte aligned scales, MXFP4 with 16-byte aligned scale rows): one
-// launch, no workspace.
+// Skinny-M kernels, one launch, no workspace (Kb % 1024 == 0):
+//   M <= 32: FP8_TENSOR; FP8_BLOCK and MXFP4 with 16-byte aligned scales
+//            and K % 512 == 0;
+//   M <= 4:  NVFP4 GEMV with 4-byte aligned scales and M * Kb/1024 <= 8.
 bool decode_supported(int mode, int M, int K, int Kb, bool scales4, bool scales16);
 hipError_t launch_gemm_decode(int mode, const GemmArgs &p, hipStream_t st);
 

@@ -290,7 +290,8 @@ def test_fp8_mfma_accumulation_bound():
 
 
 # ------------------------------------------------ skinny-M decode kernel --
-DECODE_SHAPES = [(1, 1000, 4096), (7, 2048, 1024), (16, 7168, 4096), (32, 1040, 2048)]
+DECODE_SHAPES = [(1, 1000, 4096), (7, 2048, 1024), (16, 7168, 4096), (32, 1040, 2048),
+                 (17, 48, 8192), (16, 7184, 12288), (5, 16, 3072)]
 
 
 @pytest.mark.parametrize("m,n,k", DECODE_SHAPES)
@@ -325,6 +326,20 @@ def test_mxfp4_decode(m, n, k):
     c = G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4")
     ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
     assert_close(c, ref, what=f"mxfp4 decode {m}x{n}x{k}")
+
+
+# NVFP4 with M <= 4 and M * K/2048 <= 8 runs the GEMV kernel; the other
+# shapes here take the dense paths (same oracle).
+@pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (2, 1000, 2048), (3, 530, 4096),
+                                   (4, 64, 4096), (1, 33, 16384), (3, 520, 8192), (4, 100, 8192)])
+def test_nvfp4_decode(m, n, k):
+    a = W.randn_bf16((m, k), 451)
+    w = W.randn_bf16((n, k), 452, 0.02)
+    qa, sa, ga = Q.quant_nvfp4(a.to(DEV))
+    qw, sw, gw = Q.quant_nvfp4(w.to(DEV))
+    c = G.fp4_gemm_packed(qa, sa, qw, sw, fmt="nvfp4", global_a=ga, global_w=gw)
+    ref = OG.ref_nvfp4(np_u8(qa), np_u8(sa), np_f32(ga)[0], np_u8(qw), np_u8(sw), np_f32(gw)[0])
+    assert_close(c, ref, what=f"nvfp4 decode {m}x{n}x{k}")
 
 
 def test_grouped_moe_skewed_counts_pipelined():

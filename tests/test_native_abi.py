@@ -59,8 +59,10 @@ def test_fp8_gemm_argument_validation(lib):
 def test_workspace_query_matches_the_planned_path(lib):
     # skinny M with K a multiple of 1024 takes the single-pass decode kernel
     assert lib.dsl_gemm_workspace_bytes(N.OP_FP8, 16, 8192, 8192) == 0
-    # FP4 reports the larger of the MXFP4 and NVFP4 plans (NVFP4 decode is split-K)
-    assert lib.dsl_gemm_workspace_bytes(N.OP_FP4, 1, 14336, 4096) >= 14336 * 4
+    # FP4 reports the larger of the MXFP4 and NVFP4 plans: NVFP4 with M <= 4
+    # runs the GEMV kernel (no workspace), with M = 8 it plans split-K
+    assert lib.dsl_gemm_workspace_bytes(N.OP_FP4, 1, 14336, 4096) == 0
+    assert lib.dsl_gemm_workspace_bytes(N.OP_FP4, 8, 14336, 4096) >= 8 * 14336 * 4
     # large problems take the pipelined kernels, which need none either
     assert lib.dsl_gemm_workspace_bytes(N.OP_FP8, 8192, 8192, 8192) == 0
     # a skinny problem the decode kernel does not cover plans split-K and
