@@ -1,0 +1,486 @@
+// Persistent pipelined GEMM for gfx950 (FP8 per-tensor, FP8 1x128/128x128
+// block-scaled): C[M,N] = A[M,K] . W[N,K]^T, both operands K-major.
+//
+// One workgroup per CU walks its output tiles (tile v = blockIdx.x +
+// r * gridDim.x in the XCD-aware order of tile_coords), 256x256 with 8 waves
+// (2 x 4, each 128 x 64, 32x32x64 MFMAs with the W tile in the first operand
+// slot, so a lane owns one output row).
+//
+// Data path.  K advances in 64-byte steps, but operands move in pairs of
+// steps: a pair is 128 bytes of K for every row of the tile, and each
+// direct-to-LDS load (global_load_lds_dwordx4) copies 8 rows x 128 bytes,
+// i.e. whole 128-byte lines.  With 64-byte rows the L1 sends one 64-byte
+// request to L2 per half line and cannot keep the other half until the next
+// step, so the same bytes cost twice the requests; the L1's outstanding
+// requests are what limit the copy rate, so whole lines double it.  Two pair
+// slots form the ring in LDS: pair q+2 is copied into the slot of pair q
+// during the second step of pair q+1, one step after the barrier that
+// certifies pair q read, and waited for two steps later.  A barrier is
+// needed only at the start of the second step of a pair (it publishes the
+// next pair and frees the previous slot), so there is one per 128 K.  The
+// ring runs on across tile boundaries: the first pairs of tile r+1 are
+// copied during the last steps of tile r.
+//
+// Fragments: W fragments double-buffered by step parity, A rows reloaded in
+// place right after the MFMAs that consume them (they are not read again
+// until the next step), which keeps the 128 fp32 accumulators, both
+// fragment sets and the copy plan within 256 VGPRs.
+//
+// Scales.  FP8 block: a pair is exactly one 128-K scale group, and its slot
+// carries sa[row][g] for the tile's 256 rows and sb[nb][g] for the tile's
+// two 128-column weight blocks.  The accumulator is kept in units of the
+// current group's scale s_g(m) = sa[m][g] * sb[n/128][g] and multiplied by
+// s_g / s_{g+1} at each group boundary; the epilogue multiplies by the last
+// s_g.  This is the group-partial sum of cuda/gemm/fp8_gemm.cu:84-97 up to
+// fp32 rounding.
+//
+// Epilogue: each wave converts its accumulators (v_cvt_pk_bf16_f32) and
+// stores 8 bytes (4 columns of one row) per store straight from registers.
+// Stores share vmcnt with the ring's loads; the next pair wait (vmcnt(0))
+// also waits for them.
+#include <type_traits>
+
+#include "pipe_core.h"
+
+namespace dsl {
+
+template <int MODE_>
+struct PersCfg {
+  static constexpr int MODE = MODE_;
+  static constexpr int BM = 256, BN = 256, WGM = 2, WGN = 4;
+  static constexpr int NW = WGM * WGN, NT = NW * 64, OCC = 2;
+  static constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
+  static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;
+  static constexpr int PKB = 128;                      // K bytes per pair (per row)
+  static constexpr int CH = PKB / 16, RPI = 1024 / PKB;  // chunks per row, rows per DMA
+  static constexpr int A_BYTES = BM * PKB, B_BYTES = BN * PKB;
+  static constexpr int SA_BYTES = BLOCK ? BM * 4 : 0;  // sa[row][g] of the pair's group
+  static constexpr int SB_BYTES = BLOCK ? 256 : 0;     // sb of the two column blocks (8 B used)
+  static constexpr int PAIR = A_BYTES + B_BYTES + SA_BYTES + SB_BYTES;
+  static constexpr int LDS = 2 * PAIR;
+  static constexpr int A_DMA = A_BYTES / 1024, B_DMA = B_BYTES / 1024;
+  static constexpr int SA_DMA = SA_BYTES / 256, SB_DMA = SB_BYTES / 256;
+  static constexpr int DATA_DMA = A_DMA + B_DMA, SC_DMA = SA_DMA + SB_DMA;
+  static constexpr int DD = DATA_DMA / NW, DS = (SC_DMA + NW - 1) / NW, D = DD + DS;
+  static_assert(DATA_DMA % NW == 0 && A_DMA % DD == 0, "whole waves per operand");
+  static_assert(DS <= 1, "at most one scale DMA per wave and pair");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(!BLOCK || (WN <= 128 && 128 % WN == 0), "one weight-scale block per wave");
+};
+
+namespace pers {
+
+// Direct-to-LDS loads in the saddr form: a wave-uniform 64-bit base (SGPRs)
+// plus a 32-bit per-lane offset (one VGPR).
+DSL_DEV void dma16(const uint8_t *base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff),
+               "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+DSL_DEV void dma4(const uint8_t *base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff),
+               "s"(base), "s"(lds)
+               : "memory", "m0");
+}
+
+// Copy plan of one thread for the tile at (m0, n0): DD operand DMAs (8 rows
+// x 128 bytes each) and, for waves below SC_DMA, one scale-word DMA per
+// pair.  A wave's operand DMAs all read the same operand (waves below
+// A_DMA/DD copy A, the others W), so one uniform base serves them; the lane
+// offsets are formed at issue time from the lane's row and chunk (a few
+// VALU ops beside the MFMAs instead of DD live registers).
+// `full`: this wave issues all D instructions.
+template <class Cfg>
+struct Ring {
+  const uint8_t *dbase;          // operand rows of the tile, pair 0
+  const uint8_t *sbase;          // scale words of the tile, pair 0
+  int wrow;                      // the wave's first tile row (uniform)
+  int lim;                       // last valid tile row of the operand (uniform)
+  int kb;
+  uint32_t vsub;                 // lane's row within one DMA
+  uint32_t vchunk;               // lane's chunk byte offset for even DMAs
+  uint32_t soff;                 // lane's scale offset
+  int wave;
+  bool full;
+
+  DSL_DEV void target(const GemmArgs &p, int m0, int n0, int wave_, int lane) {
+    wave = wave_;
+    full = Cfg::DS == 0 || wave < Cfg::SC_DMA;
+    const bool isA = wave * Cfg::DD < Cfg::A_DMA;
+    const int r0 = isA ? m0 : n0;
+    lim = (isA ? p.M : p.N) - 1 - r0;
+    kb = p.Kb;
+    wrow = (isA ? wave * Cfg::DD : wave * Cfg::DD - Cfg::A_DMA) * Cfg::RPI;
+    dbase = (isA ? p.a : p.b) + (int64_t)r0 * p.Kb;
+    vsub = lane / Cfg::CH;
+    // DMA j covers tile rows wrow + j*RPI + vsub; RPI is even, so the row
+    // swizzle only depends on vsub and the parity of wrow/RPI + j
+    vchunk = (uint32_t)(((lane % Cfg::CH) ^ pipe::swz<Cfg::PKB>(wrow + (int)vsub)) * 16);
+    sbase = p.a;
+    soff = 0;
+    if constexpr (Cfg::DS > 0) {
+      const int64_t rowb = (int64_t)(p.K / 128) * 4;   // bytes per scale row
+      if (wave < Cfg::SA_DMA) {
+        int grow = m0 + wave * 64 + lane;
+        grow = grow < p.M ? grow : p.M - 1;
+        sbase = static_cast<const uint8_t *>(p.sa) + m0 * rowb;
+        soff = (uint32_t)((grow - m0) * rowb);
+      } else {
+        // lanes 0 / 1: the tile's two 128-column blocks (others repeat them)
+        const int nbb = (p.N + 127) / 128, b0 = n0 / 128;
+        int blk = b0 + (lane & 1);
+        blk = blk < nbb ? blk : nbb - 1;
+        sbase = static_cast<const uint8_t *>(p.sb) + b0 * rowb;
+        soff = (uint32_t)((blk - b0) * rowb);
+      }
+    }
+  }
+
+  // DMA instruction j of tile-local pair q into the pair slot at `slot`
+  DSL_DEV void issue_one(int j, int q, uint32_t slot) const {
+    if (j < Cfg::DD) {
+      int r = (int)vsub + (wrow + j * Cfg::RPI);
+      r = r < lim ? r : lim;           // rows past the edge re-read the last row
+      // swz(wrow + j*RPI + vsub) = swz(wrow + vsub) ^ swz(j*RPI): the row
+      // offset j*RPI only flips bit 2 of the swizzle, by the parity of j
+      const uint32_t ch = vchunk ^ (uint32_t)(pipe::swz<Cfg::PKB>(j * Cfg::RPI) * 16);
+      dma16(dbase + (int64_t)q * Cfg::PKB, (uint32_t)(r * kb) + ch,
+            slot + (uint32_t)((wave * Cfg::DD + j) * 1024));
+    } else if (full) {
+      const bool sa = wave < Cfg::SA_DMA;
+      const uint32_t dst = Cfg::A_BYTES + Cfg::B_BYTES + (sa ? wave * 256 : Cfg::SA_BYTES);
+      dma4(sbase + (int64_t)q * 4, soff, slot + dst);   // group q: one float per row
+    }
+  }
+};
+
+// Operand fragments of one 64-byte step (half p of a pair slot) of one wave:
+// lane l holds row l%32 of each 32-row tile and 32 bytes of K (two 16-byte
+// chunks, K half h = l/32), the layout of v_mfma_scale_f32_32x32x64_f8f6f4.
+template <class Cfg>
+struct Frag {
+  v8i a[Cfg::TM], b[Cfg::TN];
+  static DSL_DEV v8i ld(const uint8_t *base, int row, int p, int h) {
+    const int s = pipe::swz<Cfg::PKB>(row), c0 = 4 * p + 2 * h;
+    const v4i lo = *reinterpret_cast<const v4i *>(base + row * Cfg::PKB + ((c0 ^ s) << 4));
+    const v4i hi = *reinterpret_cast<const v4i *>(base + row * Cfg::PKB + (((c0 + 1) ^ s) << 4));
+    return (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  }
+  DSL_DEV void load_a(const uint8_t *slot, int p, int i, int wm, int r32, int h) {
+    a[i] = ld(slot, wm * Cfg::WM + i * 32 + r32, p, h);
+  }
+  DSL_DEV void load_b(const uint8_t *slot, int p, int wn, int r32, int h) {
+#pragma unroll
+    for (int j = 0; j < Cfg::TN; ++j) b[j] = ld(slot + Cfg::A_BYTES, wn * Cfg::WN + j * 32 + r32, p, h);
+  }
+};
+
+// MFMAs of row i: W fragments from fb, A from fa (operands swapped).
+template <class Cfg>
+DSL_DEV void mma_row(const Frag<Cfg> &fa, const Frag<Cfg> &fb, int i, v16f (&acc)[Cfg::TM][Cfg::TN]) {
+#pragma unroll
+  for (int j = 0; j < Cfg::TN; ++j)
+    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb.b[j], fa.a[i], acc[i][j], 0, 0,
+                                                                0, 0, 0, 0);
+}
+
+}  // namespace pers
+
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT) __attribute__((amdgpu_waves_per_eu(Cfg::OCC, Cfg::OCC)))
+void gemm_persist_kernel(const GemmArgs p) {
+  constexpr int D = Cfg::D, TM = Cfg::TM, TN = Cfg::TN;
+  __shared__ __align__(16) uint8_t smem[Cfg::LDS];
+  // per-tensor scales first: no global load may follow the DMA asm
+  float s1 = 1.f, s2 = 1.f;
+  if constexpr (Cfg::MODE == MODE_FP8_TENSOR) {
+    s1 = *p.ga;
+    s2 = *p.gb;
+  }
+  const int nbm = (p.M + Cfg::BM - 1) / Cfg::BM, nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
+  const int ntiles = nbm * nbn;
+  const int b = blockIdx.x, grid = gridDim.x;
+  const int my_tiles = (ntiles - b + grid - 1) / grid;   // >= 1: grid <= ntiles
+  const int nkp = p.Kb / Cfg::PKB;                        // pairs per tile, >= 1
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+  const int r32 = lane & 31, h = lane >> 5;
+  const uint32_t lds0 = pipe::lds_addr(smem);
+
+  auto tile_origin = [&](int t, int &m0, int &n0) __attribute__((always_inline)) {
+    int tm, tn;
+    tile_coords(b + t * grid, nbm, nbn, tm, tn);
+    m0 = tm * Cfg::BM;
+    n0 = tn * Cfg::BN;
+  };
+
+  // issue cursor: the next pair to copy is pair iq of local tile it, global
+  // pair number ig (its slot: ig % 2).  Past the workgroup's last pair the
+  // cursor stays on it, so every step copies a pair (into a slot nobody reads
+  // again) and all steps have the same shape.
+  pers::Ring<Cfg> ring;
+  int it = 0, iq = 0, ig = 0;
+  {
+    int m0, n0;
+    tile_origin(0, m0, n0);
+    ring.target(p, m0, n0, wave, lane);
+  }
+  auto issue_pair_prep = [&]() __attribute__((always_inline)) {
+    if (iq == nkp && it + 1 < my_tiles) {
+      iq = 0;
+      ++it;
+      int m0, n0;
+      tile_origin(it, m0, n0);
+      ring.target(p, m0, n0, wave, lane);
+    }
+  };
+  auto slot_of = [&](int gp) __attribute__((always_inline)) { return lds0 + (uint32_t)((gp & 1) * Cfg::PAIR); };
+
+  // block scales of a lane's rows in the wave's column block, from a pair slot
+  auto block_scale = [&](const uint8_t *slot, int i) __attribute__((always_inline)) {
+    const float *sa = reinterpret_cast<const float *>(slot + Cfg::A_BYTES + Cfg::B_BYTES);
+    const float *sb = sa + Cfg::BM;
+    return sa[wm * Cfg::WM + i * 32 + r32] * sb[(wn * Cfg::WN) / 128];
+  };
+
+  v16f acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  float sc[TM];           // block: s_g(row) of the group the accumulator is expressed in
+#pragma unroll
+  for (int i = 0; i < TM; ++i) sc[i] = 1.f;
+
+  // ---- epilogue of local tile t: convert, scale, store from registers.
+  // Lane (r32, h) stores, for each of its rows, 4 consecutive columns per
+  // (j, q): col = n0 + wn*WN + 32j + 8q + 4h.  Interior tiles (the common
+  // case) take an unchecked path with one row pointer and constant column
+  // offsets; edge tiles check every element.
+  auto epilogue = [&](int t) __attribute__((always_inline)) {
+    int m0, n0;
+    tile_origin(t, m0, n0);
+    const int c0 = n0 + wn * Cfg::WN + 4 * h;
+    const bool interior = m0 + Cfg::BM <= p.M && n0 + Cfg::BN <= p.N && (p.ldc % 4) == 0 &&
+                          (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
+    auto val = [&](int i, int j, int r) __attribute__((always_inline)) {
+      float x = acc[i][j][r];
+      if constexpr (Cfg::MODE == MODE_FP8_TENSOR) x = (x * s1) * s2;
+      else if constexpr (Cfg::BLOCK) x = x * sc[i];
+      return x;
+    };
+    if (interior) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int64_t row = m0 + wm * Cfg::WM + i * 32 + r32;
+        if (p.out_f32) {
+          float *dst = static_cast<float *>(p.c) + row * p.ldc + c0;
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              *reinterpret_cast<float4 *>(dst + j * 32 + q * 8) =
+                  make_float4(val(i, j, 4 * q), val(i, j, 4 * q + 1), val(i, j, 4 * q + 2),
+                              val(i, j, 4 * q + 3));
+        } else {
+          uint16_t *dst = static_cast<uint16_t *>(p.c) + row * p.ldc + c0;
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const uint32_t lo = pack_bf16x2(val(i, j, 4 * q), val(i, j, 4 * q + 1));
+              const uint32_t hi = pack_bf16x2(val(i, j, 4 * q + 2), val(i, j, 4 * q + 3));
+              *reinterpret_cast<uint2 *>(dst + j * 32 + q * 8) = make_uint2(lo, hi);
+            }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = m0 + wm * Cfg::WM + i * 32 + r32;
+        if (row >= p.M) continue;
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int col = c0 + j * 32 + 8 * (r >> 2) + (r & 3);
+            if (col >= p.N) continue;
+            const float v = val(i, j, r);
+            if (p.out_f32) static_cast<float *>(p.c)[(int64_t)row * p.ldc + col] = v;
+            else static_cast<uint16_t *>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16(v);
+          }
+      }
+    }
+    // keep the zeroing below the stores: hoisted, it would double the live
+    // accumulator registers
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+  };
+
+  // ---- prologue: pairs 0 and 1, then the fragments of step 0
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    issue_pair_prep();
+    const uint32_t slot = slot_of(ig);
+    const int qq = iq < nkp ? iq : nkp - 1;
+#pragma unroll
+    for (int j = 0; j < D; ++j) ring.issue_one(j, qq, slot);
+    ++iq;
+    ++ig;
+  }
+  if (ring.full) pipe::wait_vmcnt<D>();       // pair 0 landed, pair 1 may be in flight
+  else pipe::wait_vmcnt<D - 1>();
+  __syncthreads();
+  pers::Frag<Cfg> fa, fb[2];
+  fb[0].load_b(smem, 0, wn, r32, h);
+#pragma unroll
+  for (int i = 0; i < TM; ++i) fa.load_a(smem, 0, i, wm, r32, h);
+  if constexpr (Cfg::BLOCK) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) sc[i] = block_scale(smem, i);
+  }
+
+  // First step of local pair gp: MFMAs of its half 0 (fragments in fb[0] /
+  // fa), reads of its half 1 from the same slot (landed and published with
+  // the pair).
+  auto step0 = [&](int gp) __attribute__((always_inline)) {
+    const uint8_t *st = smem + (gp & 1) * Cfg::PAIR;
+    fb[1].load_b(st, 1, wn, r32, h);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      pers::mma_row<Cfg>(fa, fb[0], i, acc);
+      fa.load_a(st, 1, i, wm, r32, h);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // Second step of local pair gp: wait for pair gp+1 (the only pair in
+  // flight), barrier (publishes it; every wave has read pair gp), copy pair
+  // gp+2 into the slot of pair gp during the MFMAs of half 1, read half 0 of
+  // pair gp+1.  KIND 1: the group ends (block: rescale to the next group's
+  // scale); KIND 2: the tile ends (epilogue, then the next tile's step 0).
+  auto step1 = [&](auto kind_tag, int gp) __attribute__((always_inline)) {
+    constexpr int KIND = decltype(kind_tag)::value;
+    pipe::wait_vmcnt<0>();
+    pipe::wait_lds();
+    __syncthreads();
+    const uint8_t *stn = smem + ((gp + 1) & 1) * Cfg::PAIR;
+    issue_pair_prep();
+    const uint32_t islot = slot_of(ig);
+    const int qq = iq < nkp ? iq : nkp - 1;
+    if constexpr (KIND != 2) fb[0].load_b(stn, 0, wn, r32, h);
+    float sn[TM], rt[TM];
+    if constexpr (Cfg::BLOCK) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i) sn[i] = block_scale(stn, i);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      pers::mma_row<Cfg>(fa, fb[1], i, acc);
+#pragma unroll
+      for (int j = i * D / TM; j < (i + 1) * D / TM; ++j) ring.issue_one(j, qq, islot);
+      if constexpr (KIND != 2) fa.load_a(stn, 0, i, wm, r32, h);
+      if constexpr (Cfg::BLOCK && KIND == 1) {
+        // row i-1 had its last MFMA of the group issued one row ago
+        if (i == 1) {
+#pragma unroll
+          for (int u = 0; u < TM; ++u) {
+            rt[u] = sc[u] * __builtin_amdgcn_rcpf(sn[u]);
+            sc[u] = sn[u];
+          }
+        }
+        if (i >= 1) {
+#pragma unroll
+          for (int j = 0; j < TN; ++j) acc[i - 1][j] *= rt[i - 1];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (Cfg::BLOCK && KIND == 1) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[TM - 1][j] *= rt[TM - 1];
+    }
+    ++iq;
+    ++ig;
+    if constexpr (KIND == 2) {
+      epilogue(gp / nkp);
+      if constexpr (Cfg::BLOCK) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i) sc[i] = sn[i];   // the next tile's first group
+      }
+      fb[0].load_b(stn, 0, wn, r32, h);
+#pragma unroll
+      for (int i = 0; i < TM; ++i) fa.load_a(stn, 0, i, wm, r32, h);
+    }
+  };
+
+  // Tiles, each a run of pairs; the tile's last pair is peeled, so no branch
+  // carries MFMAs (the accumulators would be copied at the join).
+  using K1 = std::integral_constant<int, 1>;
+  using K2 = std::integral_constant<int, 2>;
+  int gp = 0;
+  for (int t = 0; t < my_tiles; ++t) {
+    for (int q = 0; q + 1 < nkp; ++q, ++gp) {
+      step0(gp);
+      step1(K1{}, gp);
+    }
+    step0(gp);
+    step1(K2{}, gp);
+    ++gp;
+  }
+  // the ring's last copies target LDS this workgroup still owns: let them
+  // land before the workgroup ends
+  pipe::wait_vmcnt<0>();
+}
+
+static int persist_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+template <int MODE>
+static hipError_t launch_persist_mode(const GemmArgs &p, hipStream_t st) {
+  using Cfg = PersCfg<MODE>;
+  const int ntiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * ((p.N + Cfg::BN - 1) / Cfg::BN);
+  int grid = persist_cu_count();
+  if (grid > ntiles) grid = ntiles;
+  gemm_persist_kernel<Cfg><<<grid, Cfg::NT, 0, st>>>(p);
+  return hipGetLastError();
+}
+
+bool persist_supported(int mode, int M, int N, int K, int Kb, bool scales4) {
+  (void)M;
+  (void)N;
+  if (Kb % 128 != 0 || Kb < 128) return false;          // whole pairs of 64-byte steps
+  if (mode == MODE_FP8_TENSOR) return true;
+  if (mode == MODE_FP8_BLOCK) return scales4 && K % 128 == 0;
+  return false;                                          // MXFP4 keeps the per-tile kernel
+}
+
+hipError_t launch_gemm_persist(int mode, const GemmArgs &p, hipStream_t st) {
+  switch (mode) {
+    case MODE_FP8_TENSOR: return launch_persist_mode<MODE_FP8_TENSOR>(p, st);
+    case MODE_FP8_BLOCK: return launch_persist_mode<MODE_FP8_BLOCK>(p, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace dsl

@@ -162,7 +162,9 @@ static bool env_off(const char *name) {
 //   DSL_GEMM_DECODE = 0/off    never use the skinny-M kernel
 //   DSL_GEMM_PIPE   = 0/off    never use the LDS-DMA pipelined kernels
 //   DSL_GEMM_PIPE   = 1..9     force that pipelined variant for large problems
-enum { PATH_DECODE = 0, PATH_PIPE = 1, PATH_TILED = 2 };
+//   DSL_GEMM_PERSIST = 0/off   use the per-tile pipelined kernels instead of
+//                              the persistent one for large problems
+enum { PATH_DECODE = 0, PATH_PIPE = 1, PATH_TILED = 2, PATH_PERSIST = 3 };
 struct Route {
   int path;
   int variant;    // PATH_PIPE variant
@@ -171,6 +173,7 @@ struct Route {
 
 static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc16) {
   static const bool decode_on = !env_off("DSL_GEMM_DECODE");
+  static const bool persist_on = !env_off("DSL_GEMM_PERSIST");
   static const int pipe_forced = [] {
     if (env_off("DSL_GEMM_PIPE")) return -2;
     const char *e = getenv("DSL_GEMM_PIPE");
@@ -188,6 +191,8 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
     if (t256 >= 240) {
       r.path = PATH_PIPE;
       r.variant = pipe_forced >= 0 ? pipe_forced : 0;
+      if (persist_on && pipe_forced < 0 && persist_supported(mode, M, N, K, Kb, sc4))
+        r.path = PATH_PERSIST;
     } else if (M > 64 && N > 64 && t128 >= 200) {
       r.path = PATH_PIPE;
       r.variant = 1;
@@ -210,6 +215,7 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
   p.ksplit = 1;
   if (r.path == PATH_DECODE) return launch_gemm_decode(mode, p, st);
   if (r.path == PATH_PIPE) return launch_gemm_pipe(mode, p, r.variant, st);
+  if (r.path == PATH_PERSIST) return launch_gemm_persist(mode, p, st);
   const Plan pl = r.tiled;
   p.ksplit = p.ws ? pl.ksplit : 1;
   if (p.ksplit > 1) {

@@ -222,6 +222,32 @@ def test_fp8_block_pipelined(m, n, k):
     assert_close(c, ref, what=f"fp8 block pipelined {m}x{n}x{k}")
 
 
+# The persistent kernel with more tiles than CUs: several tiles per
+# workgroup with the DMA ring running across tile boundaries, ragged M/N
+# edges (the unchecked store path for interior tiles, the checked one for
+# edge tiles), bf16 and fp32 output.
+PERSIST_SHAPES = [(8192, 4352, 512), (4500, 4200, 384), (4352, 8192, 256)]
+
+
+@pytest.mark.parametrize("m,n,k", PERSIST_SHAPES)
+@pytest.mark.parametrize("block", [False, True])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_fp8_persistent(m, n, k, block, out_dtype):
+    a = W.activations(4, m, k, outliers=True) if block else W.randn_bf16((m, k), 141)
+    w = W.randn_bf16((n, k), 142, 0.02)
+    if block:
+        qa, sa = Q.quant_fp8_blocks(a.to(DEV), 1, 128)
+        qw, sw = Q.quant_fp8_blocks(w.to(DEV), 128, 128)
+        ref = OG.ref_fp8_groupwise(np_u8(qa), np_f32(sa), np_u8(qw), np_f32(sw))
+    else:
+        qa, sa = Q.quant_fp8_tensor(a.to(DEV))
+        qw, sw = Q.quant_fp8_tensor(w.to(DEV))
+        ref = OG.ref_fp8_per_tensor(np_u8(qa), np_f32(sa)[0], np_u8(qw), np_f32(sw)[0])
+    c = G.fp8_gemm_packed(qa, qw, sa, sw, block=block, out_dtype=out_dtype)
+    assert c.dtype == out_dtype
+    assert_close(c, ref, what=f"fp8 persistent block={block} {m}x{n}x{k} {out_dtype}")
+
+
 # K % 512 == 0: the block-scaled kernel with the activation-scale ring (two
 # slots of four 128-K groups), over 2, 3 and 9 scale sets, ragged M/N.
 BLOCK_RING_SHAPES = [(4096, 3840, 1024), (4000, 4100, 1536), (3840, 4096, 4608)]
