@@ -34,10 +34,11 @@
 // s_g.  This is the group-partial sum of cuda/gemm/fp8_gemm.cu:84-97 up to
 // fp32 rounding.
 //
-// Epilogue: each wave converts its accumulators (v_cvt_pk_bf16_f32) and
-// stores 8 bytes (4 columns of one row) per store straight from registers.
-// Stores share vmcnt with the ring's loads; the next pair wait (vmcnt(0))
-// also waits for them.
+// Epilogue: each wave converts its accumulators (v_cvt_pk_bf16_f32),
+// regroups them across lanes (v_permlane32_swap, v_permlane16_swap) and
+// stores 16 bytes per lane, 16 rows x 64 contiguous bytes per store, straight
+// from registers.  Stores share vmcnt with the ring's loads; the next pair
+// wait (vmcnt(0)) also waits for them.
 #include <type_traits>
 
 #include "pipe_core.h"
@@ -197,6 +198,7 @@ void gemm_persist_kernel(const GemmArgs p) {
     s1 = *p.ga;
     s2 = *p.gb;
   }
+  const float s12 = s1 * s2;
   const int nbm = (p.M + Cfg::BM - 1) / Cfg::BM, nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
   const int ntiles = nbm * nbn;
   const int b = blockIdx.x, grid = gridDim.x;
@@ -264,11 +266,12 @@ void gemm_persist_kernel(const GemmArgs p) {
     int m0, n0;
     tile_origin(t, m0, n0);
     const int c0 = n0 + wn * Cfg::WN + 4 * h;
-    const bool interior = m0 + Cfg::BM <= p.M && n0 + Cfg::BN <= p.N && (p.ldc % 4) == 0 &&
+    const bool interior = m0 + Cfg::BM <= p.M && n0 + Cfg::BN <= p.N &&
+                          (p.ldc % (p.out_f32 ? 4 : 8)) == 0 &&
                           (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
     auto val = [&](int i, int j, int r) __attribute__((always_inline)) {
       float x = acc[i][j][r];
-      if constexpr (Cfg::MODE == MODE_FP8_TENSOR) x = (x * s1) * s2;
+      if constexpr (Cfg::MODE == MODE_FP8_TENSOR) x = x * s12;
       else if constexpr (Cfg::BLOCK) x = x * sc[i];
       return x;
     };
@@ -286,15 +289,48 @@ void gemm_persist_kernel(const GemmArgs p) {
                   make_float4(val(i, j, 4 * q), val(i, j, 4 * q + 1), val(i, j, 4 * q + 2),
                               val(i, j, 4 * q + 3));
         } else {
-          uint16_t *dst = static_cast<uint16_t *>(p.c) + row * p.ldc + c0;
+          // Lane (h, r32) holds columns 8q + 4h .. +3 (q = 0..3) of row r32
+          // of each 32x32 block.  Two lane exchanges regroup them so that
+          // lane (h, g, r16), r32 = 16g + r16, holds the 8 columns 8(h+2g)
+          // .. +7 of rows r16 (X) and 16 + r16 (Y): each store then writes
+          // 16 rows x 64 contiguous bytes instead of 32 rows x 16 bytes.
+          const int r16 = r32 & 15, seg = h + 2 * (r32 >> 4);
+          uint16_t *dst = static_cast<uint16_t *>(p.c) +
+                          (int64_t)(m0 + wm * Cfg::WM + i * 32 + r16) * p.ldc + n0 +
+                          wn * Cfg::WN + 8 * seg;
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
+          for (int j = 0; j < TN; ++j) {
+            uint32_t P[4][2];
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
-              const uint32_t lo = pack_bf16x2(val(i, j, 4 * q), val(i, j, 4 * q + 1));
-              const uint32_t hi = pack_bf16x2(val(i, j, 4 * q + 2), val(i, j, 4 * q + 3));
-              *reinterpret_cast<uint2 *>(dst + j * 32 + q * 8) = make_uint2(lo, hi);
+              P[q][0] = pack_bf16x2(val(i, j, 4 * q), val(i, j, 4 * q + 1));
+              P[q][1] = pack_bf16x2(val(i, j, 4 * q + 2), val(i, j, 4 * q + 3));
             }
+            // upper half of the first operand <-> lower half of the second:
+            // lane h=0 ends with columns 8q0 .. +7, lane h=1 with 8q0+8 .. +7
+            uint32_t U[4], W[4];
+#pragma unroll
+            for (int k = 0; k < 2; ++k) {
+              const auto u = __builtin_amdgcn_permlane32_swap(P[0][k], P[1][k], false, false);
+              const auto w = __builtin_amdgcn_permlane32_swap(P[2][k], P[3][k], false, false);
+              U[k] = u[0];
+              U[2 + k] = u[1];
+              W[k] = w[0];
+              W[2 + k] = w[1];
+            }
+            // odd 16-lane groups of U <-> even groups of W
+            uint4 X, Y;
+            {
+              const auto t0 = __builtin_amdgcn_permlane16_swap(U[0], W[0], false, false);
+              const auto t1 = __builtin_amdgcn_permlane16_swap(U[1], W[1], false, false);
+              const auto t2 = __builtin_amdgcn_permlane16_swap(U[2], W[2], false, false);
+              const auto t3 = __builtin_amdgcn_permlane16_swap(U[3], W[3], false, false);
+              X = make_uint4(t0[0], t1[0], t2[0], t3[0]);
+              Y = make_uint4(t0[1], t1[1], t2[1], t3[1]);
+            }
+            *reinterpret_cast<uint4 *>(dst + j * 32) = X;
+            *reinterpret_cast<uint4 *>(dst + 16 * p.ldc + j * 32) = Y;
+          }
         }
       }
     } else {
