@@ -176,6 +176,14 @@ struct Frag {
   }
 };
 
+// Lane id from v_mbcnt in volatile asm, so that the compiler cannot merge it
+// with an earlier copy and keep that live.
+DSL_DEV int lane_id() {
+  int x;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(x));
+  return x;
+}
+
 // MFMAs of row i: W fragments from fb, A from fa (operands swapped).
 template <class Cfg>
 DSL_DEV void mma_row(const Frag<Cfg> &fa, const Frag<Cfg> &fb, int i, v16f (&acc)[Cfg::TM][Cfg::TN]) {
@@ -254,8 +262,9 @@ void gemm_persist_kernel(const GemmArgs p) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   float sc[TM];           // block: s_g(row) of the group the accumulator is expressed in
+  float rt[TM];           // block: s_g / s_{g+1} at a group boundary
 #pragma unroll
-  for (int i = 0; i < TM; ++i) sc[i] = 1.f;
+  for (int i = 0; i < TM; ++i) sc[i] = rt[i] = 1.f;
 
   // ---- epilogue of local tile t: convert, scale, store from registers.
   // Lane (r32, h) stores, for each of its rows, 4 consecutive columns per
@@ -263,6 +272,10 @@ void gemm_persist_kernel(const GemmArgs p) {
   // case) take an unchecked path with one row pointer and constant column
   // offsets; edge tiles check every element.
   auto epilogue = [&](int t) __attribute__((always_inline)) {
+    // the lane's coordinates are formed afresh (opaque to CSE): values kept
+    // from the prologue would be live across the whole loop and spill
+    const int eln = pers::lane_id();
+    const int r32 = eln & 31, h = eln >> 5;
     int m0, n0;
     tile_origin(t, m0, n0);
     const int c0 = n0 + wn * Cfg::WN + 4 * h;
@@ -387,12 +400,21 @@ void gemm_persist_kernel(const GemmArgs p) {
   // First step of local pair gp: MFMAs of its half 0 (fragments in fb[0] /
   // fa), reads of its half 1 from the same slot (landed and published with
   // the pair).
-  auto step0 = [&](int gp) __attribute__((always_inline)) {
+  // RESCALE (block, not on a tile's first pair): the accumulator still
+  // carries the previous group's scale; each row is brought to this group's
+  // right before its first MFMA of the group, overlapping the MFMAs of the
+  // row before and reading results that completed a step ago.
+  auto step0 = [&](auto rescale_tag, int gp) __attribute__((always_inline)) {
+    constexpr bool RESCALE = Cfg::BLOCK && decltype(rescale_tag)::value;
     const uint8_t *st = smem + (gp & 1) * Cfg::PAIR;
     fb[1].load_b(st, 1, wn, r32, h);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
+      if constexpr (RESCALE) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] *= rt[i];
+      }
       pers::mma_row<Cfg>(fa, fb[0], i, acc);
       fa.load_a(st, 1, i, wm, r32, h);
       __builtin_amdgcn_sched_barrier(0);
@@ -413,7 +435,7 @@ void gemm_persist_kernel(const GemmArgs p) {
     const uint32_t islot = slot_of(ig);
     const int qq = iq < nkp ? iq : nkp - 1;
     if constexpr (KIND != 2) fb[0].load_b(stn, 0, wn, r32, h);
-    float sn[TM], rt[TM];
+    float sn[TM];
     if constexpr (Cfg::BLOCK) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) sn[i] = block_scale(stn, i);
@@ -425,25 +447,16 @@ void gemm_persist_kernel(const GemmArgs p) {
 #pragma unroll
       for (int j = i * D / TM; j < (i + 1) * D / TM; ++j) ring.issue_one(j, qq, islot);
       if constexpr (KIND != 2) fa.load_a(stn, 0, i, wm, r32, h);
-      if constexpr (Cfg::BLOCK && KIND == 1) {
-        // row i-1 had its last MFMA of the group issued one row ago
-        if (i == 1) {
-#pragma unroll
-          for (int u = 0; u < TM; ++u) {
-            rt[u] = sc[u] * __builtin_amdgcn_rcpf(sn[u]);
-            sc[u] = sn[u];
-          }
-        }
-        if (i >= 1) {
-#pragma unroll
-          for (int j = 0; j < TN; ++j) acc[i - 1][j] *= rt[i - 1];
-        }
-      }
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (Cfg::BLOCK && KIND == 1) {
+      // the group ends: factors that bring the accumulator from this
+      // group's scale to the next group's, applied by the next step0
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[TM - 1][j] *= rt[TM - 1];
+      for (int u = 0; u < TM; ++u) {
+        rt[u] = sc[u] * __builtin_amdgcn_rcpf(sn[u]);
+        sc[u] = sn[u];
+      }
     }
     ++iq;
     ++ig;
@@ -463,13 +476,16 @@ void gemm_persist_kernel(const GemmArgs p) {
   // carries MFMAs (the accumulators would be copied at the join).
   using K1 = std::integral_constant<int, 1>;
   using K2 = std::integral_constant<int, 2>;
+  using NoRescale = std::false_type;
+  using Rescale = std::true_type;
   int gp = 0;
   for (int t = 0; t < my_tiles; ++t) {
-    for (int q = 0; q + 1 < nkp; ++q, ++gp) {
-      step0(gp);
+    step0(NoRescale{}, gp);
+    for (int q = 0; q + 1 < nkp; ++q) {
       step1(K1{}, gp);
+      ++gp;
+      step0(Rescale{}, gp);
     }
-    step0(gp);
     step1(K2{}, gp);
     ++gp;
   }
