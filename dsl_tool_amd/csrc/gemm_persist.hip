@@ -1,5 +1,5 @@
 // Persistent pipelined GEMM for gfx950 (FP8 per-tensor, FP8 1x128/128x128
-// block-scaled): C[M,N] = A[M,K] . W[N,K]^T, both operands K-major.
+// block-scaled, MXFP4): C[M,N] = A[M,K] . W[N,K]^T, both operands K-major.
 //
 // One workgroup per CU walks its output tiles (tile v = blockIdx.x +
 // r * gridDim.x in the XCD-aware order of tile_coords), 256x256 with 8 waves
@@ -26,13 +26,24 @@
 // until the next step), which keeps the 128 fp32 accumulators, both
 // fragment sets and the copy plan within 256 VGPRs.
 //
-// Scales.  FP8 block: a pair is exactly one 128-K scale group, and its slot
-// carries sa[row][g] for the tile's 256 rows and sb[nb][g] for the tile's
-// two 128-column weight blocks.  The accumulator is kept in units of the
-// current group's scale s_g(m) = sa[m][g] * sb[n/128][g] and multiplied by
-// s_g / s_{g+1} at each group boundary; the epilogue multiplies by the last
-// s_g.  This is the group-partial sum of cuda/gemm/fp8_gemm.cu:84-97 up to
-// fp32 rounding.
+// Scales move 16 bytes per row at a time, in a ring of their own: one
+// "quad" holds a row's scales for QP pairs (FP8 block: four fp32 group
+// scales, QP = 4; MXFP4: sixteen E8M0 bytes, QP = 2), so one
+// global_load_lds_dwordx4 per 64 rows fetches QP pairs' worth.  Per-pair
+// 4-byte loads would touch one cache line per row for every pair (50% more
+// L1 requests than the operands for FP8 block, 200% for MXFP4).  Two quad
+// slots alternate; quad c+2 is copied with the first pair of that quad,
+// after every wave has read quad c.
+//
+// FP8 block: a pair is exactly one 128-K scale group.  The accumulator is
+// kept in units of the current group's scale s_g(m) = sa[m][g] * sb[n/128][g]
+// and multiplied by s_g / s_{g+1} at each group boundary; the epilogue
+// multiplies by the last s_g.  This is the group-partial sum of
+// cuda/gemm/fp8_gemm.cu:84-97 up to fp32 rounding.
+//
+// MXFP4: each 64-byte step is two 32x32x64 FP4 MFMAs per tile, the E8M0
+// block scales of W and A go into the MFMA's scale operands (exact powers
+// of two), cuda/gemm/fp4_gemm.cu semantics.
 //
 // Epilogue: each wave converts its accumulators (v_cvt_pk_bf16_f32),
 // regroups them across lanes (v_permlane32_swap, v_permlane16_swap) and
@@ -52,19 +63,24 @@ struct PersCfg {
   static constexpr int NW = WGM * WGN, NT = NW * 64, OCC = 2;
   static constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
   static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;
+  static constexpr bool MX = MODE == MODE_MXFP4;
+  static constexpr bool SCALED = BLOCK || MX;
   static constexpr int PKB = 128;                      // K bytes per pair (per row)
   static constexpr int CH = PKB / 16, RPI = 1024 / PKB;  // chunks per row, rows per DMA
   static constexpr int A_BYTES = BM * PKB, B_BYTES = BN * PKB;
-  static constexpr int SA_BYTES = BLOCK ? BM * 4 : 0;  // sa[row][g] of the pair's group
-  static constexpr int SB_BYTES = BLOCK ? 256 : 0;     // sb of the two column blocks (8 B used)
-  static constexpr int PAIR = A_BYTES + B_BYTES + SA_BYTES + SB_BYTES;
-  static constexpr int LDS = 2 * PAIR;
+  static constexpr int PAIR = A_BYTES + B_BYTES;
+  // scale quads: 16 bytes per row cover QP pairs
+  static constexpr int QP = BLOCK ? 4 : 2;
+  static constexpr int SQA = SCALED ? BM * 16 : 0;                  // [row][16 B]
+  static constexpr int SQB = BLOCK ? 1024 : (MX ? BN * 16 : 0);     // block: [2 blocks][16 B] (+copies)
+  static constexpr int SQ = SQA + SQB;
+  static constexpr int LDS = 2 * PAIR + 2 * SQ;
   static constexpr int A_DMA = A_BYTES / 1024, B_DMA = B_BYTES / 1024;
-  static constexpr int SA_DMA = SA_BYTES / 256, SB_DMA = SB_BYTES / 256;
+  static constexpr int SA_DMA = SQA / 1024, SB_DMA = SQB / 1024;
   static constexpr int DATA_DMA = A_DMA + B_DMA, SC_DMA = SA_DMA + SB_DMA;
   static constexpr int DD = DATA_DMA / NW, DS = (SC_DMA + NW - 1) / NW, D = DD + DS;
   static_assert(DATA_DMA % NW == 0 && A_DMA % DD == 0, "whole waves per operand");
-  static_assert(DS <= 1, "at most one scale DMA per wave and pair");
+  static_assert(DS <= 1, "at most one scale DMA per wave and quad");
   static_assert(LDS <= 160 * 1024, "LDS budget");
   static_assert(!BLOCK || (WN <= 128 && 128 % WN == 0), "one weight-scale block per wave");
 };
@@ -78,23 +94,41 @@ DSL_DEV void dma16(const uint8_t *base, uint32_t voff, uint32_t lds) {
                "s"(base), "s"(lds)
                : "memory", "m0");
 }
-DSL_DEV void dma4(const uint8_t *base, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" ::"v"(voff),
-               "s"(base), "s"(lds)
-               : "memory", "m0");
+// dma16 when the wave-uniform `on` is non-zero.  The test is a branch
+// inside the asm, so the compiler sees straight-line code: a branch in the
+// source splits the step into basic blocks, and the compiler then gathers
+// all of the step's copies ahead of its MFMAs.
+DSL_DEV void dma16_if(int on, const uint8_t *base, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_cmp_eq_u32 %3, 0\n\t"
+      "s_cbranch_scc1 .Ldma_skip_%=\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, %1\n"
+      ".Ldma_skip_%=:" ::"v"(voff),
+      "s"(base), "s"(lds), "s"(on)
+      : "memory", "m0", "scc");
 }
 
-// Copy plan of one thread for the tile at (m0, n0): DD operand DMAs (8 rows
-// x 128 bytes each) and, for waves below SC_DMA, one scale-word DMA per
-// pair.  A wave's operand DMAs all read the same operand (waves below
-// A_DMA/DD copy A, the others W), so one uniform base serves them; the lane
-// offsets are formed at issue time from the lane's row and chunk (a few
-// VALU ops beside the MFMAs instead of DD live registers).
-// `full`: this wave issues all D instructions.
+// Lane id from v_mbcnt in volatile asm, so that the compiler cannot merge it
+// with an earlier copy and keep that live.
+DSL_DEV int lane_id() {
+  int x;
+  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(x));
+  return x;
+}
+
+// Copy plan of one thread for the tile at (m0, n0): DD operand DMAs per pair
+// (8 rows x 128 bytes each) and, for waves below SC_DMA, one scale DMA per
+// quad (64 rows x 16 bytes).  A wave's operand DMAs all read the same
+// operand (waves below A_DMA/DD copy A, the others W), so one uniform base
+// serves them; the lane offsets are formed at issue time from the lane's row
+// and chunk (a few VALU ops beside the MFMAs instead of DD live registers).
+// `full`: this wave has a scale DMA.
 template <class Cfg>
 struct Ring {
   const uint8_t *dbase;          // operand rows of the tile, pair 0
-  const uint8_t *sbase;          // scale words of the tile, pair 0
+  const uint8_t *sbase;          // scale rows of the tile, quad 0
   int wrow;                      // the wave's first tile row (uniform)
   int lim;                       // last valid tile row of the operand (uniform)
   int kb;
@@ -106,7 +140,7 @@ struct Ring {
 
   DSL_DEV void target(const GemmArgs &p, int m0, int n0, int wave_, int lane) {
     wave = wave_;
-    full = Cfg::DS == 0 || wave < Cfg::SC_DMA;
+    full = Cfg::DS > 0 && wave < Cfg::SC_DMA;
     const bool isA = wave * Cfg::DD < Cfg::A_DMA;
     const int r0 = isA ? m0 : n0;
     lim = (isA ? p.M : p.N) - 1 - r0;
@@ -119,46 +153,62 @@ struct Ring {
     vchunk = (uint32_t)(((lane % Cfg::CH) ^ pipe::swz<Cfg::PKB>(wrow + (int)vsub)) * 16);
     sbase = p.a;
     soff = 0;
-    if constexpr (Cfg::DS > 0) {
-      const int64_t rowb = (int64_t)(p.K / 128) * 4;   // bytes per scale row
+    if constexpr (Cfg::SCALED) {
+      // bytes per scale row: fp32 per 128-K group, or E8M0 per 32 elements
+      const int64_t rowb = Cfg::BLOCK ? (int64_t)(p.K / 128) * 4 : (int64_t)(p.K / 32);
       if (wave < Cfg::SA_DMA) {
         int grow = m0 + wave * 64 + lane;
         grow = grow < p.M ? grow : p.M - 1;
         sbase = static_cast<const uint8_t *>(p.sa) + m0 * rowb;
         soff = (uint32_t)((grow - m0) * rowb);
-      } else {
+      } else if (Cfg::BLOCK) {
         // lanes 0 / 1: the tile's two 128-column blocks (others repeat them)
         const int nbb = (p.N + 127) / 128, b0 = n0 / 128;
         int blk = b0 + (lane & 1);
         blk = blk < nbb ? blk : nbb - 1;
         sbase = static_cast<const uint8_t *>(p.sb) + b0 * rowb;
         soff = (uint32_t)((blk - b0) * rowb);
+      } else {
+        int grow = n0 + (wave - Cfg::SA_DMA) * 64 + lane;
+        grow = grow < p.N ? grow : p.N - 1;
+        sbase = static_cast<const uint8_t *>(p.sb) + n0 * rowb;
+        soff = (uint32_t)((grow - n0) * rowb);
       }
     }
   }
 
-  // DMA instruction j of tile-local pair q into the pair slot at `slot`
-  DSL_DEV void issue_one(int j, int q, uint32_t slot) const {
-    if (j < Cfg::DD) {
-      int r = (int)vsub + (wrow + j * Cfg::RPI);
-      r = r < lim ? r : lim;           // rows past the edge re-read the last row
-      // swz(wrow + j*RPI + vsub) = swz(wrow + vsub) ^ swz(j*RPI): the row
-      // offset j*RPI only flips bit 2 of the swizzle, by the parity of j
-      const uint32_t ch = vchunk ^ (uint32_t)(pipe::swz<Cfg::PKB>(j * Cfg::RPI) * 16);
-      dma16(dbase + (int64_t)q * Cfg::PKB, (uint32_t)(r * kb) + ch,
-            slot + (uint32_t)((wave * Cfg::DD + j) * 1024));
-    } else if (full) {
-      const bool sa = wave < Cfg::SA_DMA;
-      const uint32_t dst = Cfg::A_BYTES + Cfg::B_BYTES + (sa ? wave * 256 : Cfg::SA_BYTES);
-      dma4(sbase + (int64_t)q * 4, soff, slot + dst);   // group q: one float per row
-    }
+  // operand DMA j of tile-local pair q into the pair slot at `slot`
+  DSL_DEV void issue_data(int j, int q, uint32_t slot) const {
+    int r = (int)vsub + (wrow + j * Cfg::RPI);
+    r = r < lim ? r : lim;           // rows past the edge re-read the last row
+    // swz(wrow + j*RPI + vsub) = swz(wrow + vsub) ^ swz(j*RPI): the row
+    // offset j*RPI only flips bit 2 of the swizzle, by the parity of j
+    const uint32_t ch = vchunk ^ (uint32_t)(pipe::swz<Cfg::PKB>(j * Cfg::RPI) * 16);
+    // r < 256 and Kb < 2^24 (checked at launch): a full-rate 24-bit multiply
+    dma16(dbase + (int64_t)q * Cfg::PKB, __umul24((uint32_t)r, (uint32_t)kb) + ch,
+          slot + (uint32_t)((wave * Cfg::DD + j) * 1024));
+  }
+  // the wave's scale DMA of tile-local quad c into the quad slot at
+  // `sslot`, when `on` (uniform)
+  DSL_DEV void issue_scales(int on, int c, uint32_t sslot) const {
+    const uint32_t dst = (uint32_t)(wave * 1024);   // SA parts, then SB right after
+    dma16_if(on, sbase + (int64_t)c * 16, soff, sslot + dst);
   }
 };
 
 // Operand fragments of one 64-byte step (half p of a pair slot) of one wave:
-// lane l holds row l%32 of each 32-row tile and 32 bytes of K (two 16-byte
-// chunks, K half h = l/32), the layout of v_mfma_scale_f32_32x32x64_f8f6f4.
-template <class Cfg>
+// lane l holds row l%32 of each 32-row tile and 32 bytes of K, the layout
+// of v_mfma_scale_f32_32x32x64_f8f6f4.  FP8: one MFMA per tile, K half
+// h = l/32 (two 16-byte chunks 4p+2h, 4p+2h+1).
+//
+// MXFP4: two MFMAs per tile and step (kk = 0, 1); lane half h holds chunk
+// 4h + 2p + kk of the pair = 32 elements = one E8M0 block.  Over the pair's
+// four MFMAs (p, kk) the two lane halves cover blocks {2p+kk, 4+2p+kk}, all
+// eight once, in the same order for A and W (a permutation of the K sum).
+// With that order lane half h takes all its scales from word h of the
+// row's two pair words, byte 2p + kk: the MFMA's op_sel selects it, so the
+// word goes to the MFMA as read, once per pair.
+template <class Cfg, bool MX = Cfg::MX>
 struct Frag {
   v8i a[Cfg::TM], b[Cfg::TN];
   static DSL_DEV v8i ld(const uint8_t *base, int row, int p, int h) {
@@ -167,30 +217,74 @@ struct Frag {
     const v4i hi = *reinterpret_cast<const v4i *>(base + row * Cfg::PKB + (((c0 + 1) ^ s) << 4));
     return (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   }
-  DSL_DEV void load_a(const uint8_t *slot, int p, int i, int wm, int r32, int h) {
+  DSL_DEV void load_a(const uint8_t *slot, const uint8_t *, int, int p, int i, int wm, int r32,
+                      int h) {
     a[i] = ld(slot, wm * Cfg::WM + i * 32 + r32, p, h);
   }
-  DSL_DEV void load_b(const uint8_t *slot, int p, int wn, int r32, int h) {
+  DSL_DEV void load_b(const uint8_t *slot, const uint8_t *, int, int p, int wn, int r32, int h) {
 #pragma unroll
     for (int j = 0; j < Cfg::TN; ++j) b[j] = ld(slot + Cfg::A_BYTES, wn * Cfg::WN + j * 32 + r32, p, h);
   }
+  DSL_DEV void share_scales(const Frag &) {}
 };
 
-// Lane id from v_mbcnt in volatile asm, so that the compiler cannot merge it
-// with an earlier copy and keep that live.
-DSL_DEV int lane_id() {
-  int x;
-  asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(x));
-  return x;
-}
-
-// MFMAs of row i: W fragments from fb, A from fa (operands swapped).
 template <class Cfg>
-DSL_DEV void mma_row(const Frag<Cfg> &fa, const Frag<Cfg> &fb, int i, v16f (&acc)[Cfg::TM][Cfg::TN]) {
+struct Frag<Cfg, true> {
+  v4i a[Cfg::TM][2], b[Cfg::TN][2];
+  int as[Cfg::TM], bs[Cfg::TN];     // scale word h of the row's pair
+  static DSL_DEV v4i ld(const uint8_t *base, int row, int c) {
+    return *reinterpret_cast<const v4i *>(base + row * Cfg::PKB + ((c ^ pipe::swz<Cfg::PKB>(row)) << 4));
+  }
+  // sq: quad slot; qw: first scale word of the pair in the row's 16 bytes
+  // (2 x quad-local pair index).  The scale word is read with half 0.
+  DSL_DEV void load_a(const uint8_t *slot, const uint8_t *sq, int qw, int p, int i, int wm,
+                      int r32, int h) {
+    const int row = wm * Cfg::WM + i * 32 + r32;
+    a[i][0] = ld(slot, row, 4 * h + 2 * p);
+    a[i][1] = ld(slot, row, 4 * h + 2 * p + 1);
+    if (p == 0) as[i] = *reinterpret_cast<const int *>(sq + row * 16 + (qw + h) * 4);
+  }
+  DSL_DEV void load_b(const uint8_t *slot, const uint8_t *sq, int qw, int p, int wn, int r32,
+                      int h) {
 #pragma unroll
-  for (int j = 0; j < Cfg::TN; ++j)
-    acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb.b[j], fa.a[i], acc[i][j], 0, 0,
-                                                                0, 0, 0, 0);
+    for (int j = 0; j < Cfg::TN; ++j) {
+      const int row = wn * Cfg::WN + j * 32 + r32;
+      b[j][0] = ld(slot + Cfg::A_BYTES, row, 4 * h + 2 * p);
+      b[j][1] = ld(slot + Cfg::A_BYTES, row, 4 * h + 2 * p + 1);
+      if (p == 0) bs[j] = *reinterpret_cast<const int *>(sq + Cfg::SQA + row * 16 + (qw + h) * 4);
+    }
+  }
+  // half 1 of a pair uses the scale words read with its half 0
+  DSL_DEV void share_scales(const Frag &half0) {
+#pragma unroll
+    for (int j = 0; j < Cfg::TN; ++j) bs[j] = half0.bs[j];
+  }
+};
+
+// MFMAs of row i for half P of a pair: W fragments from fb, A from fa
+// (operands swapped).
+template <class Cfg, int P>
+DSL_DEV void mma_row(const Frag<Cfg> &fa, const Frag<Cfg> &fb, int i, v16f (&acc)[Cfg::TM][Cfg::TN]) {
+  if constexpr (Cfg::MX) {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+      for (int j = 0; j < Cfg::TN; ++j) {
+        const v4i &w4 = fb.b[j][kk], &a4 = fa.a[i][kk];
+        const v8i w8 = {w4[0], w4[1], w4[2], w4[3], 0, 0, 0, 0};
+        const v8i a8 = {a4[0], a4[1], a4[2], a4[3], 0, 0, 0, 0};
+        acc[i][j] = kk == 0 ? __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                                  w8, a8, acc[i][j], 4, 4, 2 * P, fb.bs[j], 2 * P, fa.as[i])
+                            : __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+                                  w8, a8, acc[i][j], 4, 4, 2 * P + 1, fb.bs[j], 2 * P + 1,
+                                  fa.as[i]);
+      }
+  } else {
+#pragma unroll
+    for (int j = 0; j < Cfg::TN; ++j)
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb.b[j], fa.a[i], acc[i][j], 0,
+                                                                  0, 0, 0, 0, 0);
+  }
 }
 
 }  // namespace pers
@@ -198,7 +292,7 @@ DSL_DEV void mma_row(const Frag<Cfg> &fa, const Frag<Cfg> &fb, int i, v16f (&acc
 template <class Cfg>
 __global__ __launch_bounds__(Cfg::NT) __attribute__((amdgpu_waves_per_eu(Cfg::OCC, Cfg::OCC)))
 void gemm_persist_kernel(const GemmArgs p) {
-  constexpr int D = Cfg::D, TM = Cfg::TM, TN = Cfg::TN;
+  constexpr int TM = Cfg::TM, TN = Cfg::TN;
   __shared__ __align__(16) uint8_t smem[Cfg::LDS];
   // per-tensor scales first: no global load may follow the DMA asm
   float s1 = 1.f, s2 = 1.f;
@@ -228,9 +322,10 @@ void gemm_persist_kernel(const GemmArgs p) {
   // issue cursor: the next pair to copy is pair iq of local tile it, global
   // pair number ig (its slot: ig % 2).  Past the workgroup's last pair the
   // cursor stays on it, so every step copies a pair (into a slot nobody reads
-  // again) and all steps have the same shape.
+  // again) and all steps have the same shape; those repeats copy no scales.
+  // iqc counts the quads begun (their slot: iqc % 2).
   pers::Ring<Cfg> ring;
-  int it = 0, iq = 0, ig = 0;
+  int it = 0, iq = 0, ig = 0, iqc = -1;
   {
     int m0, n0;
     tile_origin(0, m0, n0);
@@ -246,12 +341,27 @@ void gemm_persist_kernel(const GemmArgs p) {
     }
   };
   auto slot_of = [&](int gp) __attribute__((always_inline)) { return lds0 + (uint32_t)((gp & 1) * Cfg::PAIR); };
+  uint8_t *const squad = smem + 2 * Cfg::PAIR;   // the two scale-quad slots
+  // issue the operand DMAs of the cursor's pair, spread over rows i of a
+  // step (all of them when i < 0), and its scale quad if it begins one
+  auto issue_part = [&](int i, int qq, uint32_t islot, bool quad) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < Cfg::DD; ++j)
+      if (i < 0 || (j >= i * Cfg::DD / TM && j < (i + 1) * Cfg::DD / TM)) ring.issue_data(j, qq, islot);
+    if constexpr (Cfg::SCALED) {
+      if (i < 0 || i == TM - 1)
+        ring.issue_scales(__builtin_amdgcn_readfirstlane((int)(quad && ring.full)), qq / Cfg::QP,
+                          pipe::lds_addr(squad) + (uint32_t)((iqc & 1) * Cfg::SQ));
+    }
+  };
 
-  // block scales of a lane's rows in the wave's column block, from a pair slot
-  auto block_scale = [&](const uint8_t *slot, int i) __attribute__((always_inline)) {
-    const float *sa = reinterpret_cast<const float *>(slot + Cfg::A_BYTES + Cfg::B_BYTES);
-    const float *sb = sa + Cfg::BM;
-    return sa[wm * Cfg::WM + i * 32 + r32] * sb[(wn * Cfg::WN) / 128];
+  // block scale of a lane's row i in the wave's column block for tile-local
+  // pair q, from the quad slot `sq`
+  auto block_scale = [&](const uint8_t *sq, int q, int i) __attribute__((always_inline)) {
+    const float *sa = reinterpret_cast<const float *>(sq);
+    const float *sb = reinterpret_cast<const float *>(sq + Cfg::SQA);
+    const int g4 = q % Cfg::QP;
+    return sa[(wm * Cfg::WM + i * 32 + r32) * 4 + g4] * sb[((wn * Cfg::WN) / 128) * 4 + g4];
   };
 
   v16f acc[TM][TN];
@@ -374,27 +484,39 @@ void gemm_persist_kernel(const GemmArgs p) {
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
   };
 
-  // ---- prologue: pairs 0 and 1, then the fragments of step 0
+  // issue the cursor's pair (rows i of a step, or all when i < 0)
+  auto issue_next = [&](int i, bool &quad, int &qq, uint32_t &islot) __attribute__((always_inline)) {
+    issue_pair_prep();
+    quad = iq < nkp && iq % Cfg::QP == 0;
+    if (quad) ++iqc;
+    qq = iq < nkp ? iq : nkp - 1;
+    islot = slot_of(ig);
+    if (i < 0) issue_part(-1, qq, islot, quad);
+  };
+
+  // ---- prologue: pairs 0 and 1 (pair 1 never begins a quad: quads are
+  // whole and QP >= 2), then the fragments of step 0
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    issue_pair_prep();
-    const uint32_t slot = slot_of(ig);
-    const int qq = iq < nkp ? iq : nkp - 1;
-#pragma unroll
-    for (int j = 0; j < D; ++j) ring.issue_one(j, qq, slot);
+    bool quad;
+    int qq;
+    uint32_t islot;
+    issue_next(-1, quad, qq, islot);
     ++iq;
     ++ig;
   }
-  if (ring.full) pipe::wait_vmcnt<D>();       // pair 0 landed, pair 1 may be in flight
-  else pipe::wait_vmcnt<D - 1>();
+  pipe::wait_vmcnt<Cfg::DD>();                // pair 0 landed, pair 1 may be in flight
   __syncthreads();
+  // compute cursor: the pair whose half 0 was read last is tile-local pair
+  // cq, in quad slot cqc % 2
+  int cq = 0, cqc = 0;
   pers::Frag<Cfg> fa, fb[2];
-  fb[0].load_b(smem, 0, wn, r32, h);
+  fb[0].load_b(smem, squad, 0, 0, wn, r32, h);
 #pragma unroll
-  for (int i = 0; i < TM; ++i) fa.load_a(smem, 0, i, wm, r32, h);
+  for (int i = 0; i < TM; ++i) fa.load_a(smem, squad, 0, 0, i, wm, r32, h);
   if constexpr (Cfg::BLOCK) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) sc[i] = block_scale(smem, i);
+    for (int i = 0; i < TM; ++i) sc[i] = block_scale(squad, 0, i);
   }
 
   // First step of local pair gp: MFMAs of its half 0 (fragments in fb[0] /
@@ -407,7 +529,10 @@ void gemm_persist_kernel(const GemmArgs p) {
   auto step0 = [&](auto rescale_tag, int gp) __attribute__((always_inline)) {
     constexpr bool RESCALE = Cfg::BLOCK && decltype(rescale_tag)::value;
     const uint8_t *st = smem + (gp & 1) * Cfg::PAIR;
-    fb[1].load_b(st, 1, wn, r32, h);
+    const uint8_t *sq = squad + (cqc & 1) * Cfg::SQ;
+    const int sw = (cq % Cfg::QP) * 2;              // MX: the pair's scale words
+    fb[1].load_b(st, sq, sw, 1, wn, r32, h);
+    fb[1].share_scales(fb[0]);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
@@ -415,8 +540,8 @@ void gemm_persist_kernel(const GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] *= rt[i];
       }
-      pers::mma_row<Cfg>(fa, fb[0], i, acc);
-      fa.load_a(st, 1, i, wm, r32, h);
+      pers::mma_row<Cfg, 0>(fa, fb[0], i, acc);
+      fa.load_a(st, sq, sw, 1, i, wm, r32, h);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -431,22 +556,28 @@ void gemm_persist_kernel(const GemmArgs p) {
     pipe::wait_lds();
     __syncthreads();
     const uint8_t *stn = smem + ((gp + 1) & 1) * Cfg::PAIR;
-    issue_pair_prep();
-    const uint32_t islot = slot_of(ig);
-    const int qq = iq < nkp ? iq : nkp - 1;
-    if constexpr (KIND != 2) fb[0].load_b(stn, 0, wn, r32, h);
+    bool quad;
+    int qq;
+    uint32_t islot;
+    issue_next(0, quad, qq, islot);
+    // the compute cursor moves to pair gp+1 (the next tile's first pair
+    // after KIND 2)
+    cq = KIND == 2 ? 0 : cq + 1;
+    if (cq % Cfg::QP == 0) ++cqc;
+    const uint8_t *sqn = squad + (cqc & 1) * Cfg::SQ;
+    const int sw = (cq % Cfg::QP) * 2;              // MX: the pair's scale words
+    if constexpr (KIND != 2) fb[0].load_b(stn, sqn, sw, 0, wn, r32, h);
     float sn[TM];
     if constexpr (Cfg::BLOCK) {
 #pragma unroll
-      for (int i = 0; i < TM; ++i) sn[i] = block_scale(stn, i);
+      for (int i = 0; i < TM; ++i) sn[i] = block_scale(sqn, cq, i);
     }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      pers::mma_row<Cfg>(fa, fb[1], i, acc);
-#pragma unroll
-      for (int j = i * D / TM; j < (i + 1) * D / TM; ++j) ring.issue_one(j, qq, islot);
-      if constexpr (KIND != 2) fa.load_a(stn, 0, i, wm, r32, h);
+      pers::mma_row<Cfg, 1>(fa, fb[1], i, acc);
+      issue_part(i, qq, islot, quad);
+      if constexpr (KIND != 2) fa.load_a(stn, sqn, sw, 0, i, wm, r32, h);
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (Cfg::BLOCK && KIND == 1) {
@@ -466,9 +597,9 @@ void gemm_persist_kernel(const GemmArgs p) {
 #pragma unroll
         for (int i = 0; i < TM; ++i) sc[i] = sn[i];   // the next tile's first group
       }
-      fb[0].load_b(stn, 0, wn, r32, h);
+      fb[0].load_b(stn, sqn, sw, 0, wn, r32, h);
 #pragma unroll
-      for (int i = 0; i < TM; ++i) fa.load_a(stn, 0, i, wm, r32, h);
+      for (int i = 0; i < TM; ++i) fa.load_a(stn, sqn, sw, 0, i, wm, r32, h);
     }
   };
 
@@ -518,19 +649,22 @@ static hipError_t launch_persist_mode(const GemmArgs &p, hipStream_t st) {
   return hipGetLastError();
 }
 
-bool persist_supported(int mode, int M, int N, int K, int Kb, bool scales4) {
+bool persist_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
   (void)M;
   (void)N;
   if (Kb % 128 != 0 || Kb < 128) return false;          // whole pairs of 64-byte steps
+  if (Kb >= (1 << 24)) return false;                     // 24-bit row offsets
   if (mode == MODE_FP8_TENSOR) return true;
-  if (mode == MODE_FP8_BLOCK) return scales4 && K % 128 == 0;
-  return false;                                          // MXFP4 keeps the per-tile kernel
+  // scaled modes: whole 16-byte scale quads per row, 16-byte aligned rows
+  if (mode == MODE_FP8_BLOCK || mode == MODE_MXFP4) return scales16 && K % 512 == 0;
+  return false;
 }
 
 hipError_t launch_gemm_persist(int mode, const GemmArgs &p, hipStream_t st) {
   switch (mode) {
     case MODE_FP8_TENSOR: return launch_persist_mode<MODE_FP8_TENSOR>(p, st);
     case MODE_FP8_BLOCK: return launch_persist_mode<MODE_FP8_BLOCK>(p, st);
+    case MODE_MXFP4: return launch_persist_mode<MODE_MXFP4>(p, st);
     default: return hipErrorInvalidValue;
   }
 }

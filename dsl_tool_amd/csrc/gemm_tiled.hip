@@ -191,7 +191,7 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
     if (t256 >= 240) {
       r.path = PATH_PIPE;
       r.variant = pipe_forced >= 0 ? pipe_forced : 0;
-      if (persist_on && pipe_forced < 0 && persist_supported(mode, M, N, K, Kb, sc4))
+      if (persist_on && pipe_forced < 0 && persist_supported(mode, M, N, K, Kb, sc16))
         r.path = PATH_PERSIST;
     } else if (M > 64 && N > 64 && t128 >= 200) {
       r.path = PATH_PIPE;

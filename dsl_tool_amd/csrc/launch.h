@@ -45,11 +45,11 @@ struct GemmArgs {
 // variant 0: 256x256 tile, 8 waves; 1: 128x128 tile, 4 waves.
 hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_t st);
 
-// Persistent pipelined kernel (FP8_TENSOR; FP8_BLOCK with 4-byte aligned
-// scales and K % 128 == 0; Kb % 128 == 0): one workgroup per CU walks its
-// 256x256 tiles with a ring of 128-byte-per-row pair slots running across
-// tile boundaries.
-bool persist_supported(int mode, int M, int N, int K, int Kb, bool scales4);
+// Persistent pipelined kernel (Kb % 128 == 0; FP8_TENSOR; FP8_BLOCK and
+// MXFP4 with 16-byte aligned scales and K % 512 == 0): one workgroup per CU
+// walks its 256x256 tiles with a ring of 128-byte-per-row pair slots running
+// across tile boundaries.
+bool persist_supported(int mode, int M, int N, int K, int Kb, bool scales16);
 hipError_t launch_gemm_persist(int mode, const GemmArgs &p, hipStream_t st);
 
 // Skinny-M kernels, one launch, no workspace (Kb % 1024 == 0):
