@@ -56,9 +56,10 @@
 
 namespace dsl {
 
-template <int MODE_>
+template <int MODE_, bool GROUPED_ = false>
 struct PersCfg {
   static constexpr int MODE = MODE_;
+  static constexpr bool GROUPED = GROUPED_;    // FP8 grouped (MoE) tile walk
   static constexpr int BM = 256, BN = 256, WGM = 2, WGN = 4;
   static constexpr int NW = WGM * WGN, NT = NW * 64, OCC = 2;
   static constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
@@ -74,7 +75,11 @@ struct PersCfg {
   static constexpr int SQA = SCALED ? BM * 16 : 0;                  // [row][16 B]
   static constexpr int SQB = BLOCK ? 1024 : (MX ? BN * 16 : 0);     // block: [2 blocks][16 B] (+copies)
   static constexpr int SQ = SQA + SQB;
-  static constexpr int LDS = 2 * PAIR + 2 * SQ;
+  // grouped: per-tile epilogue scales sx[256] and sw[256] (fp32) in a ring
+  // of three slots (the slot of tile t is refilled with tile t+3's first
+  // pair, after tile t's epilogue even when a tile is a single pair)
+  static constexpr int ES = GROUPED ? 2 * 256 * 4 : 0, NES = 3;
+  static constexpr int LDS = 2 * PAIR + 2 * SQ + NES * ES;
   static constexpr int A_DMA = A_BYTES / 1024, B_DMA = B_BYTES / 1024;
   static constexpr int SA_DMA = SQA / 1024, SB_DMA = SQB / 1024;
   static constexpr int DATA_DMA = A_DMA + B_DMA, SC_DMA = SA_DMA + SB_DMA;
@@ -83,6 +88,18 @@ struct PersCfg {
   static_assert(DS <= 1, "at most one scale DMA per wave and quad");
   static_assert(LDS <= 160 * 1024, "LDS budget");
   static_assert(!BLOCK || (WN <= 128 && 128 % WN == 0), "one weight-scale block per wave");
+  static_assert(!GROUPED || MODE == MODE_FP8_TENSOR, "grouped: FP8 with row x channel scales");
+  static_assert(!GROUPED || NW == 8, "grouped: one epilogue-scale DMA per wave");
+};
+
+// One output tile as the kernel sees it: where its A and W rows start, how
+// many of them exist, and where it lands in C.
+struct TileRef {
+  const uint8_t *a, *b;   // first A / W row of the tile (row stride Kb)
+  int arows, brows;       // rows that exist from there on (>= 1)
+  int m0, n0;             // tile origin in C (dense: also in the scale matrices)
+  int mend;               // C rows below mend exist (dense: M; grouped: the group's end)
+  int e;                  // grouped: the tile's group
 };
 
 namespace pers {
@@ -94,6 +111,20 @@ DSL_DEV void dma16(const uint8_t *base, uint32_t voff, uint32_t lds) {
                "s"(base), "s"(lds)
                : "memory", "m0");
 }
+// dma4 (64 lanes x 4 bytes) when the wave-uniform `on` is non-zero (see
+// dma16_if below).
+DSL_DEV void dma4_if(int on, const uint8_t *base, uint32_t voff, uint32_t lds) {
+  asm volatile(
+      "s_cmp_eq_u32 %3, 0\n\t"
+      "s_cbranch_scc1 .Ldma4_skip_%=\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %0, %1\n"
+      ".Ldma4_skip_%=:" ::"v"(voff),
+      "s"(base), "s"(lds), "s"(on)
+      : "memory", "m0", "scc");
+}
+
 // dma16 when the wave-uniform `on` is non-zero.  The test is a branch
 // inside the asm, so the compiler sees straight-line code: a branch in the
 // source splits the step into basic blocks, and the compiler then gathers
@@ -138,21 +169,23 @@ struct Ring {
   int wave;
   bool full;
 
-  DSL_DEV void target(const GemmArgs &p, int m0, int n0, int wave_, int lane) {
+  DSL_DEV void target(const TileRef &tr, int kb_, int wave_, int lane) {
     wave = wave_;
     full = Cfg::DS > 0 && wave < Cfg::SC_DMA;
     const bool isA = wave * Cfg::DD < Cfg::A_DMA;
-    const int r0 = isA ? m0 : n0;
-    lim = (isA ? p.M : p.N) - 1 - r0;
-    kb = p.Kb;
+    lim = (isA ? tr.arows : tr.brows) - 1;
+    kb = kb_;
     wrow = (isA ? wave * Cfg::DD : wave * Cfg::DD - Cfg::A_DMA) * Cfg::RPI;
-    dbase = (isA ? p.a : p.b) + (int64_t)r0 * p.Kb;
+    dbase = isA ? tr.a : tr.b;
     vsub = lane / Cfg::CH;
     // DMA j covers tile rows wrow + j*RPI + vsub; RPI is even, so the row
     // swizzle only depends on vsub and the parity of wrow/RPI + j
     vchunk = (uint32_t)(((lane % Cfg::CH) ^ pipe::swz<Cfg::PKB>(wrow + (int)vsub)) * 16);
-    sbase = p.a;
+    sbase = tr.a;
     soff = 0;
+  }
+  // scale plan of a dense scaled tile at (m0, n0)
+  DSL_DEV void target_scales(const GemmArgs &p, int m0, int n0, int lane) {
     if constexpr (Cfg::SCALED) {
       // bytes per scale row: fp32 per 128-K group, or E8M0 per 32 elements
       const int64_t rowb = Cfg::BLOCK ? (int64_t)(p.K / 128) * 4 : (int64_t)(p.K / 32);
@@ -289,55 +322,153 @@ DSL_DEV void mma_row(const Frag<Cfg> &fa, const Frag<Cfg> &fb, int i, v16f (&acc
 
 }  // namespace pers
 
-template <class Cfg>
+// Group g's row range with the offsets clamped into [0, rows] and made
+// non-decreasing, so malformed tables can never address outside X / Y.
+DSL_DEV int2 group_rows_of(const int32_t *off, int g, int rows) {
+  int lo = off[g], hi = off[g + 1];
+  lo = lo < 0 ? 0 : (lo > rows ? rows : lo);
+  hi = hi < lo ? lo : (hi > rows ? rows : hi);
+  return make_int2(lo, hi);
+}
+
+// Args: GemmArgs (dense) or GroupedArgs (Cfg::GROUPED).
+template <class Cfg, class Args>
 __global__ __launch_bounds__(Cfg::NT) __attribute__((amdgpu_waves_per_eu(Cfg::OCC, Cfg::OCC)))
-void gemm_persist_kernel(const GemmArgs p) {
+void gemm_persist_kernel(const Args p) {
   constexpr int TM = Cfg::TM, TN = Cfg::TN;
+  constexpr bool GR = Cfg::GROUPED;
   __shared__ __align__(16) uint8_t smem[Cfg::LDS];
-  // per-tensor scales first: no global load may follow the DMA asm
-  float s1 = 1.f, s2 = 1.f;
-  if constexpr (Cfg::MODE == MODE_FP8_TENSOR) {
-    s1 = *p.ga;
-    s2 = *p.gb;
-  }
-  const float s12 = s1 * s2;
-  const int nbm = (p.M + Cfg::BM - 1) / Cfg::BM, nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
-  const int ntiles = nbm * nbn;
+  __shared__ int s_pre[GR ? kMaxGroups + 1 : 1];   // grouped: tile prefix per group
+  __shared__ int s_off[GR ? kMaxGroups + 1 : 1];   // grouped: row offsets clamped to [0, rows]
+  __shared__ int s_part[GR ? Cfg::NT : 1];
   const int b = blockIdx.x, grid = gridDim.x;
-  const int my_tiles = (ntiles - b + grid - 1) / grid;   // >= 1: grid <= ntiles
-  const int nkp = p.Kb / Cfg::PKB;                        // pairs per tile, >= 1
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
   const int r32 = lane & 31, h = lane >> 5;
   const uint32_t lds0 = pipe::lds_addr(smem);
+  const int nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
 
-  auto tile_origin = [&](int t, int &m0, int &n0) __attribute__((always_inline)) {
-    int tm, tn;
-    tile_coords(b + t * grid, nbm, nbn, tm, tn);
-    m0 = tm * Cfg::BM;
-    n0 = tn * Cfg::BN;
+  // per-tensor scales first: no global load may follow the DMA asm
+  float s12 = 1.f;
+  int kb, my_tiles, ntiles;
+  int xbase = 0, xstride = grid;   // local tile t is logical tile xbase + t * xstride
+  if constexpr (!GR) {
+    if constexpr (Cfg::MODE == MODE_FP8_TENSOR) s12 = *p.ga * *p.gb;
+    kb = p.Kb;
+    ntiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * nbn;
+    xbase = b;
+    my_tiles = (ntiles - b + grid - 1) / grid;   // >= 1: grid <= ntiles
+  } else {
+    kb = p.K;
+    // tile prefix over the groups (ceil(n_g / BM) * nbn tiles each), built
+    // by every workgroup from the device offset table
+    const int per = (p.G + Cfg::NT - 1) / Cfg::NT;
+    const int g0 = tid * per, g1 = min(p.G, g0 + per);
+    int local = 0;
+    for (int gi = g0; gi < g1; ++gi) {
+      const int2 gr = group_rows_of(p.offsets, gi, p.rows);
+      local += ((gr.y - gr.x + Cfg::BM - 1) / Cfg::BM) * nbn;
+    }
+    s_part[tid] = local;
+    __syncthreads();
+    for (int off = 1; off < Cfg::NT; off <<= 1) {
+      const int v = tid >= off ? s_part[tid - off] : 0;
+      __syncthreads();
+      s_part[tid] += v;
+      __syncthreads();
+    }
+    int run = s_part[tid] - local;
+    for (int gi = g0; gi < g1; ++gi) {
+      s_pre[gi] = run;
+      const int2 gr = group_rows_of(p.offsets, gi, p.rows);
+      run += ((gr.y - gr.x + Cfg::BM - 1) / Cfg::BM) * nbn;
+    }
+    // the tile walk reads group rows from LDS: a global load after the
+    // first copy would wait for every copy in flight (vmcnt is in order)
+    for (int gi = tid; gi <= p.G; gi += Cfg::NT) {
+      const int o = p.offsets[gi];
+      s_off[gi] = o < 0 ? 0 : (o > p.rows ? p.rows : o);
+    }
+    if (tid == Cfg::NT - 1) s_pre[p.G] = s_part[Cfg::NT - 1];
+    __syncthreads();
+    ntiles = __builtin_amdgcn_readfirstlane(s_pre[p.G]);
+    // XCD-aware order: dispatch ids go round-robin over the 8 XCDs, so XCD
+    // x takes the contiguous logical range [x*q + min(x, rem), ...), in
+    // which consecutive tiles share a group's W panels
+    if (grid % 8 == 0) {
+      const int x = b & 7, q = ntiles >> 3, rem = ntiles & 7;
+      const int size = q + (x < rem ? 1 : 0), j0 = b >> 3;
+      xbase = x * q + (x < rem ? x : rem) + j0;
+      xstride = grid >> 3;
+      my_tiles = size > j0 ? (size - j0 + xstride - 1) / xstride : 0;
+    } else {
+      xbase = b;
+      my_tiles = b < ntiles ? (ntiles - b + grid - 1) / grid : 0;
+    }
+  }
+  if (my_tiles <= 0) return;                      // before any copy is issued
+  const int nkp = kb / Cfg::PKB;                  // pairs per tile, >= 1
+
+  auto tile_ref = [&](int t) __attribute__((always_inline)) {
+    TileRef tr;
+    if constexpr (!GR) {
+      int tm, tn;
+      tile_coords(xbase + t * xstride, (p.M + Cfg::BM - 1) / Cfg::BM, nbn, tm, tn);
+      tr.m0 = tm * Cfg::BM;
+      tr.n0 = tn * Cfg::BN;
+      tr.a = p.a + (int64_t)tr.m0 * kb;
+      tr.b = p.b + (int64_t)tr.n0 * kb;
+      tr.arows = p.M - tr.m0;
+      tr.mend = p.M;
+      tr.e = 0;
+    } else {
+      const int id = xbase + t * xstride;
+      int l = 0, u = p.G - 1;              // largest group e with s_pre[e] <= id
+      while (l < u) {
+        const int mid = (l + u + 1) >> 1;
+        if (s_pre[mid] <= id) l = mid;
+        else u = mid - 1;
+      }
+      const int e = __builtin_amdgcn_readfirstlane(l);
+      const int in = id - s_pre[e];
+      const int mt = in / nbn, nt = in - mt * nbn;
+      // the rows of group_rows_of(), from the clamped copy in LDS
+      const int lo = s_off[e], hi0 = s_off[e + 1], hi = hi0 < lo ? lo : hi0;
+      tr.m0 = __builtin_amdgcn_readfirstlane(lo + mt * Cfg::BM);
+      tr.n0 = nt * Cfg::BN;
+      tr.mend = __builtin_amdgcn_readfirstlane(hi);
+      tr.a = p.x + (int64_t)tr.m0 * kb;
+      tr.b = p.w + ((int64_t)e * p.N + tr.n0) * kb;
+      tr.arows = tr.mend - tr.m0;
+      tr.e = e;
+    }
+    tr.brows = p.N - tr.n0;
+    return tr;
   };
 
   // issue cursor: the next pair to copy is pair iq of local tile it, global
   // pair number ig (its slot: ig % 2).  Past the workgroup's last pair the
   // cursor stays on it, so every step copies a pair (into a slot nobody reads
   // again) and all steps have the same shape; those repeats copy no scales.
-  // iqc counts the quads begun (their slot: iqc % 2).
+  // iqc counts the quads begun (their slot: iqc % 2); grouped: ies is the
+  // epilogue-scale slot of tile it.
   pers::Ring<Cfg> ring;
-  int it = 0, iq = 0, ig = 0, iqc = -1;
-  {
-    int m0, n0;
-    tile_origin(0, m0, n0);
-    ring.target(p, m0, n0, wave, lane);
-  }
+  int it = 0, iq = 0, ig = 0, iqc = -1, ies = 0;
+  TileRef itr = tile_ref(0);
+  auto retarget = [&]() __attribute__((always_inline)) {
+    ring.target(itr, kb, wave, lane);
+    if constexpr (Cfg::SCALED) ring.target_scales(p, itr.m0, itr.n0, lane);
+  };
+  retarget();
   auto issue_pair_prep = [&]() __attribute__((always_inline)) {
     if (iq == nkp && it + 1 < my_tiles) {
       iq = 0;
       ++it;
-      int m0, n0;
-      tile_origin(it, m0, n0);
-      ring.target(p, m0, n0, wave, lane);
+      ies = ies == Cfg::NES - 1 ? 0 : ies + 1;
+      itr = tile_ref(it);
+      retarget();
     }
   };
   auto slot_of = [&](int gp) __attribute__((always_inline)) { return lds0 + (uint32_t)((gp & 1) * Cfg::PAIR); };
@@ -352,6 +483,21 @@ void gemm_persist_kernel(const GemmArgs p) {
       if (i < 0 || i == TM - 1)
         ring.issue_scales(__builtin_amdgcn_readfirstlane((int)(quad && ring.full)), qq / Cfg::QP,
                           pipe::lds_addr(squad) + (uint32_t)((iqc & 1) * Cfg::SQ));
+    }
+    if constexpr (GR) {
+      // a tile's first pair also brings its epilogue scales: waves 0-3 the
+      // 256 row scales sx, waves 4-7 the 256 channel scales sw of its group
+      if (i < 0 || i == TM - 1) {
+        const bool rows = wave < 4;
+        const int w4 = rows ? wave : wave - 4;
+        const int last = (rows ? itr.mend - itr.m0 : p.N - itr.n0) - 1;
+        int k = w4 * 64 + pers::lane_id();
+        k = k < last ? k : last;
+        const float *src = rows ? p.sx + itr.m0 : p.sw + (int64_t)itr.e * p.N + itr.n0;
+        pers::dma4_if(__builtin_amdgcn_readfirstlane((int)(qq == 0 && iq < nkp)),
+                      reinterpret_cast<const uint8_t *>(src), (uint32_t)k * 4u,
+                      lds0 + (uint32_t)(2 * Cfg::PAIR + 2 * Cfg::SQ + ies * Cfg::ES + wave * 256));
+      }
     }
   };
 
@@ -378,39 +524,60 @@ void gemm_persist_kernel(const GemmArgs p) {
 
   // ---- epilogue of local tile t: convert, scale, store from registers.
   // Lane (r32, h) stores, for each of its rows, 4 consecutive columns per
-  // (j, q): col = n0 + wn*WN + 32j + 8q + 4h.  Interior tiles (the common
-  // case) take an unchecked path with one row pointer and constant column
-  // offsets; edge tiles check every element.
+  // (j, q): col = n0 + wn*WN + 32j + 8q + 4h.  Tiles whose columns all exist
+  // (all but a ragged last column of tiles) take the wide-store path, where
+  // rows past the end (a group's or the matrix's last partial tile) are
+  // masked per lane; the rest check every element.
+  int ces = 0;                     // grouped: epilogue-scale slot of the tile being finished
   auto epilogue = [&](int t) __attribute__((always_inline)) {
     // the lane's coordinates are formed afresh (opaque to CSE): values kept
     // from the prologue would be live across the whole loop and spill
     const int eln = pers::lane_id();
     const int r32 = eln & 31, h = eln >> 5;
-    int m0, n0;
-    tile_origin(t, m0, n0);
+    const TileRef tr = tile_ref(t);
+    const int m0 = tr.m0, n0 = tr.n0, mend = tr.mend;
+    void *cout;
+    int64_t ldc;
+    if constexpr (GR) {
+      cout = p.y;
+      ldc = p.ldy;
+    } else {
+      cout = p.c;
+      ldc = p.ldc;
+    }
     const int c0 = n0 + wn * Cfg::WN + 4 * h;
-    const bool interior = m0 + Cfg::BM <= p.M && n0 + Cfg::BN <= p.N &&
-                          (p.ldc % (p.out_f32 ? 4 : 8)) == 0 &&
-                          (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
+    const bool wide = n0 + Cfg::BN <= p.N && (ldc % (p.out_f32 ? 4 : 8)) == 0 &&
+                      (reinterpret_cast<uintptr_t>(cout) & 15) == 0;
+    const float *esx = reinterpret_cast<const float *>(smem + 2 * Cfg::PAIR + 2 * Cfg::SQ + ces * Cfg::ES);
+    const float *esw = esx + 256;
     auto val = [&](int i, int j, int r) __attribute__((always_inline)) {
       float x = acc[i][j][r];
-      if constexpr (Cfg::MODE == MODE_FP8_TENSOR) x = x * s12;
-      else if constexpr (Cfg::BLOCK) x = x * sc[i];
+      if constexpr (GR) {
+        // (acc * sx[row]) * sw[g, col], the grouped epilogue
+        x = (x * esx[wm * Cfg::WM + i * 32 + r32]) *
+            esw[wn * Cfg::WN + j * 32 + 8 * (r >> 2) + 4 * h + (r & 3)];
+      } else if constexpr (Cfg::MODE == MODE_FP8_TENSOR) {
+        x = x * s12;
+      } else if constexpr (Cfg::BLOCK) {
+        x = x * sc[i];
+      }
       return x;
     };
-    if (interior) {
+    if (wide) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int64_t row = m0 + wm * Cfg::WM + i * 32 + r32;
         if (p.out_f32) {
-          float *dst = static_cast<float *>(p.c) + row * p.ldc + c0;
+          float *dst = static_cast<float *>(cout) + row * ldc + c0;
+          if (row < mend) {
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
+            for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-              *reinterpret_cast<float4 *>(dst + j * 32 + q * 8) =
-                  make_float4(val(i, j, 4 * q), val(i, j, 4 * q + 1), val(i, j, 4 * q + 2),
-                              val(i, j, 4 * q + 3));
+              for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<float4 *>(dst + j * 32 + q * 8) =
+                    make_float4(val(i, j, 4 * q), val(i, j, 4 * q + 1), val(i, j, 4 * q + 2),
+                                val(i, j, 4 * q + 3));
+          }
         } else {
           // Lane (h, r32) holds columns 8q + 4h .. +3 (q = 0..3) of row r32
           // of each 32x32 block.  Two lane exchanges regroup them so that
@@ -418,8 +585,8 @@ void gemm_persist_kernel(const GemmArgs p) {
           // .. +7 of rows r16 (X) and 16 + r16 (Y): each store then writes
           // 16 rows x 64 contiguous bytes instead of 32 rows x 16 bytes.
           const int r16 = r32 & 15, seg = h + 2 * (r32 >> 4);
-          uint16_t *dst = static_cast<uint16_t *>(p.c) +
-                          (int64_t)(m0 + wm * Cfg::WM + i * 32 + r16) * p.ldc + n0 +
+          const int rowx = m0 + wm * Cfg::WM + i * 32 + r16;     // X's row; Y's is rowx + 16
+          uint16_t *dst = static_cast<uint16_t *>(cout) + (int64_t)rowx * ldc + n0 +
                           wn * Cfg::WN + 8 * seg;
 #pragma unroll
           for (int j = 0; j < TN; ++j) {
@@ -451,8 +618,8 @@ void gemm_persist_kernel(const GemmArgs p) {
               X = make_uint4(t0[0], t1[0], t2[0], t3[0]);
               Y = make_uint4(t0[1], t1[1], t2[1], t3[1]);
             }
-            *reinterpret_cast<uint4 *>(dst + j * 32) = X;
-            *reinterpret_cast<uint4 *>(dst + 16 * p.ldc + j * 32) = Y;
+            if (rowx < mend) *reinterpret_cast<uint4 *>(dst + j * 32) = X;
+            if (rowx + 16 < mend) *reinterpret_cast<uint4 *>(dst + 16 * ldc + j * 32) = Y;
           }
         }
       }
@@ -460,7 +627,7 @@ void gemm_persist_kernel(const GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < TM; ++i) {
         const int row = m0 + wm * Cfg::WM + i * 32 + r32;
-        if (row >= p.M) continue;
+        if (row >= mend) continue;
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -468,8 +635,8 @@ void gemm_persist_kernel(const GemmArgs p) {
             const int col = c0 + j * 32 + 8 * (r >> 2) + (r & 3);
             if (col >= p.N) continue;
             const float v = val(i, j, r);
-            if (p.out_f32) static_cast<float *>(p.c)[(int64_t)row * p.ldc + col] = v;
-            else static_cast<uint16_t *>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16(v);
+            if (p.out_f32) static_cast<float *>(cout)[(int64_t)row * ldc + col] = v;
+            else static_cast<uint16_t *>(cout)[(int64_t)row * ldc + col] = f32_to_bf16(v);
           }
       }
     }
@@ -482,6 +649,7 @@ void gemm_persist_kernel(const GemmArgs p) {
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+    ces = ces == Cfg::NES - 1 ? 0 : ces + 1;
   };
 
   // issue the cursor's pair (rows i of a step, or all when i < 0)
@@ -645,7 +813,7 @@ static hipError_t launch_persist_mode(const GemmArgs &p, hipStream_t st) {
   const int ntiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * ((p.N + Cfg::BN - 1) / Cfg::BN);
   int grid = persist_cu_count();
   if (grid > ntiles) grid = ntiles;
-  gemm_persist_kernel<Cfg><<<grid, Cfg::NT, 0, st>>>(p);
+  gemm_persist_kernel<Cfg, GemmArgs><<<grid, Cfg::NT, 0, st>>>(p);
   return hipGetLastError();
 }
 
@@ -667,6 +835,24 @@ hipError_t launch_gemm_persist(int mode, const GemmArgs &p, hipStream_t st) {
     case MODE_MXFP4: return launch_persist_mode<MODE_MXFP4>(p, st);
     default: return hipErrorInvalidValue;
   }
+}
+
+bool grouped_persist_supported(const GroupedArgs &p) {
+  return p.K % 128 == 0 && p.K >= 128 && p.K < (1 << 24) && p.G >= 1 && p.G <= kMaxGroups;
+}
+
+// The device-side tile count is not known here: the grid is one workgroup
+// per CU (at most the tile-count upper bound); workgroups without a tile
+// return before issuing anything.
+hipError_t launch_grouped_persist(const GroupedArgs &p, hipStream_t st) {
+  using Cfg = PersCfg<MODE_FP8_TENSOR, true>;
+  const int nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
+  const int64_t upper = ((int64_t)(p.rows + Cfg::BM - 1) / Cfg::BM + p.G) * nbn;
+  int64_t grid = persist_cu_count();
+  if (grid > upper) grid = upper;
+  if (grid < 1) grid = 1;
+  gemm_persist_kernel<Cfg, GroupedArgs><<<(unsigned)grid, Cfg::NT, 0, st>>>(p);
+  return hipGetLastError();
 }
 
 }  // namespace dsl

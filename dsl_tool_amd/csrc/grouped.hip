@@ -8,13 +8,12 @@
 // Epilogue: y = (acc * sx[row]) * sw[g, col] (per-row activation scale,
 // per-channel weight scale).
 #include <cstdlib>
+#include <cstring>
 
 #include "gemm_core.h"
 #include "pipe_core.h"
 
 namespace dsl {
-
-constexpr int kMaxGroups = 2048;
 
 // Group g's row range with the offsets clamped into [0, rows] and made
 // non-decreasing, so malformed tables can never address outside X / Y.
@@ -247,6 +246,15 @@ static void launch_grouped_pipe_cfg(const GroupedArgs &p, hipStream_t st) {
 hipError_t launch_grouped_fp8(GroupedArgs p, hipStream_t st) {
   if (p.rows == 0 || p.N == 0) return hipSuccess;
   const int avg = p.rows / (p.G > 0 ? p.G : 1);
+  // DSL_GEMM_PERSIST=0 keeps the per-tile pipelined walk below (tuning)
+  static const bool persist_on = [] {
+    const char *e = getenv("DSL_GEMM_PERSIST");
+    if (!e) return true;
+    char v[8] = {0};
+    for (int i = 0; i < 7 && e[i]; ++i) v[i] = (char)((e[i] >= 'A' && e[i] <= 'Z') ? e[i] + 32 : e[i]);
+    return !(strcmp(v, "0") == 0 || strcmp(v, "off") == 0 || strcmp(v, "false") == 0);
+  }();
+  if (persist_on && avg >= 256 && grouped_persist_supported(p)) return launch_grouped_persist(p, st);
   if (p.K % 64 == 0) {
     // DSL_GROUPED_TILE=256 / 128 forces the 256x256 / 128x256 tile (tuning)
     static const int forced = [] {

@@ -65,6 +65,8 @@ hipError_t launch_gemm(int mode, GemmArgs args, hipStream_t st);
 // Workspace the launcher will need for this shape (0 if none).
 size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K);
 
+constexpr int kMaxGroups = 2048;   // groups per grouped launch (LDS tables)
+
 struct GroupedArgs {
   const uint8_t *x;      // [rows][K]
   const uint8_t *w;      // [G][N][K]
@@ -77,5 +79,8 @@ struct GroupedArgs {
   int out_f32;
 };
 hipError_t launch_grouped_fp8(GroupedArgs args, hipStream_t st);
+// Grouped FP8 on the persistent kernel (K % 128 == 0, K < 2^24).
+bool grouped_persist_supported(const GroupedArgs &args);
+hipError_t launch_grouped_persist(const GroupedArgs &args, hipStream_t st);
 
 }  // namespace dsl

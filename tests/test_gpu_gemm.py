@@ -393,6 +393,31 @@ def test_grouped_moe_skewed_counts_pipelined():
     assert_close(y, ref, what=f"grouped MoE {counts}")
 
 
+# Grouped GEMM on the persistent kernel (K % 128 == 0, >= 256 rows per group
+# on average): Zipf-skewed experts with empty ones and more tiles than CUs
+# (the tile walk crosses groups inside a workgroup; epilogue scales ride in
+# with each tile's first pair), and a small problem whose grid is not a
+# multiple of 8 (plain tile order) with workgroups that get no tile.
+@pytest.mark.parametrize("case", ["moe", "small"])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_grouped_persistent(case, out_dtype):
+    if case == "moe":
+        counts = W.moe_counts(num_experts=32, tokens=4096, top_k=4, n_empty=3, seed=778).tolist()
+        n, k = 1536, 512
+    else:
+        counts, n, k = [600, 300], 512, 256
+    x, w, offsets = _grouped_case(counts, n, k, 721)
+    G_ = len(counts)
+    qx, sx = Q.quant_fp8_blocks(x.to(DEV), 1, k)
+    qw, sw = Q.quant_fp8_blocks(w.reshape(G_ * n, k).to(DEV), 1, k)
+    y = G.grouped_fp8_gemm_packed(qx, sx, qw.reshape(G_, n, k), sw.reshape(G_, n),
+                                  torch.from_numpy(offsets).to(DEV), out_dtype=out_dtype)
+    assert y.dtype == out_dtype
+    ref = OG.ref_grouped_fp8(np_u8(qx), np_f32(sx)[:, 0], np_u8(qw).reshape(G_, n, k),
+                             np_f32(sw).reshape(G_, n), offsets)
+    assert_close(y, ref, what=f"grouped persistent {case} {out_dtype}")
+
+
 def test_grouped_register_staged_fallback_k_not_multiple_of_64():
     counts = [9, 0, 70, 33]
     x, w, offsets = _grouped_case(counts, 96, 272, 711)
