@@ -49,6 +49,7 @@ HEADLINE = "fp8_block_m4096"
 MALL_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fp8_block_m4096_traffic.txt")
 COPY_BYTES = 256 << 20          # calibration copy for the HBM byte counters
+WARM_MS = 50.0                  # per-case warm-up time on the GPU before timing
 
 
 def log(msg: str) -> None:
@@ -265,6 +266,22 @@ def time_case(case, steps, warmup, dev, graph):
         for i in range(warmup):
             run(i, sp)
     torch.cuda.synchronize(dev)
+    # then keep the GPU busy with this case for WARM_MS: the shader clock
+    # settles under the power limit within tens of milliseconds, and a case
+    # timed right after a different one otherwise measures the transition
+    w0 = torch.cuda.Event(enable_timing=True)
+    w1 = torch.cuda.Event(enable_timing=True)
+    busy = 0.0
+    for _ in range(200):
+        if busy >= WARM_MS:
+            break
+        with torch.cuda.stream(stream):
+            w0.record(stream)
+            for i in range(max(warmup, 1)):
+                run(i, sp)
+            w1.record(stream)
+        torch.cuda.synchronize(dev)
+        busy += w0.elapsed_time(w1)
     start = torch.cuda.Event(enable_timing=True)
     end = torch.cuda.Event(enable_timing=True)
     if graph:

@@ -45,6 +45,13 @@
 // block scales of W and A go into the MFMA's scale operands (exact powers
 // of two), cuda/gemm/fp4_gemm.cu semantics.
 //
+// NVFP4: the E4M3 block scales (one per 16 elements) are not powers of two,
+// so operands are dequantized in registers: each 8-element group becomes
+// 8 fp16 values (hardware E2M1 -> fp16 and E4M3 -> fp16 conversions, then
+// one packed fp16 multiply per 2 values; E2M1 x E4M3 has at most 6
+// significant bits, so the fp16 values are exact) and feeds 32x32x16 fp16
+// MFMAs; the fp32 global scales apply in the epilogue.
+//
 // Epilogue: each wave converts its accumulators (v_cvt_pk_bf16_f32),
 // regroups them across lanes (v_permlane32_swap, v_permlane16_swap) and
 // stores 16 bytes per lane, 16 rows x 64 contiguous bytes per store, straight
@@ -65,15 +72,16 @@ struct PersCfg {
   static constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
   static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;
   static constexpr bool MX = MODE == MODE_MXFP4;
-  static constexpr bool SCALED = BLOCK || MX;
+  static constexpr bool NV = MODE == MODE_NVFP4;
+  static constexpr bool SCALED = BLOCK || MX || NV;
   static constexpr int PKB = 128;                      // K bytes per pair (per row)
   static constexpr int CH = PKB / 16, RPI = 1024 / PKB;  // chunks per row, rows per DMA
   static constexpr int A_BYTES = BM * PKB, B_BYTES = BN * PKB;
   static constexpr int PAIR = A_BYTES + B_BYTES;
   // scale quads: 16 bytes per row cover QP pairs
-  static constexpr int QP = BLOCK ? 4 : 2;
+  static constexpr int QP = BLOCK ? 4 : (MX ? 2 : 1);
   static constexpr int SQA = SCALED ? BM * 16 : 0;                  // [row][16 B]
-  static constexpr int SQB = BLOCK ? 1024 : (MX ? BN * 16 : 0);     // block: [2 blocks][16 B] (+copies)
+  static constexpr int SQB = BLOCK ? 1024 : (SCALED ? BN * 16 : 0); // block: [2 blocks][16 B] (+copies)
   static constexpr int SQ = SQA + SQB;
   // grouped: per-tile epilogue scales sx[256] and sw[256] (fp32) in a ring
   // of three slots (the slot of tile t is refilled with tile t+3's first
@@ -187,8 +195,10 @@ struct Ring {
   // scale plan of a dense scaled tile at (m0, n0)
   DSL_DEV void target_scales(const GemmArgs &p, int m0, int n0, int lane) {
     if constexpr (Cfg::SCALED) {
-      // bytes per scale row: fp32 per 128-K group, or E8M0 per 32 elements
-      const int64_t rowb = Cfg::BLOCK ? (int64_t)(p.K / 128) * 4 : (int64_t)(p.K / 32);
+      // bytes per scale row: fp32 per 128-K group, E8M0 per 32 elements or
+      // E4M3 per 16
+      const int64_t rowb = Cfg::BLOCK ? (int64_t)(p.K / 128) * 4
+                                      : (Cfg::MX ? (int64_t)(p.K / 32) : (int64_t)(p.K / 16));
       if (wave < Cfg::SA_DMA) {
         int grow = m0 + wave * 64 + lane;
         grow = grow < p.M ? grow : p.M - 1;
@@ -241,7 +251,7 @@ struct Ring {
 // With that order lane half h takes all its scales from word h of the
 // row's two pair words, byte 2p + kk: the MFMA's op_sel selects it, so the
 // word goes to the MFMA as read, once per pair.
-template <class Cfg, bool MX = Cfg::MX>
+template <class Cfg, int KIND = Cfg::MX ? 1 : (Cfg::NV ? 2 : 0)>
 struct Frag {
   v8i a[Cfg::TM], b[Cfg::TN];
   static DSL_DEV v8i ld(const uint8_t *base, int row, int p, int h) {
@@ -262,7 +272,7 @@ struct Frag {
 };
 
 template <class Cfg>
-struct Frag<Cfg, true> {
+struct Frag<Cfg, 1> {
   v4i a[Cfg::TM][2], b[Cfg::TN][2];
   int as[Cfg::TM], bs[Cfg::TN];     // scale word h of the row's pair
   static DSL_DEV v4i ld(const uint8_t *base, int row, int c) {
@@ -293,6 +303,82 @@ struct Frag<Cfg, true> {
     for (int j = 0; j < Cfg::TN; ++j) bs[j] = half0.bs[j];
   }
 };
+
+// NVFP4: the FP8 fragment layout (lane half h holds the 64 elements
+// [64h, 64h+64) of the half as four u32 words, word s = elements 8s..8s+7,
+// block s/2 of the lane's four) plus the lane's four E4M3 block-scale bytes
+// (bytes 8p + 4h .. +3 of the row's 16 scale bytes of the pair).  K-step s
+// of the 32x32x16 fp16 MFMA takes word s from both lane halves, the same
+// element order for A and W.
+template <class Cfg>
+struct Frag<Cfg, 2> {
+  v8i a[Cfg::TM], b[Cfg::TN];
+  int as[Cfg::TM], bs[Cfg::TN];
+  static DSL_DEV v8i ld(const uint8_t *base, int row, int p, int h) {
+    return Frag<Cfg, 0>::ld(base, row, p, h);
+  }
+  DSL_DEV void load_a(const uint8_t *slot, const uint8_t *sq, int, int p, int i, int wm, int r32,
+                      int h) {
+    const int row = wm * Cfg::WM + i * 32 + r32;
+    a[i] = ld(slot, row, p, h);
+    as[i] = *reinterpret_cast<const int *>(sq + row * 16 + 8 * p + 4 * h);
+  }
+  DSL_DEV void load_b(const uint8_t *slot, const uint8_t *sq, int, int p, int wn, int r32, int h) {
+#pragma unroll
+    for (int j = 0; j < Cfg::TN; ++j) {
+      const int row = wn * Cfg::WN + j * 32 + r32;
+      b[j] = ld(slot + Cfg::A_BYTES, row, p, h);
+      bs[j] = *reinterpret_cast<const int *>(sq + Cfg::SQA + row * 16 + 8 * p + 4 * h);
+    }
+  }
+  DSL_DEV void share_scales(const Frag &) {}
+};
+
+// fp16 block scale (both halves of the result) of block `blk` (0..3) of a
+// lane's E4M3 scale word
+DSL_DEV v2h nv_scale2(int word, int blk) {
+  const uint32_t w = blk >= 2 ? (uint32_t)word >> 16 : (uint32_t)word;
+  const v2h t = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, false);
+  const _Float16 s = (blk & 1) ? t[1] : t[0];
+  return (v2h){s, s};
+}
+// 8 E2M1 codes (low nibble first) times an fp16 scale, as 8 fp16 values
+DSL_DEV v8h nv_deq(uint32_t w, v2h s2) {
+  const v2h p0 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 0) * s2;
+  const v2h p1 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 1) * s2;
+  const v2h p2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 2) * s2;
+  const v2h p3 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(w, 1.0f, 3) * s2;
+  return (v8h){p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+}
+
+// NVFP4 part i of a step: K-steps 2i and 2i+1 (block i of each lane's four)
+// for all rows; W fragments are dequantized once per K-step.  With
+// `last`, each A row is handed to `reload` right after its last MFMA of
+// the step.
+template <class Cfg, class Reload>
+DSL_DEV void nv_part(int i, const Frag<Cfg> &fa, const Frag<Cfg> &fb,
+                     v16f (&acc)[Cfg::TM][Cfg::TN], bool last, Reload &&reload) {
+  v2h sa[Cfg::TM], sb[Cfg::TN];
+#pragma unroll
+  for (int j = 0; j < Cfg::TN; ++j) sb[j] = nv_scale2(fb.bs[j], i);
+#pragma unroll
+  for (int r = 0; r < Cfg::TM; ++r) sa[r] = nv_scale2(fa.as[r], i);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int st = 2 * i + u;
+    v8h bq[Cfg::TN];
+#pragma unroll
+    for (int j = 0; j < Cfg::TN; ++j) bq[j] = nv_deq((uint32_t)fb.b[j][st], sb[j]);
+#pragma unroll
+    for (int r = 0; r < Cfg::TM; ++r) {
+      const v8h aq = nv_deq((uint32_t)fa.a[r][st], sa[r]);
+#pragma unroll
+      for (int j = 0; j < Cfg::TN; ++j)
+        acc[r][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bq[j], aq, acc[r][j], 0, 0, 0);
+      if (last && u == 1) reload(r);
+    }
+  }
+}
 
 // MFMAs of row i for half P of a pair: W fragments from fb, A from fa
 // (operands swapped).
@@ -355,7 +441,7 @@ void gemm_persist_kernel(const Args p) {
   int kb, my_tiles, ntiles;
   int xbase = 0, xstride = grid;   // local tile t is logical tile xbase + t * xstride
   if constexpr (!GR) {
-    if constexpr (Cfg::MODE == MODE_FP8_TENSOR) s12 = *p.ga * *p.gb;
+    if constexpr (Cfg::MODE == MODE_FP8_TENSOR || Cfg::NV) s12 = *p.ga * *p.gb;
     kb = p.Kb;
     ntiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * nbn;
     xbase = b;
@@ -556,7 +642,7 @@ void gemm_persist_kernel(const Args p) {
         // (acc * sx[row]) * sw[g, col], the grouped epilogue
         x = (x * esx[wm * Cfg::WM + i * 32 + r32]) *
             esw[wn * Cfg::WN + j * 32 + 8 * (r >> 2) + 4 * h + (r & 3)];
-      } else if constexpr (Cfg::MODE == MODE_FP8_TENSOR) {
+      } else if constexpr (Cfg::MODE == MODE_FP8_TENSOR || Cfg::NV) {
         x = x * s12;
       } else if constexpr (Cfg::BLOCK) {
         x = x * sc[i];
@@ -704,12 +790,17 @@ void gemm_persist_kernel(const Args p) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      if constexpr (RESCALE) {
+      if constexpr (Cfg::NV) {
+        pers::nv_part<Cfg>(i, fa, fb[0], acc, i == TM - 1,
+                           [&](int r) __attribute__((always_inline)) { fa.load_a(st, sq, sw, 1, r, wm, r32, h); });
+      } else {
+        if constexpr (RESCALE) {
 #pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] *= rt[i];
+          for (int j = 0; j < TN; ++j) acc[i][j] *= rt[i];
+        }
+        pers::mma_row<Cfg, 0>(fa, fb[0], i, acc);
+        fa.load_a(st, sq, sw, 1, i, wm, r32, h);
       }
-      pers::mma_row<Cfg, 0>(fa, fb[0], i, acc);
-      fa.load_a(st, sq, sw, 1, i, wm, r32, h);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -743,9 +834,15 @@ void gemm_persist_kernel(const Args p) {
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
-      pers::mma_row<Cfg, 1>(fa, fb[1], i, acc);
-      issue_part(i, qq, islot, quad);
-      if constexpr (KIND != 2) fa.load_a(stn, sqn, sw, 0, i, wm, r32, h);
+      if constexpr (Cfg::NV) {
+        pers::nv_part<Cfg>(i, fa, fb[1], acc, KIND != 2 && i == TM - 1,
+                           [&](int r) __attribute__((always_inline)) { fa.load_a(stn, sqn, sw, 0, r, wm, r32, h); });
+        issue_part(i, qq, islot, quad);
+      } else {
+        pers::mma_row<Cfg, 1>(fa, fb[1], i, acc);
+        issue_part(i, qq, islot, quad);
+        if constexpr (KIND != 2) fa.load_a(stn, sqn, sw, 0, i, wm, r32, h);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (Cfg::BLOCK && KIND == 1) {
@@ -825,6 +922,7 @@ bool persist_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
   if (mode == MODE_FP8_TENSOR) return true;
   // scaled modes: whole 16-byte scale quads per row, 16-byte aligned rows
   if (mode == MODE_FP8_BLOCK || mode == MODE_MXFP4) return scales16 && K % 512 == 0;
+  if (mode == MODE_NVFP4) return scales16 && K % 256 == 0;   // 16 scale bytes per row and pair
   return false;
 }
 
@@ -833,6 +931,7 @@ hipError_t launch_gemm_persist(int mode, const GemmArgs &p, hipStream_t st) {
     case MODE_FP8_TENSOR: return launch_persist_mode<MODE_FP8_TENSOR>(p, st);
     case MODE_FP8_BLOCK: return launch_persist_mode<MODE_FP8_BLOCK>(p, st);
     case MODE_MXFP4: return launch_persist_mode<MODE_MXFP4>(p, st);
+    case MODE_NVFP4: return launch_persist_mode<MODE_NVFP4>(p, st);
     default: return hipErrorInvalidValue;
   }
 }

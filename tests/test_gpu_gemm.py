@@ -227,14 +227,14 @@ def test_fp8_block_pipelined(m, n, k):
 # edges (the unchecked store path for interior tiles, the checked one for
 # edge tiles), bf16 and fp32 output.  Block-scaled and MXFP4 take it when
 # K % 512 == 0, with scale quads of 4 (block) / 2 (MX) pairs: K = 512 is
-# one quad per tile, 1536 three (the quad slots alternate across tiles).
-# K = 384 / 256 keep them on the per-tile kernels (per-tensor stays
-# persistent).
+# one quad per tile, 1536 three (the quad slots alternate across tiles);
+# NVFP4 when K % 256 == 0 (one pair per quad).  K = 384 / 256 keep the
+# scaled modes on the per-tile kernels (per-tensor stays persistent).
 PERSIST_SHAPES = [(8192, 4352, 512), (4500, 4200, 1536), (4352, 8192, 256), (4100, 4500, 384)]
 
 
 @pytest.mark.parametrize("m,n,k", PERSIST_SHAPES)
-@pytest.mark.parametrize("mode", ["tensor", "block", "mxfp4"])
+@pytest.mark.parametrize("mode", ["tensor", "block", "mxfp4", "nvfp4"])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 def test_persistent(m, n, k, mode, out_dtype):
     a = W.activations(4, m, k, outliers=True) if mode == "block" else W.randn_bf16((m, k), 141)
@@ -249,11 +249,18 @@ def test_persistent(m, n, k, mode, out_dtype):
         qw, sw = Q.quant_fp8_tensor(w.to(DEV))
         ref = OG.ref_fp8_per_tensor(np_u8(qa), np_f32(sa)[0], np_u8(qw), np_f32(sw)[0])
         c = G.fp8_gemm_packed(qa, qw, sa, sw, out_dtype=out_dtype)
-    else:
+    elif mode == "mxfp4":
         qa, ea = Q.quant_mxfp4(a.to(DEV))
         qw, ew = Q.quant_mxfp4(w.to(DEV))
         ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
         c = G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4", out_dtype=out_dtype)
+    else:
+        qa, sa, ga = Q.quant_nvfp4(a.to(DEV))
+        qw, sw, gw = Q.quant_nvfp4(w.to(DEV))
+        ref = OG.ref_nvfp4(np_u8(qa), np_u8(sa), np_f32(ga)[0], np_u8(qw), np_u8(sw),
+                           np_f32(gw)[0])
+        c = G.fp4_gemm_packed(qa, sa, qw, sw, fmt="nvfp4", global_a=ga, global_w=gw,
+                              out_dtype=out_dtype)
     assert c.dtype == out_dtype
     assert_close(c, ref, what=f"persistent {mode} {m}x{n}x{k} {out_dtype}")
 
