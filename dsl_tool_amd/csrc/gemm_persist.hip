@@ -354,10 +354,12 @@ DSL_DEV v8h nv_deq(uint32_t w, v2h s2) {
 // NVFP4 part i of a step: K-steps 2i and 2i+1 (block i of each lane's four)
 // for all rows; W fragments are dequantized once per K-step.  With
 // `last`, each A row is handed to `reload` right after its last MFMA of
-// the step.
-template <class Cfg, class Reload>
+// the step.  FRESH: the first MFMA of each tile (part 0, K-step 0) starts
+// from zero instead of the accumulator.
+template <class Cfg, bool FRESH, class Reload>
 DSL_DEV void nv_part(int i, const Frag<Cfg> &fa, const Frag<Cfg> &fb,
                      v16f (&acc)[Cfg::TM][Cfg::TN], bool last, Reload &&reload) {
+  const v16f zero = {};
   v2h sa[Cfg::TM], sb[Cfg::TN];
 #pragma unroll
   for (int j = 0; j < Cfg::TN; ++j) sb[j] = nv_scale2(fb.bs[j], i);
@@ -374,16 +376,19 @@ DSL_DEV void nv_part(int i, const Frag<Cfg> &fa, const Frag<Cfg> &fb,
       const v8h aq = nv_deq((uint32_t)fa.a[r][st], sa[r]);
 #pragma unroll
       for (int j = 0; j < Cfg::TN; ++j)
-        acc[r][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(bq[j], aq, acc[r][j], 0, 0, 0);
+        acc[r][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+            bq[j], aq, (FRESH && i == 0 && u == 0) ? zero : acc[r][j], 0, 0, 0);
       if (last && u == 1) reload(r);
     }
   }
 }
 
 // MFMAs of row i for half P of a pair: W fragments from fb, A from fa
-// (operands swapped).
-template <class Cfg, int P>
+// (operands swapped).  FRESH: the tile's first MFMAs start from zero, so
+// the epilogue does not clear the accumulators.
+template <class Cfg, int P, bool FRESH = false>
 DSL_DEV void mma_row(const Frag<Cfg> &fa, const Frag<Cfg> &fb, int i, v16f (&acc)[Cfg::TM][Cfg::TN]) {
+  const v16f zero = {};
   if constexpr (Cfg::MX) {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
@@ -393,7 +398,8 @@ DSL_DEV void mma_row(const Frag<Cfg> &fa, const Frag<Cfg> &fb, int i, v16f (&acc
         const v8i w8 = {w4[0], w4[1], w4[2], w4[3], 0, 0, 0, 0};
         const v8i a8 = {a4[0], a4[1], a4[2], a4[3], 0, 0, 0, 0};
         acc[i][j] = kk == 0 ? __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
-                                  w8, a8, acc[i][j], 4, 4, 2 * P, fb.bs[j], 2 * P, fa.as[i])
+                                  w8, a8, FRESH ? zero : acc[i][j], 4, 4, 2 * P, fb.bs[j], 2 * P,
+                                  fa.as[i])
                             : __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
                                   w8, a8, acc[i][j], 4, 4, 2 * P + 1, fb.bs[j], 2 * P + 1,
                                   fa.as[i]);
@@ -401,8 +407,8 @@ DSL_DEV void mma_row(const Frag<Cfg> &fa, const Frag<Cfg> &fb, int i, v16f (&acc
   } else {
 #pragma unroll
     for (int j = 0; j < Cfg::TN; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(fb.b[j], fa.a[i], acc[i][j], 0,
-                                                                  0, 0, 0, 0, 0);
+      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(
+          fb.b[j], fa.a[i], FRESH ? zero : acc[i][j], 0, 0, 0, 0, 0, 0);
   }
 }
 
@@ -726,15 +732,9 @@ void gemm_persist_kernel(const Args p) {
           }
       }
     }
-    // keep the zeroing below the stores: hoisted, it would double the live
-    // accumulator registers
+    // the next tile's fragment loads stay below the stores: hoisted into
+    // the epilogue they would be live beside the accumulators
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
     ces = ces == Cfg::NES - 1 ? 0 : ces + 1;
   };
 
@@ -780,8 +780,10 @@ void gemm_persist_kernel(const Args p) {
   // carries the previous group's scale; each row is brought to this group's
   // right before its first MFMA of the group, overlapping the MFMAs of the
   // row before and reading results that completed a step ago.
-  auto step0 = [&](auto rescale_tag, int gp) __attribute__((always_inline)) {
-    constexpr bool RESCALE = Cfg::BLOCK && decltype(rescale_tag)::value;
+  // FRESH (a tile's first pair): the MFMAs start from zero.
+  auto step0 = [&](auto tag, int gp) __attribute__((always_inline)) {
+    constexpr bool RESCALE = Cfg::BLOCK && decltype(tag)::value == 1;
+    constexpr bool FRESH = decltype(tag)::value == 2;
     const uint8_t *st = smem + (gp & 1) * Cfg::PAIR;
     const uint8_t *sq = squad + (cqc & 1) * Cfg::SQ;
     const int sw = (cq % Cfg::QP) * 2;              // MX: the pair's scale words
@@ -791,14 +793,14 @@ void gemm_persist_kernel(const Args p) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       if constexpr (Cfg::NV) {
-        pers::nv_part<Cfg>(i, fa, fb[0], acc, i == TM - 1,
+        pers::nv_part<Cfg, FRESH>(i, fa, fb[0], acc, i == TM - 1,
                            [&](int r) __attribute__((always_inline)) { fa.load_a(st, sq, sw, 1, r, wm, r32, h); });
       } else {
         if constexpr (RESCALE) {
 #pragma unroll
           for (int j = 0; j < TN; ++j) acc[i][j] *= rt[i];
         }
-        pers::mma_row<Cfg, 0>(fa, fb[0], i, acc);
+        pers::mma_row<Cfg, 0, FRESH>(fa, fb[0], i, acc);
         fa.load_a(st, sq, sw, 1, i, wm, r32, h);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -835,7 +837,7 @@ void gemm_persist_kernel(const Args p) {
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       if constexpr (Cfg::NV) {
-        pers::nv_part<Cfg>(i, fa, fb[1], acc, KIND != 2 && i == TM - 1,
+        pers::nv_part<Cfg, false>(i, fa, fb[1], acc, KIND != 2 && i == TM - 1,
                            [&](int r) __attribute__((always_inline)) { fa.load_a(stn, sqn, sw, 0, r, wm, r32, h); });
         issue_part(i, qq, islot, quad);
       } else {
@@ -872,11 +874,11 @@ void gemm_persist_kernel(const Args p) {
   // carries MFMAs (the accumulators would be copied at the join).
   using K1 = std::integral_constant<int, 1>;
   using K2 = std::integral_constant<int, 2>;
-  using NoRescale = std::false_type;
-  using Rescale = std::true_type;
+  using Rescale = std::integral_constant<int, 1>;
+  using Fresh = std::integral_constant<int, 2>;
   int gp = 0;
   for (int t = 0; t < my_tiles; ++t) {
-    step0(NoRescale{}, gp);
+    step0(Fresh{}, gp);
     for (int q = 0; q + 1 < nkp; ++q) {
       step1(K1{}, gp);
       ++gp;
