@@ -96,6 +96,52 @@ DSL_HD uint32_t e2m1_encode(float v) {
   return s | c;
 }
 
+// ----------------------------------------------- hardware encoders (gfx950) --
+// v_cvt_pk_fp8_f32 and v_cvt_scalef32_pk_fp4_f32 (scale 1.0) return exactly
+// e4m3_encode / e2m1_encode of every finite fp32 input (checked on gfx950
+// over all 2^32 patterns; E4M3 differs only in the sign of the NaN code for
+// NaN inputs, fixed below by taking the sign from the input).
+//
+// Quotients x / s (IEEE division, then RNE to the format) are formed as
+// p = |x| * rs with rs = 1 / s (IEEE).  p lies within 3 ulp of the correctly
+// rounded |x| / s and the encoding is monotonic, so where the codes of
+// p - 3 ulp and p + 3 ulp agree they are the code of |x| / s; elsewhere (a
+// quotient within a few ulp of a rounding boundary) the exact division is
+// used.  The sign comes from x (s > 0).
+
+// E4M3 codes of x0 / s (low byte) and x1 / s; rs = 1.0f / s.
+DSL_DEV uint32_t e4m3_div_pk(float x0, float x1, float s, float rs) {
+  const float a0 = __builtin_fabsf(x0), a1 = __builtin_fabsf(x1);
+  const uint32_t b0 = f2u(a0 * rs), b1 = f2u(a1 * rs);
+  // p - 3 ulp clamped at +0 (the wrap of a tiny p is a NaN pattern; fmaxf drops it)
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+                          __builtin_fmaxf(u2f(b0 - 3u), 0.f), __builtin_fmaxf(u2f(b1 - 3u), 0.f), 0, false) &
+                      0xffffu;
+  const uint32_t hi =
+      (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(u2f(b0 + 3u), u2f(b1 + 3u), 0, false) & 0xffffu;
+  uint32_t c = hi;
+  if (lo != hi) c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a0 / s, a1 / s, 0, false) & 0xffffu;
+  const uint32_t sg = ((f2u(x0) >> 24) & 0x80u) | ((f2u(x1) >> 16) & 0x8000u);
+  return (c & 0x7f7fu) | sg;
+}
+
+// E2M1 codes of v0 (low nibble) and v1, as e2m1_encode.
+DSL_DEV uint32_t e2m1_pk(float v0, float v1) {
+  return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, v0, v1, 1.0f, 0) & 0xffu;
+}
+
+// E2M1 codes of x0 / d (low nibble) and x1 / d; rd = 1.0f / d, d > 0.
+DSL_DEV uint32_t e2m1_div_pk(float x0, float x1, float d, float rd) {
+  const float a0 = __builtin_fabsf(x0), a1 = __builtin_fabsf(x1);
+  const uint32_t b0 = f2u(a0 * rd), b1 = f2u(a1 * rd);
+  const uint32_t lo = e2m1_pk(__builtin_fmaxf(u2f(b0 - 3u), 0.f), __builtin_fmaxf(u2f(b1 - 3u), 0.f));
+  const uint32_t hi = e2m1_pk(u2f(b0 + 3u), u2f(b1 + 3u));
+  uint32_t c = hi;
+  if (lo != hi) c = e2m1_pk(a0 / d, a1 / d);
+  const uint32_t sg = ((f2u(x0) >> 28) & 0x8u) | ((f2u(x1) >> 24) & 0x80u);
+  return (c & 0x77u) | sg;
+}
+
 // ------------------------------------------------------------------ E8M0 --
 // MXFP4 shared exponent: clamp(floor(log2(amax)) - 2, -127, 127); amax == 0
 // gives -127.  Integer exponent extraction (exact for subnormals).

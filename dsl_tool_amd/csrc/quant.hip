@@ -10,7 +10,10 @@
 //     contiguous [K,N] tensor): one thread per scale group, threads ordered
 //     so that the unit-stride axis is the fast one across lanes.
 // Arithmetic is the bit-exact contract of include/dsl_gemm.h (fp32 scales,
-// IEEE division x / scale, RNE encoders from common.h).
+// IEEE division x / scale, RNE encoders from common.h); the vector paths
+// encode with the gfx950 hardware converters, which common.h shows equal to
+// those encoders, dividing through the exact reciprocal with an exact
+// fallback near rounding boundaries.
 #include "common.h"
 #include "launch.h"
 
@@ -67,6 +70,14 @@ DSL_DEV float nv_global_of(float amax) {
   return s < kScaleFloor ? kScaleFloor : s;
 }
 
+// 8 values / s as E4M3 codes (2 x u32), with the hardware encoder (see
+// e4m3_div_pk); rs = 1.0f / s.
+DSL_DEV uint2 e4m3_div8(const float (&f)[8], float s, float rs) {
+  const uint32_t lo = e4m3_div_pk(f[0], f[1], s, rs) | (e4m3_div_pk(f[2], f[3], s, rs) << 16);
+  const uint32_t hi = e4m3_div_pk(f[4], f[5], s, rs) | (e4m3_div_pk(f[6], f[7], s, rs) << 16);
+  return make_uint2(lo, hi);
+}
+
 // ---------------------------------------------------------------------------
 // Pass 1 of the per-tensor / NVFP4 quantizers: per-block amax partials.
 // ---------------------------------------------------------------------------
@@ -108,6 +119,7 @@ __global__ __launch_bounds__(256) void quant_fp8_tensor_kernel(
     float *__restrict__ scale_out) {
   __shared__ float sh[4];
   const float scale = fp8_scale_of(reduce_partials(partial, nparts, sh));
+  const float rscale = 1.0f / scale;
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   if (VEC) {
@@ -116,12 +128,7 @@ __global__ __launch_bounds__(256) void quant_fp8_tensor_kernel(
       const int64_t r = i / cpr, c8 = i - r * cpr;
       float f[8];
       unpack8(*reinterpret_cast<const uint4 *>(x + r * sr + c8 * 8), f);
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) lo |= (uint32_t)e4m3_encode(f[j] / scale) << (8 * j);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) hi |= (uint32_t)e4m3_encode(f[4 + j] / scale) << (8 * j);
-      *reinterpret_cast<uint2 *>(q + r * cols + c8 * 8) = make_uint2(lo, hi);
+      *reinterpret_cast<uint2 *>(q + r * cols + c8 * 8) = e4m3_div8(f, scale, rscale);
     }
   } else {
     const int64_t total = rows * cols;
@@ -173,21 +180,14 @@ __global__ __launch_bounds__(256) void quant_rowgroup_kernel(
     if (KIND == KIND_FP8) {
       const float s = fp8_scale_of(m);
       if (lane == 0) reinterpret_cast<float *>(scales)[g] = s;
-      if (ok) {
-        uint32_t lo = 0, hi = 0;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) lo |= (uint32_t)e4m3_encode(f[j] / s) << (8 * j);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) hi |= (uint32_t)e4m3_encode(f[4 + j] / s) << (8 * j);
-        *reinterpret_cast<uint2 *>(q + r * cols + c) = make_uint2(lo, hi);
-      }
+      if (ok) *reinterpret_cast<uint2 *>(q + r * cols + c) = e4m3_div8(f, s, 1.0f / s);
     } else if (KIND == KIND_MX) {
       const int e = mx_exponent(m);
       const float mul = pow2_neg(e);
       if (lane == 0) reinterpret_cast<uint8_t *>(scales)[g] = (uint8_t)(e + 127);
       uint32_t p = 0;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) p |= e2m1_encode(f[j] * mul) << (4 * j);
+      for (int j = 0; j < 4; ++j) p |= e2m1_pk(f[2 * j] * mul, f[2 * j + 1] * mul) << (8 * j);
       if (ok) *reinterpret_cast<uint32_t *>(q + ((r * cols + c) >> 1)) = p;
     } else {  // KIND_NV
       const uint8_t sb = e4m3_encode((m / 6.0f) / sg);
@@ -195,8 +195,9 @@ __global__ __launch_bounds__(256) void quant_rowgroup_kernel(
       if (lane == 0) reinterpret_cast<uint8_t *>(scales)[g] = sb;
       uint32_t p = 0;
       if (d != 0.f) {
+        const float rd = 1.0f / d;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) p |= e2m1_encode(f[j] / d) << (4 * j);
+        for (int j = 0; j < 4; ++j) p |= e2m1_div_pk(f[2 * j], f[2 * j + 1], d, rd) << (8 * j);
       }
       if (ok) *reinterpret_cast<uint32_t *>(q + ((r * cols + c) >> 1)) = p;
     }
@@ -288,6 +289,7 @@ __global__ __launch_bounds__(256) void quant_fp8_tile_kernel(
     }
   }
   const float s = fp8_scale_of(block_max(m, sh));
+  const float rs = 1.0f / s;
   if (threadIdx.x == 0) scales[blockIdx.x] = s;
   if (VEC) {
     const int64_t cpr = nc >> 3, total = nr * cpr;
@@ -295,12 +297,7 @@ __global__ __launch_bounds__(256) void quant_fp8_tile_kernel(
       const int64_t r = r0 + i / cpr, c = c0 + (i % cpr) * 8;
       float f[8];
       unpack8(*reinterpret_cast<const uint4 *>(x + r * sr + c), f);
-      uint32_t lo = 0, hi = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) lo |= (uint32_t)e4m3_encode(f[j] / s) << (8 * j);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) hi |= (uint32_t)e4m3_encode(f[4 + j] / s) << (8 * j);
-      *reinterpret_cast<uint2 *>(q + r * cols + c) = make_uint2(lo, hi);
+      *reinterpret_cast<uint2 *>(q + r * cols + c) = e4m3_div8(f, s, rs);
     }
   } else {
     const int64_t total = nr * nc;

@@ -73,6 +73,45 @@ def test_e4m3_encoder_exhaustive_at_unit_scale():
     assert np.array_equal(np_u8(q), want)
 
 
+# The vector quantizers divide through the reciprocal of the scale and fall
+# back to the exact quotient only where it lies within a few ulp of an E4M3 /
+# E2M1 rounding boundary.  Every bf16 value under a pinned group amax with a
+# non-power-of-two scale puts many quotients at or next to those boundaries.
+@pytest.mark.parametrize("amax", [1.7, 3.3, 100.1, 0.013, 447.0, 5.9e-3, 2.0e4])
+def test_fp8_division_near_rounding_boundaries(amax):
+    amax = float(np.float32(torch.tensor(amax).bfloat16().float()))
+    rows = _rows_with_pin(_all_bf16_upto(amax), 128, amax)
+    for layout in ("row", "tile", "tensor"):
+        if layout == "tensor":
+            q, s = Q.quant_fp8_tensor(_to_gpu_bf16(rows))
+            q_ref, s_ref = OQ.quant_fp8_per_tensor(rows)
+            assert np_f32(s)[0] == np.float32(s_ref)
+        else:
+            gr, gc = (1, 128) if layout == "row" else (128, 128)
+            q, s = Q.quant_fp8_blocks(_to_gpu_bf16(rows), gr, gc)
+            q_ref, s_ref = OQ.quant_fp8_blockwise(rows, gr, gc)
+            assert np.array_equal(np_f32(s), s_ref)
+        assert np.array_equal(np_u8(q), q_ref), layout
+
+
+@pytest.mark.parametrize("amax,boost", [(1.7, 1.0), (5.3, 1.37), (100.1, 1.0),
+                                        (0.013, 2.9), (3.0e3, 1.11)])
+def test_nvfp4_division_near_rounding_boundaries(amax, boost):
+    # `boost` adds one block whose amax sets the global scale above the pinned
+    # blocks', so their E4M3 block scales land between powers of two.
+    amax = float(np.float32(torch.tensor(amax).bfloat16().float()))
+    flat = _rows_with_pin(_all_bf16_upto(amax), 16, amax).reshape(-1)
+    top = np.zeros(16, np.float32)
+    top[0] = float(np.float32(torch.tensor(amax * boost).bfloat16().float()))
+    flat = np.concatenate([top, flat, np.zeros(-(flat.size + 16) % 64, np.float32)])
+    rows = flat.reshape(-1, 64)
+    q, sb, sg = Q.quant_nvfp4(_to_gpu_bf16(rows))
+    q_ref, sb_ref, sg_ref = OQ.quant_nvfp4(rows)
+    assert np_f32(sg)[0] == sg_ref
+    assert np.array_equal(np_u8(sb), sb_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+
+
 @pytest.mark.parametrize("gr,gc", [(1, 128), (128, 128), (1, 4096), (1, 64), (16, 48)])
 def test_fp8_blocks_match_oracle(gr, gc):
     x = W.activations(2, 300, 4096, outliers=True)
