@@ -99,47 +99,59 @@ DSL_HD uint32_t e2m1_encode(float v) {
 // ----------------------------------------------- hardware encoders (gfx950) --
 // v_cvt_pk_fp8_f32 and v_cvt_scalef32_pk_fp4_f32 (scale 1.0) return exactly
 // e4m3_encode / e2m1_encode of every finite fp32 input (checked on gfx950
-// over all 2^32 patterns; E4M3 differs only in the sign of the NaN code for
-// NaN inputs, fixed below by taking the sign from the input).
+// over all 2^32 patterns; E4M3 differs only in the sign of the NaN code).
 //
-// Quotients x / s (IEEE division, then RNE to the format) are formed as
-// p = |x| * rs with rs = 1 / s (IEEE).  p lies within 3 ulp of the correctly
-// rounded |x| / s and the encoding is monotonic, so where the codes of
-// p - 3 ulp and p + 3 ulp agree they are the code of |x| / s; elsewhere (a
-// quotient within a few ulp of a rounding boundary) the exact division is
-// used.  The sign comes from x (s > 0).
+// Quotients.  The contract encodes the IEEE quotient RN(x / s).  The vector
+// paths form instead
+//     q = x * r,   e = fma(q, s, -x),   q' = fma(-e, r, q)
+// (one correction step after Markstein) with r = v_rcp_f32(s).  q' is not
+// always RN(x / s) in fp32, but for every bf16 x and every scale these
+// quantizers produce, its E4M3 / E2M1 code is the code of RN(x / s) whenever
+// r is within 1 ulp of 1/s: tests/quot_exhaustive.c checks every bf16
+// (amax, x) pair for E4M3 (s = amax / 448 with the floor) and every
+// (global scale, block scale code, x) triple for NVFP4, with r at RN(1/s) and
+// one ulp either side.  v_rcp_f32 is specified to 1 ulp, and on gfx950 it lies
+// within 1 ulp of 1.0f / s for every normal s in [2^-125, 2^125] (measured).
+// The same step with a constant r = RN(1/b) gives RN(a / b) exactly for every
+// bf16 a and b = 448, 6, 2688 (also checked there), which yields the scales.
+// A zero x keeps its sign: e = +0 and q' = q + (-0) = q.
+// Inputs are finite; codes for NaN or infinite inputs are not specified.
 
-// E4M3 codes of x0 / s (low byte) and x1 / s; rs = 1.0f / s.
-DSL_DEV uint32_t e4m3_div_pk(float x0, float x1, float s, float rs) {
-  const float a0 = __builtin_fabsf(x0), a1 = __builtin_fabsf(x1);
-  const uint32_t b0 = f2u(a0 * rs), b1 = f2u(a1 * rs);
-  // p - 3 ulp clamped at +0 (the wrap of a tiny p is a NaN pattern; fmaxf drops it)
-  const uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
-                          __builtin_fmaxf(u2f(b0 - 3u), 0.f), __builtin_fmaxf(u2f(b1 - 3u), 0.f), 0, false) &
-                      0xffffu;
-  const uint32_t hi =
-      (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(u2f(b0 + 3u), u2f(b1 + 3u), 0, false) & 0xffffu;
-  uint32_t c = hi;
-  if (lo != hi) c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(a0 / s, a1 / s, 0, false) & 0xffffu;
-  const uint32_t sg = ((f2u(x0) >> 24) & 0x80u) | ((f2u(x1) >> 16) & 0x8000u);
-  return (c & 0x7f7fu) | sg;
+DSL_DEV float quot(float x, float s, float r) {
+  const float q = x * r;
+  const float e = __builtin_fmaf(q, s, -x);
+  return __builtin_fmaf(-e, r, q);
 }
 
-// E2M1 codes of v0 (low nibble) and v1, as e2m1_encode.
-DSL_DEV uint32_t e2m1_pk(float v0, float v1) {
-  return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(0u, v0, v1, 1.0f, 0) & 0xffu;
+DSL_DEV float rcp_approx(float s) { return __builtin_amdgcn_rcpf(s); }
+
+// E4M3 codes of x[i] / s for 4 values, byte i = element i.
+DSL_DEV uint32_t e4m3_quot4(float x0, float x1, float x2, float x3, float s, float r) {
+  uint32_t c = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(quot(x0, s, r), quot(x1, s, r), 0, false);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(quot(x2, s, r), quot(x3, s, r), (int)c, true);
 }
 
-// E2M1 codes of x0 / d (low nibble) and x1 / d; rd = 1.0f / d, d > 0.
-DSL_DEV uint32_t e2m1_div_pk(float x0, float x1, float d, float rd) {
-  const float a0 = __builtin_fabsf(x0), a1 = __builtin_fabsf(x1);
-  const uint32_t b0 = f2u(a0 * rd), b1 = f2u(a1 * rd);
-  const uint32_t lo = e2m1_pk(__builtin_fmaxf(u2f(b0 - 3u), 0.f), __builtin_fmaxf(u2f(b1 - 3u), 0.f));
-  const uint32_t hi = e2m1_pk(u2f(b0 + 3u), u2f(b1 + 3u));
-  uint32_t c = hi;
-  if (lo != hi) c = e2m1_pk(a0 / d, a1 / d);
-  const uint32_t sg = ((f2u(x0) >> 28) & 0x8u) | ((f2u(x1) >> 24) & 0x80u);
-  return (c & 0x77u) | sg;
+// E2M1 codes of v0 (low nibble) and v1, as e2m1_encode, into byte `b` of `old`.
+template <int B>
+DSL_DEV uint32_t e2m1_pk_into(uint32_t old, float v0, float v1) {
+  return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(old, v0, v1, 1.0f, B);
+}
+DSL_DEV uint32_t e2m1_pk(float v0, float v1) { return e2m1_pk_into<0>(0u, v0, v1) & 0xffu; }
+
+// E2M1 codes of x[i] / d for 8 values (nibble i = element i); r = rcp(d).
+DSL_DEV uint32_t e2m1_quot8(const float *x, float d, float r) {
+  uint32_t c = e2m1_pk_into<0>(0u, quot(x[0], d, r), quot(x[1], d, r));
+  c = e2m1_pk_into<1>(c, quot(x[2], d, r), quot(x[3], d, r));
+  c = e2m1_pk_into<2>(c, quot(x[4], d, r), quot(x[5], d, r));
+  return e2m1_pk_into<3>(c, quot(x[6], d, r), quot(x[7], d, r));
+}
+
+// E2M1 codes of x[i] * m for 8 values (m a power of two: exact).
+DSL_DEV uint32_t e2m1_mul8(const float *x, float m) {
+  uint32_t c = e2m1_pk_into<0>(0u, x[0] * m, x[1] * m);
+  c = e2m1_pk_into<1>(c, x[2] * m, x[3] * m);
+  c = e2m1_pk_into<2>(c, x[4] * m, x[5] * m);
+  return e2m1_pk_into<3>(c, x[6] * m, x[7] * m);
 }
 
 // ------------------------------------------------------------------ E8M0 --

@@ -2,22 +2,33 @@
 // MXFP4 (E2M1 + E8M0 / 32), NVFP4 (E2M1 + E4M3 / 16 + fp32 global).
 //
 // All kernels read x[r*sr + c*sc] (bf16) and write K-major codes q[r*C + c]
-// (FP8) or packed nibbles q[r*C/2 + c/2] (FP4).  Two code paths:
-//   * vector path (sc == 1, C % 8 == 0, sr % 8 == 0, 16-B aligned x):
-//     each thread owns 8 consecutive elements (one 16-B load); a "team" of
-//     T threads owns one scale group and reduces its amax with lane shuffles;
+// (FP8) or packed nibbles q[r*C/2 + c/2] (FP4).  Code paths, fastest first:
+//   * packed path (sc == 1, sr == C, C % 8 == 0, 16-B aligned x, fewer than
+//     2^31 chunks; row groups also need C % group == 0): the input is one run
+//     of 16-byte chunks and group g is chunks [g*CG, (g+1)*CG), so indices
+//     are 32-bit and division-free.  TL lanes share a group (amax by DPP),
+//     each holding CG/TL chunks, and every lane keeps several groups' loads
+//     in flight;
+//   * register tile path (FP8 tiles up to 128x128, vector-aligned rows):
+//     one workgroup holds its tile in registers, so x is read once;
+//   * team path (vector-aligned rows, any C): a team of T lanes owns one
+//     group of 8*T elements of a row;
 //   * strided path (anything else, e.g. the reference's B[K,N] given as a
 //     contiguous [K,N] tensor): one thread per scale group, threads ordered
 //     so that the unit-stride axis is the fast one across lanes.
 // Arithmetic is the bit-exact contract of include/dsl_gemm.h (fp32 scales,
-// IEEE division x / scale, RNE encoders from common.h); the vector paths
-// encode with the gfx950 hardware converters, which common.h shows equal to
-// those encoders, dividing through the exact reciprocal with an exact
-// fallback near rounding boundaries.
+// codes of the IEEE quotient x / scale, RNE).  The vector paths encode with
+// the gfx950 converters and the corrected reciprocal quotient of common.h
+// (quot), which give the same codes; the strided path divides and encodes in
+// software.
 #include "common.h"
 #include "launch.h"
 
 namespace dsl {
+
+constexpr float kRcp448 = 1.0f / 448.0f;     // RN(1/448)
+constexpr float kRcp6 = 1.0f / 6.0f;         // RN(1/6)
+constexpr float kRcp2688 = 1.0f / 2688.0f;   // RN(1/2688)
 
 DSL_DEV float wave_max(float v) {
 #pragma unroll
@@ -37,14 +48,33 @@ DSL_DEV float block_max(float v, float *sh) {
   return r;
 }
 
-DSL_DEV void unpack8(const uint4 &v, float f[8]) {
+template <int CTRL>
+DSL_DEV float dpp_f(float v) {
+  return u2f((uint32_t)__builtin_amdgcn_mov_dpp((int)f2u(v), CTRL, 0xf, 0xf, false));
+}
+
+// Max over aligned teams of TL lanes (TL = 1, 2, 4, 8, 16); every lane of a
+// team gets it.  quad_perm [1,0,3,2] and [2,3,0,1] reduce a quad, the half-row
+// mirror pairs quads, the row mirror pairs half rows.  All lanes must be
+// active.
+template <int TL>
+DSL_DEV float team_max(float v) {
+  static_assert(TL == 1 || TL == 2 || TL == 4 || TL == 8 || TL == 16, "team size");
+  if constexpr (TL >= 2) v = fmaxf(v, dpp_f<0xb1>(v));
+  if constexpr (TL >= 4) v = fmaxf(v, dpp_f<0x4e>(v));
+  if constexpr (TL >= 8) v = fmaxf(v, dpp_f<0x141>(v));
+  if constexpr (TL >= 16) v = fmaxf(v, dpp_f<0x140>(v));
+  return v;
+}
+
+DSL_DEV void unpack8(const uint4 &v, float *f) {
   f[0] = u2f(v.x << 16); f[1] = u2f(v.x & 0xffff0000u);
   f[2] = u2f(v.y << 16); f[3] = u2f(v.y & 0xffff0000u);
   f[4] = u2f(v.z << 16); f[5] = u2f(v.z & 0xffff0000u);
   f[6] = u2f(v.w << 16); f[7] = u2f(v.w & 0xffff0000u);
 }
 
-DSL_DEV float amax8(const float f[8]) {
+DSL_DEV float amax8(const float *f) {
   float m = 0.f;
 #pragma unroll
   for (int i = 0; i < 8; ++i) m = fmaxf(m, __builtin_fabsf(f[i]));
@@ -60,27 +90,57 @@ DSL_DEV float reduce_partials(const float *partial, int n, float *sh) {
   return block_max(m, sh);
 }
 
+// max(amax / 448, 1e-12) and max(amax / 2688, 1e-12); quot with the constant
+// reciprocal is the IEEE quotient for every bf16 amax.
 DSL_DEV float fp8_scale_of(float amax) {
-  float s = amax / kE4M3Max;
+  const float s = quot(amax, kE4M3Max, kRcp448);
   return s < kScaleFloor ? kScaleFloor : s;
 }
 
 DSL_DEV float nv_global_of(float amax) {
-  float s = amax / kNvGlobalDiv;
+  const float s = quot(amax, kNvGlobalDiv, kRcp2688);
   return s < kScaleFloor ? kScaleFloor : s;
 }
 
-// 8 values / s as E4M3 codes (2 x u32), with the hardware encoder (see
-// e4m3_div_pk); rs = 1.0f / s.
-DSL_DEV uint2 e4m3_div8(const float (&f)[8], float s, float rs) {
-  const uint32_t lo = e4m3_div_pk(f[0], f[1], s, rs) | (e4m3_div_pk(f[2], f[3], s, rs) << 16);
-  const uint32_t hi = e4m3_div_pk(f[4], f[5], s, rs) | (e4m3_div_pk(f[6], f[7], s, rs) << 16);
-  return make_uint2(lo, hi);
+// NVFP4 block scale code e4m3((amax16 / 6) / sg) (rsg = rcp(sg)).
+DSL_DEV uint32_t nv_block_code(float m, float sg, float rsg) {
+  const float t = quot(m, 6.0f, kRcp6);
+  return (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(quot(t, sg, rsg), 0.f, 0, false) & 0xffu;
+}
+
+DSL_DEV float e4m3_value(uint32_t code) { return __builtin_amdgcn_cvt_f32_fp8((int)code, 0); }
+
+// 8 values / s as E4M3 codes (2 x u32); r = rcp(s).
+DSL_DEV uint2 e4m3_quot8(const float *f, float s, float r) {
+  return make_uint2(e4m3_quot4(f[0], f[1], f[2], f[3], s, r), e4m3_quot4(f[4], f[5], f[6], f[7], s, r));
 }
 
 // ---------------------------------------------------------------------------
 // Pass 1 of the per-tensor / NVFP4 quantizers: per-block amax partials.
 // ---------------------------------------------------------------------------
+template <int V>
+__global__ __launch_bounds__(256) void amax_packed_kernel(
+    const uint4 *__restrict__ x, uint32_t nchunks, float *__restrict__ partial) {
+  __shared__ float sh[4];
+  float m = 0.f;
+  for (uint32_t base = blockIdx.x * (256u * V); base < nchunks; base += gridDim.x * (256u * V)) {
+    uint4 d[V];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {   // lanes past the end re-read the last chunk
+      const uint32_t i = base + v * 256u + threadIdx.x;
+      d[v] = x[i < nchunks ? i : nchunks - 1];
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      float f[8];
+      unpack8(d[v], f);
+      m = fmaxf(m, amax8(f));
+    }
+  }
+  m = block_max(m, sh);
+  if (threadIdx.x == 0) partial[blockIdx.x] = m;
+}
+
 template <bool VEC>
 __global__ __launch_bounds__(256) void amax_partial_kernel(
     const uint16_t *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
@@ -110,7 +170,93 @@ __global__ __launch_bounds__(256) void amax_partial_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Per-tensor E4M3, pass 2.
+// Packed path.  KIND selects the format; CG = chunks (8 elements) per scale
+// group (1 for the per-tensor scale); TL lanes per group, lane k of a team
+// holding chunks k, k+TL, ... of it (each load instruction reads whole
+// contiguous runs); V groups per lane in flight.
+// ---------------------------------------------------------------------------
+enum { KIND_FP8 = 0, KIND_MX = 1, KIND_NV = 2, KIND_TENSOR = 3 };
+
+template <int KIND, int CG, int TL, int V>
+__global__ __launch_bounds__(256) void quant_packed_kernel(
+    const uint4 *__restrict__ x, uint32_t ngroups, uint8_t *__restrict__ q,
+    void *__restrict__ scales, const float *__restrict__ partial, int nparts,
+    float *__restrict__ scale_out) {
+  constexpr int U = CG / TL;           // chunks per lane per group
+  constexpr uint32_t GB = 256 / TL;    // groups per block per set
+  static_assert(CG % TL == 0, "team must divide the group");
+  __shared__ float sh[4];
+  float st = 1.f, rt = 1.f;            // per-tensor scale (FP8) / global scale (NVFP4)
+  if constexpr (KIND == KIND_TENSOR || KIND == KIND_NV) {
+    const float am = reduce_partials(partial, nparts, sh);
+    st = KIND == KIND_TENSOR ? fp8_scale_of(am) : nv_global_of(am);
+    rt = rcp_approx(st);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = st;
+  }
+  const uint32_t k = threadIdx.x % TL;
+  for (uint32_t base = blockIdx.x * (GB * V); base < ngroups; base += gridDim.x * (GB * V)) {
+    // Lanes past the end read the last group (their team's result is not
+    // stored), so the loads need no mask.
+    uint4 d[V][U];
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const uint32_t g = base + v * GB + threadIdx.x / TL;
+      const uint32_t gl = g < ngroups ? g : ngroups - 1;
+#pragma unroll
+      for (int j = 0; j < U; ++j) d[v][j] = x[gl * CG + k + j * TL];
+    }
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const uint32_t g = base + v * GB + threadIdx.x / TL;
+      const bool ok = g < ngroups;
+      float f[U * 8];
+      float m = 0.f;
+#pragma unroll
+      for (int j = 0; j < U; ++j) {
+        unpack8(d[v][j], f + 8 * j);
+        m = fmaxf(m, amax8(f + 8 * j));
+      }
+      if constexpr (KIND != KIND_TENSOR) m = team_max<TL>(m);
+      const uint32_t c0 = g * CG + k;
+      if constexpr (KIND == KIND_FP8 || KIND == KIND_TENSOR) {
+        float s = st, r = rt;
+        if constexpr (KIND == KIND_FP8) {
+          s = fp8_scale_of(m);
+          r = rcp_approx(s);
+          if (ok && k == 0) reinterpret_cast<float *>(scales)[g] = s;
+        }
+        if (ok) {
+#pragma unroll
+          for (int j = 0; j < U; ++j)
+            *reinterpret_cast<uint2 *>(q + (size_t)(c0 + j * TL) * 8) = e4m3_quot8(f + 8 * j, s, r);
+        }
+      } else if constexpr (KIND == KIND_MX) {
+        const int e = mx_exponent(m);
+        const float mul = pow2_neg(e);
+        if (ok && k == 0) reinterpret_cast<uint8_t *>(scales)[g] = (uint8_t)(e + 127);
+        if (ok) {
+#pragma unroll
+          for (int j = 0; j < U; ++j)
+            *reinterpret_cast<uint32_t *>(q + (size_t)(c0 + j * TL) * 4) = e2m1_mul8(f + 8 * j, mul);
+        }
+      } else {  // KIND_NV
+        const uint32_t sb = nv_block_code(m, st, rt);
+        const float dd = e4m3_value(sb) * st;
+        const float rd = rcp_approx(dd);
+        if (ok && k == 0) reinterpret_cast<uint8_t *>(scales)[g] = (uint8_t)sb;
+        if (ok) {
+#pragma unroll
+          for (int j = 0; j < U; ++j)
+            *reinterpret_cast<uint32_t *>(q + (size_t)(c0 + j * TL) * 4) =
+                dd != 0.f ? e2m1_quot8(f + 8 * j, dd, rd) : 0u;
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Per-tensor E4M3, pass 2 (non-packed input).
 // ---------------------------------------------------------------------------
 template <bool VEC>
 __global__ __launch_bounds__(256) void quant_fp8_tensor_kernel(
@@ -119,7 +265,7 @@ __global__ __launch_bounds__(256) void quant_fp8_tensor_kernel(
     float *__restrict__ scale_out) {
   __shared__ float sh[4];
   const float scale = fp8_scale_of(reduce_partials(partial, nparts, sh));
-  const float rscale = 1.0f / scale;
+  const float rscale = rcp_approx(scale);
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   if (VEC) {
@@ -128,7 +274,7 @@ __global__ __launch_bounds__(256) void quant_fp8_tensor_kernel(
       const int64_t r = i / cpr, c8 = i - r * cpr;
       float f[8];
       unpack8(*reinterpret_cast<const uint4 *>(x + r * sr + c8 * 8), f);
-      *reinterpret_cast<uint2 *>(q + r * cols + c8 * 8) = e4m3_div8(f, scale, rscale);
+      *reinterpret_cast<uint2 *>(q + r * cols + c8 * 8) = e4m3_quot8(f, scale, rscale);
     }
   } else {
     const int64_t total = rows * cols;
@@ -142,11 +288,9 @@ __global__ __launch_bounds__(256) void quant_fp8_tensor_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Row-group team kernels (vector path).  A team of T lanes (T | 64) owns one
-// group of 8*T consecutive elements of a row.  KIND selects the format.
+// Team path: a team of T lanes (T | 64) owns one group of 8*T consecutive
+// elements of a row (rows with any stride, any C).
 // ---------------------------------------------------------------------------
-enum { KIND_FP8 = 0, KIND_MX = 1, KIND_NV = 2 };
-
 template <int KIND, int T>
 __global__ __launch_bounds__(256) void quant_rowgroup_kernel(
     const uint16_t *__restrict__ x, int64_t rows, int64_t cols, int64_t sr,
@@ -154,9 +298,10 @@ __global__ __launch_bounds__(256) void quant_rowgroup_kernel(
     const float *__restrict__ partial, int nparts, float *__restrict__ global_out) {
   constexpr int G = 8 * T;                      // elements per group
   __shared__ float sh[4];
-  float sg = 1.f;
+  float sg = 1.f, rsg = 1.f;
   if (KIND == KIND_NV) {
     sg = nv_global_of(reduce_partials(partial, nparts, sh));
+    rsg = rcp_approx(sg);
     if (blockIdx.x == 0 && threadIdx.x == 0) *global_out = sg;
   }
   const int64_t gpr = (cols + G - 1) / G;       // groups per row
@@ -180,25 +325,16 @@ __global__ __launch_bounds__(256) void quant_rowgroup_kernel(
     if (KIND == KIND_FP8) {
       const float s = fp8_scale_of(m);
       if (lane == 0) reinterpret_cast<float *>(scales)[g] = s;
-      if (ok) *reinterpret_cast<uint2 *>(q + r * cols + c) = e4m3_div8(f, s, 1.0f / s);
+      if (ok) *reinterpret_cast<uint2 *>(q + r * cols + c) = e4m3_quot8(f, s, rcp_approx(s));
     } else if (KIND == KIND_MX) {
       const int e = mx_exponent(m);
-      const float mul = pow2_neg(e);
       if (lane == 0) reinterpret_cast<uint8_t *>(scales)[g] = (uint8_t)(e + 127);
-      uint32_t p = 0;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) p |= e2m1_pk(f[2 * j] * mul, f[2 * j + 1] * mul) << (8 * j);
-      if (ok) *reinterpret_cast<uint32_t *>(q + ((r * cols + c) >> 1)) = p;
+      if (ok) *reinterpret_cast<uint32_t *>(q + ((r * cols + c) >> 1)) = e2m1_mul8(f, pow2_neg(e));
     } else {  // KIND_NV
-      const uint8_t sb = e4m3_encode((m / 6.0f) / sg);
-      const float d = e4m3_decode(sb) * sg;
-      if (lane == 0) reinterpret_cast<uint8_t *>(scales)[g] = sb;
-      uint32_t p = 0;
-      if (d != 0.f) {
-        const float rd = 1.0f / d;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) p |= e2m1_div_pk(f[2 * j], f[2 * j + 1], d, rd) << (8 * j);
-      }
+      const uint32_t sb = nv_block_code(m, sg, rsg);
+      const float d = e4m3_value(sb) * sg;
+      if (lane == 0) reinterpret_cast<uint8_t *>(scales)[g] = (uint8_t)sb;
+      const uint32_t p = d != 0.f ? e2m1_quot8(f, d, rcp_approx(d)) : 0u;
       if (ok) *reinterpret_cast<uint32_t *>(q + ((r * cols + c) >> 1)) = p;
     }
   }
@@ -259,9 +395,47 @@ __global__ __launch_bounds__(256) void quant_group_scalar_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Tile kernel: one workgroup per group_rows x group_cols FP8 tile (128x128
-// weight blocks, per-row / per-channel scales over long rows).
+// Register tile path: one workgroup per gr x gc FP8 tile with gr, gc <= 128
+// and gc % 8 == 0 (128x128 weight blocks).  Lane t holds chunk t % 16 of rows
+// t / 16 + 16 j (j < 8) in registers, so the tile is read from HBM once.
 // ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quant_fp8_tile_reg_kernel(
+    const uint16_t *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int gr, int gc,
+    uint8_t *__restrict__ q, float *__restrict__ scales) {
+  __shared__ float sh[4];
+  const int64_t ntc = (cols + gc - 1) / gc;
+  const int64_t tr = blockIdx.x / ntc, tc = blockIdx.x - tr * ntc;
+  const int64_t r0 = tr * gr, c0 = tc * gc;
+  const int nr = (int)(r0 + gr < rows ? gr : rows - r0), nc = (int)(c0 + gc < cols ? gc : cols - c0);
+  const int cc = threadIdx.x & 15, rr = threadIdx.x >> 4;
+  const bool cok = cc * 8 < nc;
+  uint4 d[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = rr + 16 * j;
+    d[j] = (cok && r < nr) ? *reinterpret_cast<const uint4 *>(x + (r0 + r) * sr + c0 + cc * 8)
+                           : make_uint4(0, 0, 0, 0);
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float f[8];
+    unpack8(d[j], f);
+    m = fmaxf(m, amax8(f));
+  }
+  const float s = fp8_scale_of(block_max(m, sh));
+  const float rs = rcp_approx(s);
+  if (threadIdx.x == 0) scales[blockIdx.x] = s;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int r = rr + 16 * j;
+    float f[8];
+    unpack8(d[j], f);
+    if (cok && r < nr) *reinterpret_cast<uint2 *>(q + (r0 + r) * cols + c0 + cc * 8) = e4m3_quot8(f, s, rs);
+  }
+}
+
+// One workgroup per gr x gc FP8 tile of any size (two reads of the tile).
 template <bool VEC>
 __global__ __launch_bounds__(256) void quant_fp8_tile_kernel(
     const uint16_t *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
@@ -289,15 +463,15 @@ __global__ __launch_bounds__(256) void quant_fp8_tile_kernel(
     }
   }
   const float s = fp8_scale_of(block_max(m, sh));
-  const float rs = 1.0f / s;
   if (threadIdx.x == 0) scales[blockIdx.x] = s;
   if (VEC) {
+    const float rs = rcp_approx(s);
     const int64_t cpr = nc >> 3, total = nr * cpr;
     for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
       const int64_t r = r0 + i / cpr, c = c0 + (i % cpr) * 8;
       float f[8];
       unpack8(*reinterpret_cast<const uint4 *>(x + r * sr + c), f);
-      *reinterpret_cast<uint2 *>(q + r * cols + c) = e4m3_div8(f, s, rs);
+      *reinterpret_cast<uint2 *>(q + r * cols + c) = e4m3_quot8(f, s, rs);
     }
   } else {
     const int64_t total = nr * nc;
@@ -317,11 +491,28 @@ static bool vec_ok(const void *x, int64_t cols, int64_t sr, int64_t sc) {
          (reinterpret_cast<uintptr_t>(x) % 16) == 0;
 }
 
+// One run of 16-byte chunks with 32-bit chunk indices (group = elements per
+// scale group; the input must hold whole groups).
+static bool packed_ok(const void *x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
+                      int64_t group) {
+  return vec_ok(x, cols, sr, sc) && (sr == cols || rows == 1) && (cols % group) == 0 &&
+         rows * cols / 8 < ((int64_t)1 << 31);
+}
+
 static int grid_for(int64_t work, int per_block) {
   int64_t g = (work + per_block - 1) / per_block;
   if (g < 1) g = 1;
   if (g > 65535) g = 65535;
   return (int)g;
+}
+
+template <int KIND, int CG, int TL, int V>
+static void launch_packed(const uint16_t *x, int64_t rows, int64_t cols, uint8_t *q, void *scales,
+                          const float *partial, int np, float *sout, hipStream_t st) {
+  const uint32_t ngroups = (uint32_t)(rows * cols / (8 * CG));
+  const int g = grid_for(ngroups, (256 / TL) * V);
+  quant_packed_kernel<KIND, CG, TL, V><<<g, 256, 0, st>>>(
+      reinterpret_cast<const uint4 *>(x), ngroups, q, scales, partial, np, sout);
 }
 
 static int partial_blocks(int64_t elems) {
@@ -333,6 +524,14 @@ static int partial_blocks(int64_t elems) {
 
 hipError_t launch_amax_partials(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
                                 int64_t sc, float *partial, int *nparts, hipStream_t st) {
+  if (packed_ok(x, rows, cols, sr, sc, 8)) {
+    const uint32_t n = (uint32_t)(rows * cols / 8);
+    const int g = (int)((n + 256 * 4 - 1) / (256 * 4) < kMaxPartials ? (n + 256 * 4 - 1) / (256 * 4)
+                                                                      : kMaxPartials);
+    *nparts = g < 1 ? 1 : g;
+    amax_packed_kernel<4><<<*nparts, 256, 0, st>>>(reinterpret_cast<const uint4 *>(x), n, partial);
+    return hipGetLastError();
+  }
   const int g = partial_blocks(rows * cols);
   *nparts = g;
   if (vec_ok(x, cols, sr, sc))
@@ -348,7 +547,9 @@ hipError_t launch_quant_fp8_tensor(const uint16_t *x, int64_t rows, int64_t cols
   int np = 0;
   hipError_t e = launch_amax_partials(x, rows, cols, sr, sc, partial, &np, st);
   if (e != hipSuccess) return e;
-  if (vec_ok(x, cols, sr, sc))
+  if (packed_ok(x, rows, cols, sr, sc, 8))
+    launch_packed<KIND_TENSOR, 1, 1, 4>(x, rows, cols, q, nullptr, partial, np, scale, st);
+  else if (vec_ok(x, cols, sr, sc))
     quant_fp8_tensor_kernel<true><<<grid_for(rows * cols / 8, 256 * 4), 256, 0, st>>>(
         x, rows, cols, sr, sc, partial, np, q, scale);
   else
@@ -369,7 +570,17 @@ hipError_t launch_quant_fp8_blocks(const uint16_t *x, int64_t rows, int64_t cols
                                    int64_t sc, int64_t gr, int64_t gc, uint8_t *q,
                                    float *scales, hipStream_t st) {
   const bool vec = vec_ok(x, cols, sr, sc);
-  if (gr == 1 && vec && (gc == 32 || gc == 64 || gc == 128 || gc == 256)) {
+  const bool row_team = gc == 32 || gc == 64 || gc == 128 || gc == 256;
+  if (gr == 1 && row_team && packed_ok(x, rows, cols, sr, sc, gc)) {
+    switch (gc) {
+      case 32: launch_packed<KIND_FP8, 4, 4, 4>(x, rows, cols, q, scales, nullptr, 0, nullptr, st); break;
+      case 64: launch_packed<KIND_FP8, 8, 4, 2>(x, rows, cols, q, scales, nullptr, 0, nullptr, st); break;
+      case 128: launch_packed<KIND_FP8, 16, 8, 2>(x, rows, cols, q, scales, nullptr, 0, nullptr, st); break;
+      default: launch_packed<KIND_FP8, 32, 8, 1>(x, rows, cols, q, scales, nullptr, 0, nullptr, st); break;
+    }
+    return hipGetLastError();
+  }
+  if (gr == 1 && vec && row_team) {
     switch (gc) {
       case 32: launch_team<KIND_FP8, 4>(x, rows, cols, sr, q, scales, nullptr, 0, nullptr, st); break;
       case 64: launch_team<KIND_FP8, 8>(x, rows, cols, sr, q, scales, nullptr, 0, nullptr, st); break;
@@ -386,7 +597,9 @@ hipError_t launch_quant_fp8_blocks(const uint16_t *x, int64_t rows, int64_t cols
   }
   const int64_t tiles = ((rows + gr - 1) / gr) * ((cols + gc - 1) / gc);
   const bool tvec = vec && (gc % 8) == 0;
-  if (tvec)
+  if (tvec && gr <= 128 && gc <= 128)
+    quant_fp8_tile_reg_kernel<<<(unsigned)tiles, 256, 0, st>>>(x, rows, cols, sr, (int)gr, (int)gc, q, scales);
+  else if (tvec)
     quant_fp8_tile_kernel<true><<<(unsigned)tiles, 256, 0, st>>>(x, rows, cols, sr, sc, gr, gc, q, scales);
   else
     quant_fp8_tile_kernel<false><<<(unsigned)tiles, 256, 0, st>>>(x, rows, cols, sr, sc, gr, gc, q, scales);
@@ -395,7 +608,9 @@ hipError_t launch_quant_fp8_blocks(const uint16_t *x, int64_t rows, int64_t cols
 
 hipError_t launch_quant_mxfp4(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
                               int64_t sc, uint8_t *q, uint8_t *e8m0, hipStream_t st) {
-  if (vec_ok(x, cols, sr, sc)) {
+  if (packed_ok(x, rows, cols, sr, sc, 32)) {
+    launch_packed<KIND_MX, 4, 4, 4>(x, rows, cols, q, e8m0, nullptr, 0, nullptr, st);
+  } else if (vec_ok(x, cols, sr, sc)) {
     launch_team<KIND_MX, 4>(x, rows, cols, sr, q, e8m0, nullptr, 0, nullptr, st);
   } else {
     const int64_t ngroups = rows * (cols / 32);
@@ -411,7 +626,9 @@ hipError_t launch_quant_nvfp4(const uint16_t *x, int64_t rows, int64_t cols, int
   int np = 0;
   hipError_t e = launch_amax_partials(x, rows, cols, sr, sc, partial, &np, st);
   if (e != hipSuccess) return e;
-  if (vec_ok(x, cols, sr, sc)) {
+  if (packed_ok(x, rows, cols, sr, sc, 16)) {
+    launch_packed<KIND_NV, 2, 1, 2>(x, rows, cols, q, e4m3s, partial, np, gscale, st);
+  } else if (vec_ok(x, cols, sr, sc)) {
     launch_team<KIND_NV, 2>(x, rows, cols, sr, q, e4m3s, partial, np, gscale, st);
   } else {
     const int64_t ngroups = rows * (cols / 16);

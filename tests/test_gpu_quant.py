@@ -129,6 +129,48 @@ def test_fp8_blocks_strided_input_matches():
     assert np.array_equal(np_u8(q), q_ref)
 
 
+# Row-padded views (row stride > C, still 16-byte aligned rows) and row
+# lengths that are not a multiple of the group take the team / non-packed
+# kernels instead of the packed ones.
+def _padded(shape, seed, pad=64):
+    wide = W.randn_bf16((shape[0], shape[1] + pad), seed)
+    return wide.to(DEV)[:, :shape[1]], _f32(wide[:, :shape[1]])
+
+
+@pytest.mark.parametrize("fmt", ["fp8_tensor", "fp8_row128", "fp8_row32", "fp8_tile", "mxfp4", "nvfp4"])
+def test_padded_rows_match_oracle(fmt):
+    xd, xr = _padded((40, 512), 41)
+    assert xd.stride(0) == 576
+    if fmt == "fp8_tensor":
+        q, s = Q.quant_fp8_tensor(xd)
+        q_ref, s_ref = OQ.quant_fp8_per_tensor(xr)
+        assert np_f32(s)[0] == s_ref
+    elif fmt.startswith("fp8"):
+        gr, gc = {"fp8_row128": (1, 128), "fp8_row32": (1, 32), "fp8_tile": (128, 128)}[fmt]
+        q, s = Q.quant_fp8_blocks(xd, gr, gc)
+        q_ref, s_ref = OQ.quant_fp8_blockwise(xr, gr, gc)
+        assert np.array_equal(np_f32(s), s_ref)
+    elif fmt == "mxfp4":
+        q, s = Q.quant_mxfp4(xd)
+        q_ref, s_ref = OQ.quant_mxfp4(xr)
+        assert np.array_equal(np_u8(s), s_ref)
+    else:
+        q, s, g = Q.quant_nvfp4(xd)
+        q_ref, s_ref, g_ref = OQ.quant_nvfp4(xr)
+        assert np_f32(g)[0] == g_ref
+        assert np.array_equal(np_u8(s), s_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+
+
+@pytest.mark.parametrize("cols,gc", [(200, 128), (72, 64), (520, 256)])
+def test_fp8_row_groups_ragged_cols(cols, gc):
+    x = W.randn_bf16((9, cols), 42)
+    q, s = Q.quant_fp8_blocks(x.to(DEV), 1, gc)
+    q_ref, s_ref = OQ.quant_fp8_blockwise(_f32(x), 1, gc)
+    assert np.array_equal(np_f32(s), s_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+
+
 def test_e2m1_encoder_exhaustive_at_unit_scale():
     # every bf16 value with |v| < 8 in 32-blocks pinned by 4.0 -> E8M0 127 (2^0)
     vals = _all_bf16_upto(7.96875)
