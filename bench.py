@@ -44,6 +44,7 @@ if ROOT not in sys.path:
 PEAK_FP8_TFLOPS = 5000.0      # MI355X dense fp8 MFMA
 PEAK_FP4_TFLOPS = 10100.0     # MI355X dense fp4 MFMA
 PEAK_FP16_TFLOPS = 2500.0     # MI355X dense fp16 MFMA (the NVFP4 kernels dequantize to fp16)
+PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 HEADLINE = "fp8_block_m4096"
 MALL_BYTES = 256 << 20
@@ -150,6 +151,23 @@ def build_cases(names, dev):
         return Case(name, 2.0 * m * n * k, nbytes, peak, bound, launch, rot,
                     f"{fmt} M={m} N={n} K={k}" + ("" if fmt == "mxfp4" else " (fp16 MFMA peak)"))
 
+    def bf16_case(name, m, n, k):
+        a, w = rnd((m, k), 6), rnd((n, k), 7, 0.02)
+        wbytes = 2 * n * k
+        rot = _rotations(wbytes) if m <= 256 else 1
+        ws_ = [w] + [w.clone() for _ in range(rot - 1)]
+        c = torch.empty((m, n), dtype=torch.float32, device=dev)
+        ws, nb = ws_for(N.OP_BF16, m, n, k)
+
+        def launch(i, stream):
+            return L.dsl_bf16_gemm(a.data_ptr(), ws_[i % rot].data_ptr(), c.data_ptr(), m, n, k, n,
+                                   N.OUT_F32, ws.data_ptr(), nb, stream)
+        nbytes = 2 * m * k + wbytes + 4 * m * n
+        ridge = PEAK_BF16_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9)
+        bound = "hbm" if 2 * m * n * k / nbytes < ridge else "mfma"
+        return Case(name, 2.0 * m * n * k, nbytes, PEAK_BF16_TFLOPS, bound, launch, rot,
+                    f"bf16 M={m} N={n} K={k}, fp32 out (bf16 MFMA peak)")
+
     def grouped_case(name):
         x, w, offsets, counts = W.moe_problem()
         T, K = x.shape
@@ -231,6 +249,9 @@ def build_cases(names, dev):
         "nvfp4_m1": lambda: fp4_case("nvfp4_m1", 1, 14336, 4096, "nvfp4"),
         "nvfp4_m2048": lambda: fp4_case("nvfp4_m2048", 2048, 14336, 4096, "nvfp4"),
         "grouped_moe": lambda: grouped_case("grouped_moe"),
+        "bf16_8192": lambda: bf16_case("bf16_8192", 8192, 8192, 8192),
+        "bf16_m4096": lambda: bf16_case("bf16_m4096", 4096, 7168, 4096),
+        "bf16_m16": lambda: bf16_case("bf16_m16", 16, 7168, 4096),
         "quant_fp8_block128_w": lambda: quant_case("quant_fp8_block128_w", "fp8_block128", 7168, 4096),
         "quant_fp8_row128_a": lambda: quant_case("quant_fp8_row128_a", "fp8_row128", 4096, 4096),
         "quant_fp8_tensor_w": lambda: quant_case("quant_fp8_tensor_w", "fp8_tensor", 4096, 4096),
@@ -245,6 +266,7 @@ def build_cases(names, dev):
 ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor_cfg1",
              "fp8_tensor_8192",
              "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe",
+             "bf16_8192", "bf16_m4096", "bf16_m16",
              "quant_fp8_block128_w", "quant_fp8_row128_a", "quant_fp8_tensor_w", "quant_mxfp4_w",
              "quant_nvfp4_w"]
 

@@ -29,8 +29,8 @@ DSL_ERR_HIP = -4
 OUT_BF16, OUT_F32 = 0, 1
 SCALE_TENSOR, SCALE_BLOCK128 = 0, 1
 FMT_MXFP4, FMT_NVFP4 = 0, 1
-OP_FP8, OP_FP4, OP_GROUPED_FP8 = 0, 1, 2
-ABI_VERSION = 1
+OP_FP8, OP_FP4, OP_GROUPED_FP8, OP_BF16 = 0, 1, 2, 3
+ABI_VERSION = 2
 
 
 class DslLibraryError(ImportError):
@@ -60,6 +60,7 @@ SIGNATURES = {
                             _vp, _sz, _vp]),
     "dsl_fp4_gemm": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _vp, _vp,
                             _vp, _vp, _vp, _sz, _vp]),
+    "dsl_bf16_gemm": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp, _sz, _vp]),
     "dsl_grouped_fp8_gemm": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32,
                                     _vp, _vp, _vp]),
     "dsl_gemm_workspace_bytes": (_sz, [_i32, _i64, _i64, _i64]),

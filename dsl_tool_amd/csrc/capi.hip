@@ -79,7 +79,7 @@ extern "C" {
 
 const char *dsl_last_error(void) { return g_err.c_str(); }
 
-int dsl_abi_version(void) { return 1; }
+int dsl_abi_version(void) { return 2; }
 
 size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
   (void)rows;
@@ -167,6 +167,7 @@ size_t dsl_gemm_workspace_bytes(int op, int64_t m, int64_t n, int64_t k) {
   if (op == DSL_OP_FP4)
     return mx(dsl::gemm_workspace_bytes(dsl::MODE_MXFP4, m, n, k),
               dsl::gemm_workspace_bytes(dsl::MODE_NVFP4, m, n, k));
+  if (op == DSL_OP_BF16) return dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, n, k);
   return 0;
 }
 
@@ -190,7 +191,8 @@ static int run_gemm(const char *fn, int mode, const uint8_t *a, const uint8_t *b
   p.M = (int)m;
   p.N = (int)n;
   p.K = (int)k;
-  p.Kb = (mode == dsl::MODE_MXFP4 || mode == dsl::MODE_NVFP4) ? (int)(k / 2) : (int)k;
+  p.Kb = (mode == dsl::MODE_MXFP4 || mode == dsl::MODE_NVFP4) ? (int)(k / 2)
+                                                                : (mode == dsl::MODE_BF16 ? (int)(2 * k) : (int)k);
   p.ldc = ldc;
   p.sa = sa;
   p.sb = sb;
@@ -236,6 +238,17 @@ int dsl_fp4_gemm(const uint8_t *a, const uint8_t *b, void *c, int64_t m, int64_t
                     global_a, global_b, ws, ws_bytes, stream);
   }
   return fail(DSL_ERR_ARG, "%s: unknown fmt %d", fn, fmt);
+}
+
+int dsl_bf16_gemm(const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k,
+                  int64_t ldc, int out_dtype, void *ws, size_t ws_bytes, void *stream) {
+  const char *fn = "dsl_bf16_gemm";
+  int rc = check_gemm_dims(fn, m, n, k, ldc, 8, out_dtype);
+  if (rc) return rc;
+  if (k >= (int64_t)1 << 30) return fail(DSL_ERR_ARG, "%s: k must be < 2^30", fn);
+  return run_gemm(fn, dsl::MODE_BF16, static_cast<const uint8_t *>(a),
+                  static_cast<const uint8_t *>(b), c, m, n, k, ldc, out_dtype, nullptr, nullptr,
+                  nullptr, nullptr, ws, ws_bytes, stream);
 }
 
 int dsl_grouped_fp8_gemm(const uint8_t *x, const uint8_t *w, void *y, const int32_t *offsets,

@@ -16,7 +16,8 @@
 //               accumulator as acc += part * (sa[m,g] * sb[n/128,g]);
 //   MXFP4       E8M0 bytes go straight into v_mfma_scale_f32_16x16x128_f8f6f4;
 //   NVFP4       E2M1 -> fp16 (hardware convert), times the E4M3 block scale
-//               in fp16 (exact), fp16 MFMA; global scales in the epilogue.
+//               in fp16 (exact), fp16 MFMA; global scales in the epilogue;
+//   BF16        unscaled bf16 MFMA (a stage is 64 elements of K).
 #pragma once
 
 #include "common.h"
@@ -177,6 +178,16 @@ DSL_DEV v4f mfma_fp8(const v8i &a, const v8i &b, const v4f &c) {
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 0, 0, 0);
 }
 
+// bf16: the lane's 32 bytes are 16 elements of K, fed as two 16x16x32
+// MFMAs (first and second 16-byte chunk; the same K order for A and W).
+DSL_DEV v4f mfma_bf16(const v8i &a, const v8i &b, const v4f &c) {
+  const v8bf a0 = __builtin_bit_cast(v8bf, (v4i){a[0], a[1], a[2], a[3]});
+  const v8bf a1 = __builtin_bit_cast(v8bf, (v4i){a[4], a[5], a[6], a[7]});
+  const v8bf b0 = __builtin_bit_cast(v8bf, (v4i){b[0], b[1], b[2], b[3]});
+  const v8bf b1 = __builtin_bit_cast(v8bf, (v4i){b[4], b[5], b[6], b[7]});
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1, b1, __builtin_amdgcn_mfma_f32_16x16x32_bf16(a0, b0, c, 0, 0, 0), 0, 0, 0);
+}
+
 template <int OPS>
 DSL_DEV v4f mfma_mx(const v4i &a, const v4i &b, const v4f &c, int sa, int sb) {
   const v8i a8 = {a[0], a[1], a[2], a[3], 0, 0, 0, 0};
@@ -209,7 +220,7 @@ DSL_DEV void stage_compute(const uint8_t *smem, int buf, v4f (&acc)[Cfg::TM][Cfg
   const uint8_t *sSb = smem + Cfg::OFF_SB + buf * Cfg::SB_BYTES;
   const int arow0 = wm * Cfg::WM + r16, brow0 = wn * Cfg::WN + r16;
 
-  if constexpr (MODE == MODE_FP8_TENSOR || MODE == MODE_FP8_BLOCK) {
+  if constexpr (MODE == MODE_FP8_TENSOR || MODE == MODE_FP8_BLOCK || MODE == MODE_BF16) {
     v8i bop[Cfg::TN];
 #pragma unroll
     for (int tn = 0; tn < Cfg::TN; ++tn) {
@@ -232,6 +243,9 @@ DSL_DEV void stage_compute(const uint8_t *smem, int buf, v4f (&acc)[Cfg::TM][Cfg
       if constexpr (MODE == MODE_FP8_TENSOR) {
 #pragma unroll
         for (int tn = 0; tn < Cfg::TN; ++tn) acc[tm][tn] = mfma_fp8(aop, bop[tn], acc[tm][tn]);
+      } else if constexpr (MODE == MODE_BF16) {
+#pragma unroll
+        for (int tn = 0; tn < Cfg::TN; ++tn) acc[tm][tn] = mfma_bf16(aop, bop[tn], acc[tm][tn]);
       } else {
         const v4f sa4 = *reinterpret_cast<const v4f *>(
             reinterpret_cast<const float *>(sSa) + wm * Cfg::WM + tm * 16 + 4 * g);

@@ -73,6 +73,7 @@ struct PersCfg {
   static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;
   static constexpr bool MX = MODE == MODE_MXFP4;
   static constexpr bool NV = MODE == MODE_NVFP4;
+  static constexpr bool BF16 = MODE == MODE_BF16;
   static constexpr bool SCALED = BLOCK || MX || NV;
   static constexpr int PKB = 128;                      // K bytes per pair (per row)
   static constexpr int CH = PKB / 16, RPI = 1024 / PKB;  // chunks per row, rows per DMA
@@ -404,6 +405,19 @@ DSL_DEV void mma_row(const Frag<Cfg> &fa, const Frag<Cfg> &fb, int i, v16f (&acc
                                   w8, a8, acc[i][j], 4, 4, 2 * P + 1, fb.bs[j], 2 * P + 1,
                                   fa.as[i]);
       }
+  } else if constexpr (Cfg::BF16) {
+    // the lane's 32 bytes are 16 bf16 of K: two 32x32x16 MFMAs, first and
+    // second 16-byte chunk (the same K order for A and W)
+#pragma unroll
+    for (int j = 0; j < Cfg::TN; ++j) {
+      const v8i &w = fb.b[j], &a = fa.a[i];
+      const v8bf w0 = __builtin_bit_cast(v8bf, (v4i){w[0], w[1], w[2], w[3]});
+      const v8bf w1 = __builtin_bit_cast(v8bf, (v4i){w[4], w[5], w[6], w[7]});
+      const v8bf a0 = __builtin_bit_cast(v8bf, (v4i){a[0], a[1], a[2], a[3]});
+      const v8bf a1 = __builtin_bit_cast(v8bf, (v4i){a[4], a[5], a[6], a[7]});
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w0, a0, FRESH ? zero : acc[i][j], 0, 0, 0);
+      acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w1, a1, acc[i][j], 0, 0, 0);
+    }
   } else {
 #pragma unroll
     for (int j = 0; j < Cfg::TN; ++j)
@@ -921,7 +935,7 @@ bool persist_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
   (void)N;
   if (Kb % 128 != 0 || Kb < 128) return false;          // whole pairs of 64-byte steps
   if (Kb >= (1 << 24)) return false;                     // 24-bit row offsets
-  if (mode == MODE_FP8_TENSOR) return true;
+  if (mode == MODE_FP8_TENSOR || mode == MODE_BF16) return true;
   // scaled modes: whole 16-byte scale quads per row, 16-byte aligned rows
   if (mode == MODE_FP8_BLOCK || mode == MODE_MXFP4) return scales16 && K % 512 == 0;
   if (mode == MODE_NVFP4) return scales16 && K % 256 == 0;   // 16 scale bytes per row and pair
@@ -934,6 +948,7 @@ hipError_t launch_gemm_persist(int mode, const GemmArgs &p, hipStream_t st) {
     case MODE_FP8_BLOCK: return launch_persist_mode<MODE_FP8_BLOCK>(p, st);
     case MODE_MXFP4: return launch_persist_mode<MODE_MXFP4>(p, st);
     case MODE_NVFP4: return launch_persist_mode<MODE_NVFP4>(p, st);
+    case MODE_BF16: return launch_persist_mode<MODE_BF16>(p, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -184,6 +184,12 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
     r.path = PATH_DECODE;
     return r;
   }
+  if (mode == MODE_BF16) {   // persistent kernel or the register-staged tiles
+    const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
+    if (persist_on && t256 >= 240 && persist_supported(mode, M, N, K, Kb, sc16))
+      r.path = PATH_PERSIST;
+    return r;
+  }
   const bool pipe_ok = pipe_forced != -2 && Kb % 128 == 0 && (mode == MODE_FP8_TENSOR || sc4);
   if (pipe_ok) {
     const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
@@ -202,7 +208,8 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
 }
 
 size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K) {
-  const int Kb = (mode == MODE_MXFP4 || mode == MODE_NVFP4) ? (int)(K / 2) : (int)K;
+  const int Kb = (mode == MODE_MXFP4 || mode == MODE_NVFP4) ? (int)(K / 2)
+                                                            : (mode == MODE_BF16 ? (int)(2 * K) : (int)K);
   const Route r = route_for(mode, (int)M, (int)N, (int)K, Kb, true, true);
   return (r.path == PATH_TILED && r.tiled.ksplit > 1)
              ? (size_t)((M * N + 3) / 4) * 4 * sizeof(float)
@@ -227,7 +234,9 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
     case MODE_FP8_TENSOR: launch_mode<MODE_FP8_TENSOR>(pl, p, st); break;
     case MODE_FP8_BLOCK: launch_mode<MODE_FP8_BLOCK>(pl, p, st); break;
     case MODE_MXFP4: launch_mode<MODE_MXFP4>(pl, p, st); break;
-    default: launch_mode<MODE_NVFP4>(pl, p, st); break;
+    case MODE_NVFP4: launch_mode<MODE_NVFP4>(pl, p, st); break;
+    case MODE_BF16: launch_mode<MODE_BF16>(pl, p, st); break;
+    default: return hipErrorInvalidValue;
   }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;

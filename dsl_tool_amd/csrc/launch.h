@@ -23,14 +23,14 @@ hipError_t launch_quant_nvfp4(const uint16_t *x, int64_t rows, int64_t cols, int
                               float *partial, hipStream_t st);
 
 // ---------------------------------------------------------------- GEMMs --
-enum GemmMode { MODE_FP8_TENSOR = 0, MODE_FP8_BLOCK = 1, MODE_MXFP4 = 2, MODE_NVFP4 = 3 };
+enum GemmMode { MODE_FP8_TENSOR = 0, MODE_FP8_BLOCK = 1, MODE_MXFP4 = 2, MODE_NVFP4 = 3, MODE_BF16 = 4 };
 
 struct GemmArgs {
   const uint8_t *a;      // [M][Kb] packed, K-major
   const uint8_t *b;      // [N][Kb] packed, K-major
   void *c;               // [M][ldc] bf16 or fp32
   int M, N, K;           // K in elements
-  int Kb;                // bytes per packed row (FP8: K, FP4: K/2)
+  int Kb;                // bytes per packed row (FP8: K, FP4: K/2, BF16: 2K)
   int64_t ldc;
   const void *sa;        // FP8_BLOCK: float [M][nkg]; MX: uint8 [M][K/32]; NV: uint8 [M][K/16]
   const void *sb;        // FP8_BLOCK: float [ceil(N/128)][nkg]; MX/NV as sa for N
@@ -45,8 +45,9 @@ struct GemmArgs {
 // variant 0: 256x256 tile, 8 waves; 1: 128x128 tile, 4 waves.
 hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_t st);
 
-// Persistent pipelined kernel (Kb % 128 == 0; FP8_TENSOR; FP8_BLOCK and
-// MXFP4 with 16-byte aligned scales and K % 512 == 0): one workgroup per CU
+// Persistent pipelined kernel (Kb % 128 == 0; FP8_TENSOR and BF16; FP8_BLOCK
+// and MXFP4 with 16-byte aligned scales and K % 512 == 0; NVFP4 with K % 256
+// == 0): one workgroup per CU
 // walks its 256x256 tiles with a ring of 128-byte-per-row pair slots running
 // across tile boundaries.
 bool persist_supported(int mode, int M, int N, int K, int Kb, bool scales16);

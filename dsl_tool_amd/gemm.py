@@ -9,6 +9,10 @@ The three registered entry points keep the reference's calling convention
 * ``fp4_gemm(A, B, fmt="mxfp4")`` -- ``gemm.fp4_gemm``, new name in the
   reference's ``<category>.<function>`` scheme (dispatcher/registry.py:6-8);
   semantics of cuda/gemm/fp4_gemm.cu:92-146 with MXFP4 / NVFP4 scales.
+* ``bf16_gemm(A, B)`` -- ``gemm.bf16_gemm`` (reference:
+  triton/gemm/gemm_kernels.py:46-65, registered at dispatcher/registry.py:134):
+  ``C = A @ B`` of bf16 A [M, K], B [K, N], fp32 accumulation and, as in the
+  reference, an fp32 result by default.
 * ``grouped_gemm(A, B, num_groups)`` -- ``gemm.grouped_gemm``
   (reference: triton/gemm/gemm_kernels.py:164-182).  An int third argument
   means fixed-size groups A [G, M, K], B [G, K, N]; a 1-D integer tensor of
@@ -173,6 +177,35 @@ def grouped_fp8_gemm_packed(qx, sx, qw, sw, offsets, *, out_dtype=torch.bfloat16
 
 
 # ------------------------------------------------------ registered callables --
+
+def bf16_gemm(A: torch.Tensor, B: torch.Tensor, *, out_dtype: torch.dtype = torch.float32,
+              out=None):
+    """BF16 GEMM ``C = A @ B`` with fp32 accumulation (fp32 result by default).
+
+    A [M, K] and B [K, N] must be bfloat16, as the reference asserts
+    (triton/gemm/gemm_kernels.py:47); K % 8 == 0.  ``B = W.t()`` of a
+    contiguous W [N, K] is read in place; any other layout of B (or a
+    non-contiguous A) is first copied to K-major rows on the GPU.
+    """
+    if A.dim() != 2 or B.dim() != 2:
+        raise ValueError("bf16_gemm expects A [M, K] and B [K, N]")
+    if A.dtype != torch.bfloat16 or B.dtype != torch.bfloat16:
+        raise TypeError(f"bf16_gemm: A and B must be bfloat16 (got {A.dtype}, {B.dtype})")
+    M, K = A.shape
+    K2, Nn = B.shape
+    if K != K2:
+        raise ValueError(f"K mismatch: A is [{M}, {K}], B is [{K2}, {Nn}]")
+    dev = _require_gpu(A, B)
+    a = A if A.is_contiguous() else A.contiguous()
+    w = _k_major(B)
+    c = out if out is not None else torch.empty((M, Nn), dtype=out_dtype, device=dev)
+    ws = _gemm_ws(N.OP_BF16, M, Nn, K, dev)
+    with torch.cuda.device(dev):
+        N.call("dsl_bf16_gemm", N.ptr(a), N.ptr(w), N.ptr(c), M, Nn, K, c.stride(0),
+               _out_code(c.dtype), N.ptr(ws), 0 if ws is None else ws.numel() * 4,
+               N.stream_of(dev))
+    return c
+
 
 def fp8_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=1.0, scale_b=1.0, *,
              granularity: str = "tensor", out_dtype: torch.dtype = torch.bfloat16):

@@ -41,7 +41,7 @@ enum {
 enum { DSL_OUT_BF16 = 0, DSL_OUT_F32 = 1 };
 enum { DSL_SCALE_TENSOR = 0, DSL_SCALE_BLOCK128 = 1 };
 enum { DSL_FMT_MXFP4 = 0, DSL_FMT_NVFP4 = 1 };
-enum { DSL_OP_FP8 = 0, DSL_OP_FP4 = 1, DSL_OP_GROUPED_FP8 = 2 };
+enum { DSL_OP_FP8 = 0, DSL_OP_FP4 = 1, DSL_OP_GROUPED_FP8 = 2, DSL_OP_BF16 = 3 };
 
 /* Last error message of the calling thread ("" when none). */
 const char *dsl_last_error(void);
@@ -128,6 +128,16 @@ int dsl_fp4_gemm(const uint8_t *a, const uint8_t *b, void *c,
                  const float *global_a, const float *global_b,
                  void *workspace, size_t workspace_bytes, void *stream);
 
+/* BF16 GEMM, fp32 accumulation: a [M][K] and b = W [N][K] bf16, both
+ * K-major rows (the reference's B[K, N] is W^T: pass the storage of B.t()).
+ * K % 8 == 0.  Replaces bf16_gemm / bf16_gemm_kernel
+ * (triton/gemm/gemm_kernels.py:11-65, registered as gemm.bf16_gemm,
+ * dispatcher/registry.py:134) and cuda/gemm/bf16_gemm.cu:41-143.
+ * Needs dsl_gemm_workspace_bytes(DSL_OP_BF16, m, n, k). */
+int dsl_bf16_gemm(const void *a, const void *b, void *c,
+                  int64_t m, int64_t n, int64_t k, int64_t ldc, int out_dtype,
+                  void *workspace, size_t workspace_bytes, void *stream);
+
 /* Grouped FP8 GEMM over variable-size groups (MoE experts / LoRA adapters).
  * Rows group_offsets[g] .. group_offsets[g+1]-1 of x [total_rows][K]
  * multiply w[g] (w is [num_groups][N][K]); y [total_rows][ldy].
@@ -143,8 +153,8 @@ int dsl_grouped_fp8_gemm(const uint8_t *x, const uint8_t *w, void *y,
                          int out_dtype, const float *scale_x, const float *scale_w,
                          void *stream);
 
-/* Workspace bytes dsl_fp8_gemm / dsl_fp4_gemm need for this shape
- * (op = DSL_OP_FP8 or DSL_OP_FP4; the larger of the plans of the op's two
+/* Workspace bytes dsl_fp8_gemm / dsl_fp4_gemm / dsl_bf16_gemm need for this
+ * shape (op = DSL_OP_FP8, DSL_OP_FP4 or DSL_OP_BF16; for FP8 / FP4 the larger of the plans of the op's two
  * scale modes / FP4 formats; 0 when none is needed).  The kernel choice
  * depends on the shape and on the scale pointers' alignment; with scale
  * arrays that are not 16-byte aligned a launch may fall back to a kernel

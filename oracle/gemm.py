@@ -109,6 +109,36 @@ def ref_grouped_fp8(qx, sx, qw, sw, offsets, f64=False):
     return round_to_bf16(out.astype(F32))
 
 
+def ref_bf16(a: np.ndarray, w: np.ndarray, f64: bool = True) -> np.ndarray:
+    """C = A @ W.T for bf16 operands held in float32 arrays, float32 result.
+
+    The reference accumulates bf16 tiles into an fp32 accumulator with
+    ``tl.dot`` and returns fp32 (triton/gemm/gemm_kernels.py:31-37, :50).
+    Each bf16 x bf16 product is exact in fp32, so the fp64 sum rounded once
+    to fp32 is the exact result up to that rounding; an fp32 accumulator
+    differs from it only by summation order.
+    """
+    return _mm(a, w, f64)
+
+
+def tiled_bf16_gemm(a: np.ndarray, w: np.ndarray, block_m=128, block_n=128, block_k=32):
+    """The reference's CPU path for bf16 restated: 128x128x32 tiles, fp32
+    accumulation over K tiles (tilelang/gemm/gemm_kernels.py:75-95).
+    a [M, K], w [N, K] float32 holding bf16; returns fp32 [M, N]."""
+    ta = torch.from_numpy(np.ascontiguousarray(a, np.float32))
+    tw = torch.from_numpy(np.ascontiguousarray(w, np.float32))
+    M, K = ta.shape
+    N = tw.shape[0]
+    c = torch.zeros(M, N, dtype=torch.float32)
+    for bm in range(0, M, block_m):
+        for bn in range(0, N, block_n):
+            acc = torch.zeros(min(block_m, M - bm), min(block_n, N - bn))
+            for bk in range(0, K, block_k):
+                acc += ta[bm:bm + block_m, bk:bk + block_k] @ tw[bn:bn + block_n, bk:bk + block_k].T
+            c[bm:bm + block_m, bn:bn + block_n] = acc
+    return c.numpy()
+
+
 def tiled_fp8_gemm(a_codes, w_codes, sa, sw, block_m=64, block_n=64, block_k=32):
     """The reference's CPU path restated: 64x64x32 tiles, fp32 accumulation
     over K tiles, scales applied to each finished tile

@@ -14,10 +14,10 @@ from dsl_tool_amd.dispatcher import cli as CLI
 from dsl_tool_amd.dispatcher import dispatcher as D
 from dsl_tool_amd.dispatcher.registry import KernelRegistry
 
-NAMES = {"gemm.fp8_gemm", "gemm.fp4_gemm", "gemm.grouped_gemm"}
+NAMES = {"gemm.bf16_gemm", "gemm.fp8_gemm", "gemm.fp4_gemm", "gemm.grouped_gemm"}
 
 
-def test_registry_holds_the_three_hip_entries():
+def test_registry_holds_the_four_hip_entries():
     reg = get_registry()
     ks = reg.list_kernels()
     assert {k["kernel_name"] for k in ks} == NAMES
@@ -25,6 +25,7 @@ def test_registry_holds_the_three_hip_entries():
     assert reg.get("GEMM.FP8_GEMM", "HIP").fn is G.fp8_gemm       # keys are case-insensitive
     assert reg.get("gemm.fp4_gemm", "hip").fn is G.fp4_gemm
     assert reg.get("gemm.grouped_gemm", "hip").fn is G.grouped_gemm
+    assert reg.get("gemm.bf16_gemm", "hip").fn is G.bf16_gemm
     assert reg.list_backends_for("gemm.fp8_gemm") == ["hip"]
     assert reg.get("gemm.fp8_gemm", "triton") is None
     assert get_registry() is reg
@@ -152,7 +153,7 @@ def client():
 def test_rest_discovery(client):
     assert client.get("/health").json() == {"status": "ok", "service": "kernel-dispatcher"}
     body = client.get("/api/v1/kernels").json()
-    assert body["count"] == 3 and {k["kernel_name"] for k in body["kernels"]} == NAMES
+    assert body["count"] == len(NAMES) and {k["kernel_name"] for k in body["kernels"]} == NAMES
     det = client.get("/api/v1/kernels/gemm.fp8_gemm", params={"backend": "hip"}).json()
     assert det["backends_available"] == ["hip"] and "scale_a" in det["input_schema"]
     assert client.get("/api/v1/kernels/gemm.nope", params={"backend": "hip"}).status_code == 404

@@ -56,6 +56,26 @@ def test_fp8_gemm_argument_validation(lib):
     assert lib.dsl_fp8_gemm(None, None, None, 0, 16, 16, 16, 0, 0, fake, fake, None, 0, None) == 0
 
 
+def test_bf16_gemm_argument_validation(lib):
+    fake = 1 << 20
+    rc = lib.dsl_bf16_gemm(fake, fake, fake, 16, 16, 12, 16, 0, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "multiple of 8" in _err(lib)
+    rc = lib.dsl_bf16_gemm(fake, fake, fake, 16, 32, 16, 16, 0, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "ldc" in _err(lib)
+    rc = lib.dsl_bf16_gemm(fake + 2, fake, fake, 16, 16, 16, 16, 0, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "aligned" in _err(lib)
+    rc = lib.dsl_bf16_gemm(fake, fake, fake, 16, 16, 16, 16, 5, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "out_dtype" in _err(lib)
+    # small M splits K over a workspace; without one the call is refused
+    need = lib.dsl_gemm_workspace_bytes(N.OP_BF16, 16, 256, 4096)
+    assert need >= 16 * 256 * 4
+    rc = lib.dsl_bf16_gemm(fake, fake, fake, 16, 256, 4096, 256, 0, None, 0, None)
+    assert rc == N.DSL_ERR_WORKSPACE
+    # large problems run on the persistent kernel without workspace
+    assert lib.dsl_gemm_workspace_bytes(N.OP_BF16, 4096, 4096, 4096) == 0
+    assert lib.dsl_bf16_gemm(None, None, None, 0, 16, 16, 16, 0, None, 0, None) == 0
+
+
 def test_workspace_query_matches_the_planned_path(lib):
     # skinny M with K a multiple of 1024 takes the single-pass decode kernel
     assert lib.dsl_gemm_workspace_bytes(N.OP_FP8, 16, 8192, 8192) == 0

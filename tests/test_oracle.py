@@ -241,6 +241,32 @@ def test_tiled_reference_cpu_path_matches_dense_oracle():
     assert np.allclose(tiled, dense, rtol=1e-5, atol=1e-6)
 
 
+def test_ref_bf16_matches_exact_rational_brute_force():
+    # bf16 operands: every product is exact, so the exact sum (Fractions) rounded
+    # once to fp32 is the answer; a transposed operand or a dropped K term fails.
+    from fractions import Fraction
+    rng = np.random.default_rng(8)
+    a = F.round_to_bf16((rng.standard_normal((5, 24)) * 3).astype(np.float32))
+    w = F.round_to_bf16(rng.standard_normal((7, 24)).astype(np.float32))
+    got = OG.ref_bf16(a, w)
+    want = np.empty((5, 7), np.float32)
+    for i in range(5):
+        for j in range(7):
+            want[i, j] = np.float32(float(sum(Fraction(float(a[i, k])) * Fraction(float(w[j, k]))
+                                              for k in range(24))))
+    assert np.array_equal(got, want)
+    assert not np.array_equal(OG.ref_bf16(a[:, :23], w[:, :23]), want)
+    sq = F.round_to_bf16(rng.standard_normal((24, 24)).astype(np.float32))
+    assert not np.allclose(OG.ref_bf16(sq, sq), OG.ref_bf16(sq, sq.T.copy()), rtol=1e-3)
+
+
+def test_tiled_bf16_reference_cpu_path_matches_dense_oracle():
+    rng = np.random.default_rng(9)
+    a = F.round_to_bf16(rng.standard_normal((150, 100)).astype(np.float32))
+    w = F.round_to_bf16(rng.standard_normal((140, 100)).astype(np.float32))
+    assert np.allclose(OG.tiled_bf16_gemm(a, w), OG.ref_bf16(a, w), rtol=1e-5, atol=1e-5)
+
+
 def test_grouped_empty_groups_and_permutation():
     rng = np.random.default_rng(7)
     counts = [3, 0, 2, 0]
