@@ -236,6 +236,37 @@ def build_cases(names, dev):
         return Case(name, 0.0, nbytes, PEAK_FP8_TFLOPS, "hbm", launch, 1,
                     f"quantize {kind} [{r}, {k}] bf16 ({passes} read pass{'es' if passes > 1 else ''})")
 
+    def producer_case(name, kind, r, c, fused=True):
+        """RMSNorm / SwiGLU with the output quantized to FP8 1x128 groups:
+        fused (one launch, x read once, codes written) or unfused (the
+        operator writes bf16 y, then the activation quantizer reads it)."""
+        ncol_in = 2 * c if kind == "swiglu" else c
+        x = rnd((r, ncol_in), 8)
+        w = torch.ones(c, dtype=torch.bfloat16, device=dev)
+        q = torch.empty((r, c), dtype=torch.uint8, device=dev)
+        sc = torch.empty((r, -(-c // 128)), dtype=torch.float32, device=dev)
+        y = torch.empty((r, c), dtype=torch.bfloat16, device=dev)
+        yp = 0 if fused else y.data_ptr()
+
+        def produce(stream):
+            if kind == "rmsnorm":
+                return L.dsl_rmsnorm_quant(x.data_ptr(), r, c, ncol_in, w.data_ptr(), N.W_BF16,
+                                           1e-6, N.QFMT_FP8_G128, q.data_ptr(), sc.data_ptr(),
+                                           yp or None, c, stream)
+            return L.dsl_swiglu_quant(x.data_ptr(), r, c, ncol_in, N.QFMT_FP8_G128, q.data_ptr(),
+                                      sc.data_ptr(), yp or None, c, stream)
+
+        def launch(i, stream):
+            rc = produce(stream)
+            if rc or fused:
+                return rc
+            return L.dsl_quant_fp8_blocks(y.data_ptr(), r, c, c, 1, 1, 128, q.data_ptr(),
+                                          sc.data_ptr(), stream)
+        out_b = r * c + sc.numel() * 4
+        nbytes = 2 * r * ncol_in + 2 * c + out_b if fused else 2 * r * ncol_in + 2 * c + 4 * r * c + out_b
+        return Case(name, 0.0, nbytes, PEAK_FP8_TFLOPS, "hbm", launch, 1,
+                    f"{kind} [{r}, {ncol_in}] -> FP8 1x128, {'fused' if fused else 'unfused (bf16 y, then quantize)'}")
+
     builders = {
         "fp8_block_m4096": lambda: fp8_case("fp8_block_m4096", 4096, 7168, 4096, True,
                                             W.activations(2, 4096, 4096, outliers=True),
@@ -252,6 +283,12 @@ def build_cases(names, dev):
         "bf16_8192": lambda: bf16_case("bf16_8192", 8192, 8192, 8192),
         "bf16_m4096": lambda: bf16_case("bf16_m4096", 4096, 7168, 4096),
         "bf16_m16": lambda: bf16_case("bf16_m16", 16, 7168, 4096),
+        "rmsnorm_quant_fp8": lambda: producer_case("rmsnorm_quant_fp8", "rmsnorm", 4096, 7168),
+        "rmsnorm_then_quant_fp8": lambda: producer_case("rmsnorm_then_quant_fp8", "rmsnorm", 4096, 7168,
+                                                        fused=False),
+        "swiglu_quant_fp8": lambda: producer_case("swiglu_quant_fp8", "swiglu", 4096, 14336),
+        "swiglu_then_quant_fp8": lambda: producer_case("swiglu_then_quant_fp8", "swiglu", 4096, 14336,
+                                                       fused=False),
         "quant_fp8_block128_w": lambda: quant_case("quant_fp8_block128_w", "fp8_block128", 7168, 4096),
         "quant_fp8_row128_a": lambda: quant_case("quant_fp8_row128_a", "fp8_row128", 4096, 4096),
         "quant_fp8_tensor_w": lambda: quant_case("quant_fp8_tensor_w", "fp8_tensor", 4096, 4096),
@@ -267,6 +304,7 @@ ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor
              "fp8_tensor_8192",
              "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe",
              "bf16_8192", "bf16_m4096", "bf16_m16",
+             "rmsnorm_quant_fp8", "rmsnorm_then_quant_fp8", "swiglu_quant_fp8", "swiglu_then_quant_fp8",
              "quant_fp8_block128_w", "quant_fp8_row128_a", "quant_fp8_tensor_w", "quant_mxfp4_w",
              "quant_nvfp4_w"]
 

@@ -30,7 +30,9 @@ OUT_BF16, OUT_F32 = 0, 1
 SCALE_TENSOR, SCALE_BLOCK128 = 0, 1
 FMT_MXFP4, FMT_NVFP4 = 0, 1
 OP_FP8, OP_FP4, OP_GROUPED_FP8, OP_BF16 = 0, 1, 2, 3
-ABI_VERSION = 2
+QFMT_FP8_G128, QFMT_MXFP4 = 0, 1
+W_BF16, W_F32 = 0, 1
+ABI_VERSION = 3
 
 
 class DslLibraryError(ImportError):
@@ -64,6 +66,9 @@ SIGNATURES = {
     "dsl_grouped_fp8_gemm": (_i32, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i32,
                                     _vp, _vp, _vp]),
     "dsl_gemm_workspace_bytes": (_sz, [_i32, _i64, _i64, _i64]),
+    "dsl_rmsnorm_quant": (_i32, [_vp, _i64, _i64, _i64, _vp, _i32, ctypes.c_float, _i32, _vp, _vp,
+                                 _vp, _i64, _vp]),
+    "dsl_swiglu_quant": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _i64, _vp]),
 }
 
 _lib = None

@@ -79,7 +79,7 @@ extern "C" {
 
 const char *dsl_last_error(void) { return g_err.c_str(); }
 
-int dsl_abi_version(void) { return 2; }
+int dsl_abi_version(void) { return 3; }
 
 size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
   (void)rows;
@@ -278,6 +278,75 @@ int dsl_grouped_fp8_gemm(const uint8_t *x, const uint8_t *w, void *y, const int3
   p.sw = sw;
   p.out_f32 = out_dtype == DSL_OUT_F32;
   return hip_status(dsl::launch_grouped_fp8(p, static_cast<hipStream_t>(stream)), fn);
+}
+
+static int run_fused(const char *fn, int prod, const void *x, int64_t rows, int64_t cols,
+                     int64_t ldx, const void *w, int w_dtype, float eps, int qfmt, void *q,
+                     void *scales, void *y, int64_t ldy, void *stream) {
+  if (rows < 0 || cols <= 0)
+    return fail(DSL_ERR_ARG, "%s: need rows >= 0 and cols > 0 (got %lld, %lld)", fn,
+                (long long)rows, (long long)cols);
+  if (rows >= (int64_t)1 << 31) return fail(DSL_ERR_ARG, "%s: rows must be < 2^31", fn);
+  if (qfmt != DSL_QFMT_FP8_G128 && qfmt != DSL_QFMT_MXFP4)
+    return fail(DSL_ERR_ARG, "%s: unknown qfmt %d", fn, qfmt);
+  const int mult = qfmt == DSL_QFMT_MXFP4 ? 32 : 8;
+  if (cols % mult != 0)
+    return fail(DSL_ERR_ARG, "%s: cols=%lld must be a multiple of %d", fn, (long long)cols, mult);
+  if (prod == dsl::PROD_RMSNORM && cols > 32768)
+    return fail(DSL_ERR_UNSUPPORTED, "%s: cols=%lld > 32768 (one workgroup holds a row)", fn,
+                (long long)cols);
+  if (rows * ((cols + 127) / 128) >= ((int64_t)1 << 32) / 2)
+    return fail(DSL_ERR_ARG, "%s: too many scale groups", fn);
+  const int64_t need = prod == dsl::PROD_SWIGLU ? 2 * cols : cols;
+  if (ldx < need || ldx % 8 != 0)
+    return fail(DSL_ERR_ARG, "%s: ldx=%lld must be >= %lld and a multiple of 8", fn,
+                (long long)ldx, (long long)need);
+  if (rows == 0) return ok();
+  int rc;
+  if ((rc = check_out(fn, x, "x")) || (rc = check_out(fn, q, "q")) ||
+      (rc = check_out(fn, scales, "scales")))
+    return rc;
+  if (prod == dsl::PROD_RMSNORM) {
+    if ((rc = check_out(fn, w, "weight"))) return rc;
+    if (w_dtype != DSL_W_BF16 && w_dtype != DSL_W_F32)
+      return fail(DSL_ERR_ARG, "%s: unknown weight dtype %d", fn, w_dtype);
+    if (!(eps >= 0.f)) return fail(DSL_ERR_ARG, "%s: eps must be >= 0", fn);
+  }
+  if (y) {
+    if ((rc = check_out(fn, y, "y"))) return rc;
+    if (ldy < cols || ldy % 8 != 0)
+      return fail(DSL_ERR_ARG, "%s: ldy=%lld must be >= cols and a multiple of 8", fn,
+                  (long long)ldy);
+  }
+  dsl::FusedArgs p;
+  p.x = static_cast<const uint16_t *>(x);
+  p.ldx = ldx;
+  p.w = w;
+  p.w_f32 = w_dtype == DSL_W_F32;
+  p.rows = (int)rows;
+  p.cols = (int)cols;
+  p.eps = eps;
+  p.q = static_cast<uint8_t *>(q);
+  p.scales = scales;
+  p.y = static_cast<uint16_t *>(y);
+  p.ldy = ldy;
+  return hip_status(dsl::launch_fused_quant(prod, qfmt == DSL_QFMT_MXFP4 ? dsl::QF_MXFP4
+                                                                         : dsl::QF_FP8_G128,
+                                            p, static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+int dsl_rmsnorm_quant(const void *x, int64_t rows, int64_t cols, int64_t ldx, const void *weight,
+                      int weight_dtype, float eps, int qfmt, void *q, void *scales, void *y,
+                      int64_t ldy, void *stream) {
+  return run_fused("dsl_rmsnorm_quant", dsl::PROD_RMSNORM, x, rows, cols, ldx, weight,
+                   weight_dtype, eps, qfmt, q, scales, y, ldy, stream);
+}
+
+int dsl_swiglu_quant(const void *x, int64_t rows, int64_t hidden, int64_t ldx, int qfmt, void *q,
+                     void *scales, void *y, int64_t ldy, void *stream) {
+  return run_fused("dsl_swiglu_quant", dsl::PROD_SWIGLU, x, rows, hidden, ldx, nullptr,
+                   DSL_W_BF16, 0.f, qfmt, q, scales, y, ldy, stream);
 }
 
 }  // extern "C"

@@ -84,4 +84,23 @@ hipError_t launch_grouped_fp8(GroupedArgs args, hipStream_t st);
 bool grouped_persist_supported(const GroupedArgs &args);
 hipError_t launch_grouped_persist(const GroupedArgs &args, hipStream_t st);
 
+// -------------------------------------------- fused quantize producers --
+enum { PROD_RMSNORM = 0, PROD_SWIGLU = 1 };
+enum { QF_FP8_G128 = 0, QF_MXFP4 = 1 };
+
+struct FusedArgs {
+  const uint16_t *x;     // RMSNorm: [rows][cols]; SwiGLU: [rows][2*cols] (gate | up)
+  int64_t ldx;           // row stride of x (elements)
+  const void *w;         // RMSNorm weight [cols], bf16 or fp32 (w_f32)
+  bool w_f32;
+  int rows, cols;        // cols = output row length (SwiGLU: hidden)
+  float eps;
+  uint8_t *q;            // FP8 [rows][cols] / MXFP4 [rows][cols/2]
+  void *scales;          // FP8: float [rows][ceil(cols/128)]; MXFP4: E8M0 [rows][cols/32]
+  uint16_t *y;           // optional bf16 output [rows][ldy] (nullptr: none)
+  int64_t ldy;
+};
+// cols % 8 == 0 (MXFP4: % 32); RMSNorm: cols <= 32768 (one workgroup per row).
+hipError_t launch_fused_quant(int prod, int qf, const FusedArgs &p, hipStream_t st);
+
 }  // namespace dsl

@@ -103,6 +103,10 @@ class KernelRegistry:
             self.register(name, "hip", getattr(gemm, attr), desc,
                           input_schema=gemm_input_schema(name),
                           output_schema=gemm_output_schema(name))
+        fused = importlib.import_module("dsl_tool_amd.fused")
+        for name, attr, desc, ins, outs in HIP_PRODUCER_ENTRIES:
+            self.register(name, "hip", getattr(fused, attr), desc, input_schema=dict(ins),
+                          output_schema=dict(outs))
 
 
 HIP_GEMM_ENTRIES = (
@@ -114,6 +118,24 @@ HIP_GEMM_ENTRIES = (
      "FP4 E2M1 GEMM: MXFP4 (E8M0 / 32, scaled MFMA) or NVFP4 (E4M3 / 16 + fp32 global)"),
     ("gemm.grouped_gemm", "grouped_gemm",
      "Grouped FP8 GEMM for MoE / LoRA: fixed [G,M,K] or variable-size groups by offsets"),
+)
+
+
+# The step before the GEMM, quantized in registers (new names in the
+# reference's <category>.<function> scheme, next to normalization.rmsnorm and
+# activations.swiglu, dispatcher/registry.py:146,158).
+_PRODUCER_OUT = {"q": "uint8 Tensor: E4M3 [rows, cols] (fmt 'fp8') | packed E2M1 [rows, cols/2] ('mxfp4')",
+                 "scales": "fp32 [rows, ceil(cols/128)] ('fp8') | E8M0 uint8 [rows, cols/32] ('mxfp4')"}
+HIP_PRODUCER_ENTRIES = (
+    ("normalization.rmsnorm_quant", "rmsnorm_quant",
+     "RMSNorm y = w·x/√(mean(x²)+ε) quantized in registers to FP8 1x128 groups or MXFP4",
+     {"x": "Tensor[batch, hidden] bf16", "weight": "Tensor[hidden] bf16/fp32",
+      "eps": "float (default 1e-6)", "fmt": "str 'fp8' (default) | 'mxfp4'",
+      "return_y": "bool: also return the bf16 RMSNorm output"}, _PRODUCER_OUT),
+    ("activations.swiglu_quant", "swiglu_quant",
+     "SwiGLU SiLU(gate)×up of input=[B,2H] quantized in registers to FP8 1x128 groups or MXFP4",
+     {"input": "Tensor[batch, 2*hidden] bf16", "fmt": "str 'fp8' (default) | 'mxfp4'",
+      "return_y": "bool: also return the bf16 SwiGLU output"}, _PRODUCER_OUT),
 )
 
 

@@ -42,6 +42,8 @@ enum { DSL_OUT_BF16 = 0, DSL_OUT_F32 = 1 };
 enum { DSL_SCALE_TENSOR = 0, DSL_SCALE_BLOCK128 = 1 };
 enum { DSL_FMT_MXFP4 = 0, DSL_FMT_NVFP4 = 1 };
 enum { DSL_OP_FP8 = 0, DSL_OP_FP4 = 1, DSL_OP_GROUPED_FP8 = 2, DSL_OP_BF16 = 3 };
+enum { DSL_QFMT_FP8_G128 = 0, DSL_QFMT_MXFP4 = 1 };
+enum { DSL_W_BF16 = 0, DSL_W_F32 = 1 };
 
 /* Last error message of the calling thread ("" when none). */
 const char *dsl_last_error(void);
@@ -152,6 +154,34 @@ int dsl_grouped_fp8_gemm(const uint8_t *x, const uint8_t *w, void *y,
                          int64_t total_rows, int64_t n, int64_t k, int64_t ldy,
                          int out_dtype, const float *scale_x, const float *scale_w,
                          void *stream);
+
+/* ------------------------------------------- fused quantize producers --
+ * The step before the GEMM with its output quantized in registers: the
+ * bf16 result of the reference operator (fp32 math, RNE to bf16) goes
+ * straight into activation codes, as dsl_quant_fp8_blocks(1, 128) /
+ * dsl_quant_mxfp4 would encode it:
+ *   DSL_QFMT_FP8_G128: q [rows][cols] E4M3, scales float [rows][ceil(cols/128)];
+ *   DSL_QFMT_MXFP4:    q [rows][cols/2] packed E2M1, scales E8M0 [rows][cols/32].
+ * y (optional, NULL for none) receives the bf16 values too, [rows][ldy].
+ * cols % 8 == 0 (MXFP4: % 32), RMSNorm cols <= 32768; x, q, scales, y, weight
+ * 16-byte aligned; ldx, ldy multiples of 8. */
+
+/* RMSNorm: y = (x * (1 / sqrt(sum(x^2) / cols + eps))) * w, x [rows][ldx]
+ * bf16, weight [cols] bf16 or fp32 (weight_dtype).  Replaces rmsnorm followed
+ * by the activation quantizer (triton/normalization/norm_kernels.py:21-30,
+ * :110-116, registered as normalization.rmsnorm, dispatcher/registry.py:146;
+ * the sum's order is this build's). */
+int dsl_rmsnorm_quant(const void *x, int64_t rows, int64_t cols, int64_t ldx,
+                      const void *weight, int weight_dtype, float eps,
+                      int qfmt, void *q, void *scales, void *y, int64_t ldy, void *stream);
+
+/* SwiGLU: y = (g * (1 / (1 + exp(-g)))) * u with x [rows][ldx] bf16 holding
+ * gate = x[:, :hidden], up = x[:, hidden:2*hidden].  Replaces swiglu followed
+ * by the activation quantizer (triton/activations/activation_kernels.py:
+ * 28-36, :105-115, registered as activations.swiglu, registry.py:158;
+ * cuda/activations/fused_gated_activations.cu:75-90). */
+int dsl_swiglu_quant(const void *x, int64_t rows, int64_t hidden, int64_t ldx,
+                     int qfmt, void *q, void *scales, void *y, int64_t ldy, void *stream);
 
 /* Workspace bytes dsl_fp8_gemm / dsl_fp4_gemm / dsl_bf16_gemm need for this
  * shape (op = DSL_OP_FP8, DSL_OP_FP4 or DSL_OP_BF16; for FP8 / FP4 the larger of the plans of the op's two

@@ -7,7 +7,10 @@ fp32/fp64 matmuls, what the reference computes on its quantized GEMM path:
 * quant.py   -- the quantize/pack contract (per-tensor, block-wise FP8,
                 MXFP4, NVFP4) that the HIP kernels must match bit for bit.
 * gemm.py    -- dequantize -> fp32 matmul references, the reference's tiled
-                CPU path restated, and the grouped (MoE) reference.
+                CPU path restated, the grouped (MoE) reference, and the
+                exact-sum bf16 GEMM reference.
+* fused.py   -- the bf16 values the fused quantize producers encode
+                (RMSNorm, SwiGLU).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s
 ``cpu_baseline`` leg may import this package, and only as the checker or the

@@ -14,10 +14,11 @@ from dsl_tool_amd.dispatcher import cli as CLI
 from dsl_tool_amd.dispatcher import dispatcher as D
 from dsl_tool_amd.dispatcher.registry import KernelRegistry
 
-NAMES = {"gemm.bf16_gemm", "gemm.fp8_gemm", "gemm.fp4_gemm", "gemm.grouped_gemm"}
+NAMES = {"gemm.bf16_gemm", "gemm.fp8_gemm", "gemm.fp4_gemm", "gemm.grouped_gemm",
+         "normalization.rmsnorm_quant", "activations.swiglu_quant"}
 
 
-def test_registry_holds_the_four_hip_entries():
+def test_registry_holds_the_hip_entries():
     reg = get_registry()
     ks = reg.list_kernels()
     assert {k["kernel_name"] for k in ks} == NAMES
@@ -26,6 +27,10 @@ def test_registry_holds_the_four_hip_entries():
     assert reg.get("gemm.fp4_gemm", "hip").fn is G.fp4_gemm
     assert reg.get("gemm.grouped_gemm", "hip").fn is G.grouped_gemm
     assert reg.get("gemm.bf16_gemm", "hip").fn is G.bf16_gemm
+    from dsl_tool_amd import fused as FU
+    assert reg.get("normalization.rmsnorm_quant", "hip").fn is FU.rmsnorm_quant
+    assert reg.get("activations.swiglu_quant", "hip").fn is FU.swiglu_quant
+    assert "weight" in reg.get("normalization.rmsnorm_quant", "hip").input_schema
     assert reg.list_backends_for("gemm.fp8_gemm") == ["hip"]
     assert reg.get("gemm.fp8_gemm", "triton") is None
     assert get_registry() is reg

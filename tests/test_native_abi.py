@@ -76,6 +76,24 @@ def test_bf16_gemm_argument_validation(lib):
     assert lib.dsl_bf16_gemm(None, None, None, 0, 16, 16, 16, 0, None, 0, None) == 0
 
 
+def test_fused_producer_argument_validation(lib):
+    fake = 1 << 20
+    rc = lib.dsl_rmsnorm_quant(fake, 4, 40, 40, fake, N.W_BF16, 1e-6, N.QFMT_MXFP4, fake, fake,
+                               None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "multiple of 32" in _err(lib)
+    rc = lib.dsl_rmsnorm_quant(fake, 4, 65536, 65536, fake, N.W_BF16, 1e-6, N.QFMT_FP8_G128, fake,
+                               fake, None, 0, None)
+    assert rc == N.DSL_ERR_UNSUPPORTED
+    rc = lib.dsl_swiglu_quant(fake, 4, 64, 100, N.QFMT_FP8_G128, fake, fake, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "ldx" in _err(lib)
+    rc = lib.dsl_swiglu_quant(fake, 4, 64, 128, 9, fake, fake, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "qfmt" in _err(lib)
+    rc = lib.dsl_rmsnorm_quant(fake, 4, 64, 64, fake + 2, N.W_BF16, 1e-6, N.QFMT_FP8_G128, fake,
+                               fake, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "weight" in _err(lib)
+    assert lib.dsl_swiglu_quant(None, 0, 64, 128, 0, None, None, None, 0, None) == 0
+
+
 def test_workspace_query_matches_the_planned_path(lib):
     # skinny M with K a multiple of 1024 takes the single-pass decode kernel
     assert lib.dsl_gemm_workspace_bytes(N.OP_FP8, 16, 8192, 8192) == 0

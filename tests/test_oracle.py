@@ -267,6 +267,41 @@ def test_tiled_bf16_reference_cpu_path_matches_dense_oracle():
     assert np.allclose(OG.tiled_bf16_gemm(a, w), OG.ref_bf16(a, w), rtol=1e-5, atol=1e-5)
 
 
+def test_rmsnorm_oracle_against_float64_and_closed_form():
+    from oracle import fused as OF
+    rng = np.random.default_rng(10)
+    x = F.round_to_bf16((rng.standard_normal((20, 384)) * 2).astype(np.float32))
+    w = F.round_to_bf16((1 + 0.1 * rng.standard_normal(384)).astype(np.float32))
+    y = OF.rmsnorm_bf16(x, w, 1e-6)
+    x64 = x.astype(np.float64)
+    y64 = x64 / np.sqrt((x64 ** 2).mean(axis=1, keepdims=True) + 1e-6) * w
+    d = np.abs(F.f32_to_bf16_bits(y).astype(np.int32) -
+               F.f32_to_bf16_bits(y64.astype(np.float32)).astype(np.int32))
+    assert d.max() <= 1 and (d > 0).mean() < 0.01
+    # a constant row c normalises to sign(c) * w (up to eps)
+    c = np.full((1, 64), -3.0, np.float32)
+    assert np.array_equal(OF.rmsnorm_bf16(c, np.ones(64, np.float32), 0.0), -np.ones((1, 64), np.float32))
+    # dropping the weight or squaring the wrong thing is caught by the fp64 check
+    assert not np.allclose(OF.rmsnorm_bf16(x, np.ones(384, np.float32)), y64, rtol=1e-2)
+
+
+def test_swiglu_oracle_against_float64_and_limits():
+    from oracle import fused as OF
+    rng = np.random.default_rng(11)
+    x = F.round_to_bf16((rng.standard_normal((16, 256)) * 4).astype(np.float32))
+    y = OF.swiglu_bf16(x)
+    g, u = x[:, :128].astype(np.float64), x[:, 128:].astype(np.float64)
+    y64 = g / (1 + np.exp(-g)) * u
+    d = np.abs(F.f32_to_bf16_bits(y).astype(np.int32) -
+               F.f32_to_bf16_bits(y64.astype(np.float32)).astype(np.int32))
+    assert d.max() <= 1
+    lim = np.array([[0.0, 30.0, -30.0, 1.0, 2.0, 2.0, 2.0, 0.5]], np.float32)
+    out = OF.swiglu_bf16(lim)
+    assert out[0, 0] == 0 and out[0, 1] == 60.0 and -1e-10 < out[0, 2] < 0   # silu(-30) = -30 e^-30
+    # gate and up swapped is a different function
+    assert not np.allclose(OF.swiglu_bf16(np.concatenate([x[:, 128:], x[:, :128]], 1)), y)
+
+
 def test_grouped_empty_groups_and_permutation():
     rng = np.random.default_rng(7)
     counts = [3, 0, 2, 0]
