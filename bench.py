@@ -236,6 +236,71 @@ def build_cases(names, dev):
         return Case(name, 0.0, nbytes, PEAK_FP8_TFLOPS, "hbm", launch, 1,
                     f"quantize {kind} [{r}, {k}] bf16 ({passes} read pass{'es' if passes > 1 else ''})")
 
+    def moe_case(name, stage):
+        """BASELINE config 5 routing (4096 tokens, top-8 of 64 experts,
+        K=2048, N=1536) through the MoE glue: one stage, or the whole
+        projection route -> permute + quantize -> grouped GEMM -> combine."""
+        ids, wts = W.moe_routing()
+        T, k = ids.shape
+        E, Nn, K = 64, 1536, 2048
+        ids, wts = ids.to(dev), wts.to(dev)
+        x = rnd((T, K), 9)
+        w = rnd((E * Nn, K), 10, 0.02)
+        qw, sw = Q.quant_fp8_blocks(w, 1, K)
+        del w
+        rows = T * k
+        off = torch.empty(E + 1, dtype=torch.int32, device=dev)
+        dest = torch.empty(rows, dtype=torch.int32, device=dev)
+        src = torch.empty(rows, dtype=torch.int32, device=dev)
+        nbw = L.dsl_moe_route_workspace_bytes(T, k, E)
+        rws = torch.empty(max(nbw, 4) // 4, dtype=torch.int32, device=dev)
+        qx = torch.empty((rows, K), dtype=torch.uint8, device=dev)
+        sx = torch.empty(rows, dtype=torch.float32, device=dev)
+        y = torch.empty((rows, Nn), dtype=torch.bfloat16, device=dev)
+        out = torch.empty((T, Nn), dtype=torch.bfloat16, device=dev)
+
+        def route(st):
+            return L.dsl_moe_route(ids.data_ptr(), T, k, E, off.data_ptr(), dest.data_ptr(),
+                                   src.data_ptr(), rws.data_ptr(), nbw, st)
+
+        def permute(st):
+            return L.dsl_moe_permute_quant(x.data_ptr(), T, K, K, src.data_ptr(), off.data_ptr(), E,
+                                           rows, qx.data_ptr(), sx.data_ptr(), st)
+
+        def grouped(st):
+            return L.dsl_grouped_fp8_gemm(qx.data_ptr(), qw.data_ptr(), y.data_ptr(), off.data_ptr(),
+                                          E, rows, Nn, K, Nn, N.OUT_BF16, sx.data_ptr(),
+                                          sw.data_ptr(), st)
+
+        def combine(st):
+            return L.dsl_moe_combine(y.data_ptr(), rows, Nn, Nn, dest.data_ptr(), wts.data_ptr(), T, k,
+                                     out.data_ptr(), Nn, N.OUT_BF16, st)
+        s0 = torch.cuda.current_stream().cuda_stream
+        for f in (route, permute, grouped, combine):     # tables and buffers valid before timing
+            assert f(s0) == 0
+        stages = {"route": [route], "permute": [permute], "combine": [combine],
+                  "layer": [route, permute, grouped, combine]}[stage]
+
+        def launch(i, stream):
+            for f in stages:
+                rc = f(stream)
+                if rc:
+                    return rc
+            return 0
+        counts = W.moe_counts()
+        nonempty = int((counts > 0).sum())
+        flops = 2.0 * rows * Nn * K if stage == "layer" else 0.0
+        nbytes = {"route": 4 * rows * 3 + 4 * (E + 1),
+                  "permute": 2 * rows * K + rows * K + 4 * rows,
+                  "combine": 2 * rows * Nn + 4 * rows * 2 + 2 * T * Nn,
+                  "layer": 2 * T * K + nonempty * Nn * K + 2 * T * Nn}[stage]
+        what = {"route": "MoE route (stable counting sort) of 4096x8 ids over 64 experts",
+                "permute": "MoE permute + per-row E4M3 of 32768 token rows, K=2048 (x re-read per slot)",
+                "combine": "MoE weighted combine of 32768 rows, N=1536 -> 4096 tokens",
+                "layer": "MoE projection cfg5: route + permute/quant + grouped FP8 GEMM + combine"}[stage]
+        return Case(name, flops, nbytes, PEAK_FP8_TFLOPS, "mfma" if stage == "layer" else "hbm",
+                    launch, 1, what)
+
     def producer_case(name, kind, r, c, fused=True):
         """RMSNorm / SwiGLU with the output quantized to FP8 1x128 groups:
         fused (one launch, x read once, codes written) or unfused (the
@@ -289,6 +354,10 @@ def build_cases(names, dev):
         "swiglu_quant_fp8": lambda: producer_case("swiglu_quant_fp8", "swiglu", 4096, 14336),
         "swiglu_then_quant_fp8": lambda: producer_case("swiglu_then_quant_fp8", "swiglu", 4096, 14336,
                                                        fused=False),
+        "moe_route": lambda: moe_case("moe_route", "route"),
+        "moe_permute_quant": lambda: moe_case("moe_permute_quant", "permute"),
+        "moe_combine": lambda: moe_case("moe_combine", "combine"),
+        "moe_layer_cfg5": lambda: moe_case("moe_layer_cfg5", "layer"),
         "quant_fp8_block128_w": lambda: quant_case("quant_fp8_block128_w", "fp8_block128", 7168, 4096),
         "quant_fp8_row128_a": lambda: quant_case("quant_fp8_row128_a", "fp8_row128", 4096, 4096),
         "quant_fp8_tensor_w": lambda: quant_case("quant_fp8_tensor_w", "fp8_tensor", 4096, 4096),
@@ -305,6 +374,7 @@ ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor
              "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe",
              "bf16_8192", "bf16_m4096", "bf16_m16",
              "rmsnorm_quant_fp8", "rmsnorm_then_quant_fp8", "swiglu_quant_fp8", "swiglu_then_quant_fp8",
+             "moe_route", "moe_permute_quant", "moe_combine", "moe_layer_cfg5",
              "quant_fp8_block128_w", "quant_fp8_row128_a", "quant_fp8_tensor_w", "quant_mxfp4_w",
              "quant_nvfp4_w"]
 

@@ -79,7 +79,7 @@ extern "C" {
 
 const char *dsl_last_error(void) { return g_err.c_str(); }
 
-int dsl_abi_version(void) { return 3; }
+int dsl_abi_version(void) { return 4; }
 
 size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
   (void)rows;
@@ -347,6 +347,78 @@ int dsl_swiglu_quant(const void *x, int64_t rows, int64_t hidden, int64_t ldx, i
                      void *scales, void *y, int64_t ldy, void *stream) {
   return run_fused("dsl_swiglu_quant", dsl::PROD_SWIGLU, x, rows, hidden, ldx, nullptr,
                    DSL_W_BF16, 0.f, qfmt, q, scales, y, ldy, stream);
+}
+
+size_t dsl_moe_route_workspace_bytes(int64_t tokens, int64_t topk, int64_t num_experts) {
+  if (tokens <= 0 || topk <= 0 || num_experts <= 0) return 0;
+  return dsl::moe_route_workspace_bytes(tokens * topk, num_experts);
+}
+
+int dsl_moe_route(const int32_t *topk_ids, int64_t tokens, int64_t topk, int64_t num_experts,
+                  int32_t *offsets, int32_t *dest, int32_t *src_token, void *ws, size_t ws_bytes,
+                  void *stream) {
+  const char *fn = "dsl_moe_route";
+  if (tokens < 0 || topk <= 0 || num_experts <= 0 || num_experts > dsl::kMaxGroups)
+    return fail(DSL_ERR_ARG, "%s: need tokens >= 0, topk > 0, 1 <= num_experts <= %d", fn,
+                dsl::kMaxGroups);
+  if (tokens * topk >= ((int64_t)1 << 31)) return fail(DSL_ERR_ARG, "%s: too many assignments", fn);
+  if (!offsets) return fail(DSL_ERR_ARG, "%s: offsets is NULL", fn);
+  const int64_t n = tokens * topk;
+  if (n > 0 && (!topk_ids || !dest || !src_token))
+    return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
+  const size_t need = dsl::moe_route_workspace_bytes(n, num_experts);
+  if (!ws || ws_bytes < need)
+    return fail(DSL_ERR_WORKSPACE, "%s: workspace of %zu bytes required", fn, need);
+  return hip_status(dsl::launch_moe_route(topk_ids, (int)n, (int)topk, (int)num_experts, offsets,
+                                          dest, src_token, static_cast<int32_t *>(ws),
+                                          static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+int dsl_moe_permute_quant(const void *x, int64_t tokens, int64_t k, int64_t ldx,
+                          const int32_t *src_token, const int32_t *offsets, int64_t num_experts,
+                          int64_t rows, uint8_t *qx, float *sx, void *stream) {
+  const char *fn = "dsl_moe_permute_quant";
+  if (tokens < 0 || rows < 0 || k <= 0 || num_experts <= 0)
+    return fail(DSL_ERR_ARG, "%s: bad sizes", fn);
+  if (k % 8 != 0 || k > 32768)
+    return fail(DSL_ERR_ARG, "%s: k=%lld must be a multiple of 8 and <= 32768", fn, (long long)k);
+  if (ldx < k || ldx % 8 != 0) return fail(DSL_ERR_ARG, "%s: ldx must be >= k, a multiple of 8", fn);
+  if (rows >= ((int64_t)1 << 31)) return fail(DSL_ERR_ARG, "%s: too many rows", fn);
+  if (rows == 0) return ok();
+  if (tokens == 0) return fail(DSL_ERR_ARG, "%s: rows without tokens", fn);
+  int rc;
+  if ((rc = check_out(fn, x, "x")) || (rc = check_out(fn, qx, "qx"))) return rc;
+  if (!src_token || !offsets || !sx) return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
+  return hip_status(dsl::launch_moe_permute_quant(static_cast<const uint16_t *>(x), ldx, (int)k,
+                                                  (int)tokens, src_token, offsets + num_experts,
+                                                  (int)rows, qx, sx, static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
+int dsl_moe_combine(const void *y, int64_t rows, int64_t n, int64_t ldy, const int32_t *dest,
+                    const float *topk_weights, int64_t tokens, int64_t topk, void *out,
+                    int64_t ldo, int out_dtype, void *stream) {
+  const char *fn = "dsl_moe_combine";
+  if (rows < 0 || tokens < 0 || topk <= 0 || n <= 0) return fail(DSL_ERR_ARG, "%s: bad sizes", fn);
+  if (n % 8 != 0 || n > 32768)
+    return fail(DSL_ERR_ARG, "%s: n=%lld must be a multiple of 8 and <= 32768", fn, (long long)n);
+  if (ldy < n || ldy % 8 != 0 || ldo < n || ldo % 8 != 0)
+    return fail(DSL_ERR_ARG, "%s: ldy / ldo must be >= n and multiples of 8", fn);
+  if (out_dtype != DSL_OUT_BF16 && out_dtype != DSL_OUT_F32)
+    return fail(DSL_ERR_ARG, "%s: unknown out_dtype %d", fn, out_dtype);
+  if (rows >= ((int64_t)1 << 31) || tokens * topk >= ((int64_t)1 << 31))
+    return fail(DSL_ERR_ARG, "%s: sizes must be < 2^31", fn);
+  if (tokens == 0) return ok();
+  int rc;
+  if ((rc = check_out(fn, out, "out"))) return rc;
+  if (rows > 0 && (rc = check_out(fn, y, "y"))) return rc;
+  if (!dest || !topk_weights) return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
+  return hip_status(dsl::launch_moe_combine(static_cast<const uint16_t *>(y), (int)rows, ldy, (int)n,
+                                            dest, topk_weights, (int)tokens, (int)topk, out, ldo,
+                                            out_dtype == DSL_OUT_F32,
+                                            static_cast<hipStream_t>(stream)),
+                    fn);
 }
 
 }  // extern "C"

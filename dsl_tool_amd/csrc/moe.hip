@@ -1,0 +1,277 @@
+// MoE glue on either side of the grouped FP8 GEMM:
+//   route         top-k expert ids -> group offsets, each assignment's row in
+//                 the expert-sorted order, and each sorted row's token;
+//   permute_quant gather token rows into that order, quantized per row to
+//                 E4M3 with scale amax/448 (the grouped GEMM's X and sx);
+//   combine       out[t] = sum_j w[t, j] * Y[dest[t, j]] in slot order.
+// The sorted order is stable: rows of one expert follow the flattened
+// assignment order a = t * topk + j.  Ids outside [0, E) are dropped
+// (dest = -1, no row).  Every step is deterministic (no float atomics, no
+// order that depends on scheduling).
+#include <type_traits>
+
+#include "launch.h"
+#include "quant_core.h"
+
+namespace dsl {
+
+constexpr int kRouteChunk = 1024;     // assignments per block in the count/scatter passes
+
+// Pass 1: per-block expert histograms, counts[b][e].
+__global__ __launch_bounds__(256) void moe_count_kernel(const int32_t *__restrict__ ids, int n,
+                                                        int E, int32_t *__restrict__ counts) {
+  extern __shared__ int hist[];
+  for (int e = threadIdx.x; e < E; e += 256) hist[e] = 0;
+  __syncthreads();
+  const int a0 = blockIdx.x * kRouteChunk;
+  for (int i = threadIdx.x; i < kRouteChunk && a0 + i < n; i += 256) {
+    const int e = ids[a0 + i];
+    if (e >= 0 && e < E) atomicAdd(&hist[e], 1);
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 256) counts[(int64_t)blockIdx.x * E + e] = hist[e];
+}
+
+// Pass 2 (one block): offsets[e] = rows of experts < e; counts[b][e] is
+// replaced by the first sorted row of block b's expert-e assignments.  The
+// count matrix is staged in LDS when it fits (all loads in flight at once);
+// otherwise it is walked in global memory.
+constexpr int kScanLds = 12288;        // ints of the count matrix held in LDS
+
+__global__ __launch_bounds__(1024) void moe_scan_kernel(int32_t *__restrict__ counts, int nb, int E,
+                                                       int32_t *__restrict__ offsets) {
+  __shared__ int tot[kMaxGroups];
+  __shared__ int part[1024];
+  __shared__ int cm[kScanLds];
+  const int total_c = nb * E;
+  const bool in_lds = total_c <= kScanLds;
+  if (in_lds) {
+    for (int i = threadIdx.x; i < total_c; i += 1024) cm[i] = counts[i];
+    __syncthreads();
+  }
+  auto cnt = [&](int b, int e) { return in_lds ? cm[b * E + e] : counts[(int64_t)b * E + e]; };
+  for (int e = threadIdx.x; e < E; e += 1024) {
+    int s = 0;
+    for (int b = 0; b < nb; ++b) s += cnt(b, e);
+    tot[e] = s;
+  }
+  __syncthreads();
+  // exclusive scan of tot over experts: each thread sums a contiguous run
+  const int per = (E + 1023) / 1024;
+  const int e0 = threadIdx.x * per, e1 = min(E, e0 + per);
+  int local = 0;
+  for (int e = e0; e < e1; ++e) local += tot[e];
+  part[threadIdx.x] = local;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int v = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
+    __syncthreads();
+    part[threadIdx.x] += v;
+    __syncthreads();
+  }
+  int run = part[threadIdx.x] - local;     // rows before expert e0
+  for (int e = e0; e < e1; ++e) {
+    offsets[e] = run;
+    int r = run;
+    for (int b = 0; b < nb; ++b) {
+      const int c = cnt(b, e);
+      counts[(int64_t)b * E + e] = r;
+      r += c;
+    }
+    run += tot[e];
+  }
+  if (threadIdx.x == 1023) offsets[E] = part[1023];
+}
+
+// Pass 3: stable scatter, one wave per chunk.  The wave walks its chunk 64
+// assignments at a time; the lanes holding the same expert are found with
+// one ballot per expert-id bit, so a lane's rank among the step's earlier
+// same-expert lanes is a popcount, and the step's last such lane advances
+// the expert's next row in LDS (a single wave: LDS operations stay in
+// program order).
+__global__ __launch_bounds__(64) void moe_scatter_kernel(const int32_t *__restrict__ ids, int n,
+                                                         int E, int topk,
+                                                         const int32_t *__restrict__ base,
+                                                         int32_t *__restrict__ dest,
+                                                         int32_t *__restrict__ src_token) {
+  extern __shared__ int run[];          // [E] next sorted row per expert
+  const int lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) run[e] = base[(int64_t)blockIdx.x * E + e];
+  __syncthreads();
+  int bits = 0;
+  while ((1 << bits) < E + 1) ++bits;   // ids -1 map to E: bits cover 0..E
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int a0 = blockIdx.x * kRouteChunk;
+  constexpr int STEPS = kRouteChunk / 64;
+  int idv[STEPS];                       // the chunk's ids, all loads in flight at once
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    const int a = a0 + st * 64 + lane;
+    idv[st] = a < n ? ids[a] : -1;
+  }
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    const int s0 = st * 64;
+    if (a0 + s0 >= n) break;            // uniform
+    const int a = a0 + s0 + lane;
+    const int e = idv[st];
+    const bool valid = e >= 0 && e < E;
+    const int key = valid ? e : E;      // dropped and past-the-end lanes share key E
+    uint64_t same = ~0ull;
+    for (int b = 0; b < bits; ++b) {
+      const uint64_t m = __ballot((key >> b) & 1);
+      same &= ((key >> b) & 1) ? m : ~m;
+    }
+    const int rank = __popcll(same & below);
+    const bool last = (same >> lane) == 1ull;  // no higher lane holds this key
+    int row = -1;
+    if (valid) row = run[e] + rank;
+    __builtin_amdgcn_s_waitcnt(0xc07f);        // lgkmcnt(0): every lane's read of run is back
+    __builtin_amdgcn_wave_barrier();
+    if (valid && last) run[e] = row + 1;
+    if (a < n) {
+      dest[a] = row;
+      if (valid) src_token[row] = a / topk;
+    }
+  }
+}
+
+// Gather + per-row E4M3: one workgroup per sorted row, thread t holding
+// chunks t + 256 j of the source token's row.  Rows at or past
+// offsets[E] (the routed total; the grid covers every assignment) exit.
+template <int CPL>
+__global__ __launch_bounds__(256) void moe_permute_quant_kernel(
+    const uint16_t *__restrict__ x, int64_t ldx, int k_dim, int tokens,
+    const int32_t *__restrict__ src_token, const int32_t *__restrict__ total,
+    uint8_t *__restrict__ qx, float *__restrict__ sx) {
+  __shared__ float sh[4];
+  const int row = blockIdx.x;
+  if (row >= *total) return;                       // whole workgroup
+  int t = src_token[row];
+  t = t < 0 ? 0 : (t >= tokens ? tokens - 1 : t);
+  const int nch = k_dim >> 3;
+  const uint16_t *xr = x + (int64_t)t * ldx;
+  uint4 xa[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    xa[j] = c < nch ? reinterpret_cast<const uint4 *>(xr)[c] : make_uint4(0, 0, 0, 0);
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    float f[8];
+    unpack8(xa[j], f);
+    m = fmaxf(m, amax8(f));
+  }
+  const float s = fp8_scale_of(block_max(m, sh));
+  const float r = rcp_approx(s);
+  if (threadIdx.x == 0) sx[row] = s;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    if (c < nch) {
+      float f[8];
+      unpack8(xa[j], f);
+      *reinterpret_cast<uint2 *>(qx + (int64_t)row * k_dim + (int64_t)c * 8) = e4m3_quot8(f, s, r);
+    }
+  }
+}
+
+// out[t] = sum_j w[t, j] * y[dest[t, j]] (dropped slots skipped), fp32 in
+// slot order with separate multiply and add, then bf16 or fp32.
+template <int CPL>
+__global__ __launch_bounds__(256) void moe_combine_kernel(
+    const uint16_t *__restrict__ y, int rows_y, int64_t ldy, int n, const int32_t *__restrict__ dest,
+    const float *__restrict__ w, int topk, void *__restrict__ out, int64_t ldo, int out_f32) {
+#pragma clang fp contract(off)   // one rounding per multiply and per add, as specified
+  const int t = blockIdx.x;
+  const int nch = n >> 3;
+  float acc[CPL][8];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+  for (int s = 0; s < topk; ++s) {
+    const int row = dest[(int64_t)t * topk + s];
+    if (row < 0 || row >= rows_y) continue;             // uniform across the block
+    const float ws = w[(int64_t)t * topk + s];
+    const uint16_t *yr = y + (int64_t)row * ldy;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      if (c < nch) {
+        float f[8];
+        unpack8(reinterpret_cast<const uint4 *>(yr)[c], f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j][e] = acc[j][e] + ws * f[e];
+      }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    if (c >= nch) continue;
+    if (out_f32) {
+      float *o = static_cast<float *>(out) + (int64_t)t * ldo + (int64_t)c * 8;
+      reinterpret_cast<float4 *>(o)[0] = make_float4(acc[j][0], acc[j][1], acc[j][2], acc[j][3]);
+      reinterpret_cast<float4 *>(o)[1] = make_float4(acc[j][4], acc[j][5], acc[j][6], acc[j][7]);
+    } else {
+      uint4 o;
+      o.x = pack_bf16x2(acc[j][0], acc[j][1]);
+      o.y = pack_bf16x2(acc[j][2], acc[j][3]);
+      o.z = pack_bf16x2(acc[j][4], acc[j][5]);
+      o.w = pack_bf16x2(acc[j][6], acc[j][7]);
+      reinterpret_cast<uint4 *>(static_cast<uint16_t *>(out) + (int64_t)t * ldo)[c] = o;
+    }
+  }
+}
+
+size_t moe_route_workspace_bytes(int64_t assignments, int64_t num_experts) {
+  const int64_t nb = (assignments + kRouteChunk - 1) / kRouteChunk;
+  return (size_t)(nb < 1 ? 1 : nb) * (size_t)num_experts * sizeof(int32_t);
+}
+
+hipError_t launch_moe_route(const int32_t *ids, int n, int topk, int E, int32_t *offsets,
+                            int32_t *dest, int32_t *src_token, int32_t *ws, hipStream_t st) {
+  const int nb = n > 0 ? (n + kRouteChunk - 1) / kRouteChunk : 0;
+  const size_t lds = (size_t)E * sizeof(int);
+  if (nb > 0) moe_count_kernel<<<nb, 256, lds, st>>>(ids, n, E, ws);
+  moe_scan_kernel<<<1, 1024, 0, st>>>(ws, nb, E, offsets);
+  if (nb > 0) moe_scatter_kernel<<<nb, 64, lds, st>>>(ids, n, E, topk, ws, dest, src_token);
+  return hipGetLastError();
+}
+
+template <class F>
+static void by_cpl(int cols, F &&f) {
+  const int per = (cols / 8 + 255) / 256;
+  if (per <= 1) f(std::integral_constant<int, 1>{});
+  else if (per <= 2) f(std::integral_constant<int, 2>{});
+  else if (per <= 4) f(std::integral_constant<int, 4>{});
+  else if (per <= 8) f(std::integral_constant<int, 8>{});
+  else f(std::integral_constant<int, 16>{});
+}
+
+hipError_t launch_moe_permute_quant(const uint16_t *x, int64_t ldx, int k_dim, int tokens,
+                                    const int32_t *src_token, const int32_t *total, int rows,
+                                    uint8_t *qx, float *sx, hipStream_t st) {
+  if (rows == 0) return hipSuccess;
+  by_cpl(k_dim, [&](auto cpl) {
+    moe_permute_quant_kernel<decltype(cpl)::value><<<rows, 256, 0, st>>>(x, ldx, k_dim, tokens,
+                                                                         src_token, total, qx, sx);
+  });
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_combine(const uint16_t *y, int rows_y, int64_t ldy, int n, const int32_t *dest,
+                              const float *w, int tokens, int topk, void *out, int64_t ldo,
+                              int out_f32, hipStream_t st) {
+  if (tokens == 0) return hipSuccess;
+  by_cpl(n, [&](auto cpl) {
+    moe_combine_kernel<decltype(cpl)::value><<<tokens, 256, 0, st>>>(y, rows_y, ldy, n, dest, w, topk,
+                                                                     out, ldo, out_f32);
+  });
+  return hipGetLastError();
+}
+
+}  // namespace dsl

@@ -103,10 +103,9 @@ class KernelRegistry:
             self.register(name, "hip", getattr(gemm, attr), desc,
                           input_schema=gemm_input_schema(name),
                           output_schema=gemm_output_schema(name))
-        fused = importlib.import_module("dsl_tool_amd.fused")
-        for name, attr, desc, ins, outs in HIP_PRODUCER_ENTRIES:
-            self.register(name, "hip", getattr(fused, attr), desc, input_schema=dict(ins),
-                          output_schema=dict(outs))
+        for name, mod, attr, desc, ins, outs in HIP_EXTRA_ENTRIES:
+            fn = getattr(importlib.import_module(mod), attr)
+            self.register(name, "hip", fn, desc, input_schema=dict(ins), output_schema=dict(outs))
 
 
 HIP_GEMM_ENTRIES = (
@@ -126,16 +125,24 @@ HIP_GEMM_ENTRIES = (
 # activations.swiglu, dispatcher/registry.py:146,158).
 _PRODUCER_OUT = {"q": "uint8 Tensor: E4M3 [rows, cols] (fmt 'fp8') | packed E2M1 [rows, cols/2] ('mxfp4')",
                  "scales": "fp32 [rows, ceil(cols/128)] ('fp8') | E8M0 uint8 [rows, cols/32] ('mxfp4')"}
-HIP_PRODUCER_ENTRIES = (
-    ("normalization.rmsnorm_quant", "rmsnorm_quant",
+HIP_EXTRA_ENTRIES = (
+    ("normalization.rmsnorm_quant", "dsl_tool_amd.fused", "rmsnorm_quant",
      "RMSNorm y = w·x/√(mean(x²)+ε) quantized in registers to FP8 1x128 groups or MXFP4",
      {"x": "Tensor[batch, hidden] bf16", "weight": "Tensor[hidden] bf16/fp32",
       "eps": "float (default 1e-6)", "fmt": "str 'fp8' (default) | 'mxfp4'",
       "return_y": "bool: also return the bf16 RMSNorm output"}, _PRODUCER_OUT),
-    ("activations.swiglu_quant", "swiglu_quant",
+    ("activations.swiglu_quant", "dsl_tool_amd.fused", "swiglu_quant",
      "SwiGLU SiLU(gate)×up of input=[B,2H] quantized in registers to FP8 1x128 groups or MXFP4",
      {"input": "Tensor[batch, 2*hidden] bf16", "fmt": "str 'fp8' (default) | 'mxfp4'",
       "return_y": "bool: also return the bf16 SwiGLU output"}, _PRODUCER_OUT),
+    # The step either side of gemm.grouped_gemm in an MoE layer: routing
+    # tables, expert-ordered FP8 tokens, grouped GEMM, weighted combine.
+    ("moe.routed_grouped_gemm", "dsl_tool_amd.moe", "routed_grouped_gemm",
+     "MoE projection: route top-k ids, permute + FP8-quantize tokens, grouped FP8 GEMM, weighted combine",
+     {"x": "Tensor[tokens, K] bf16", "topk_ids": "Tensor[tokens, topk] int32",
+      "topk_weights": "Tensor[tokens, topk] fp32", "w": "Tensor[E, K, N] bf16",
+      "out_dtype": "torch.bfloat16 (default) | torch.float32"},
+     {"out": "Tensor[tokens, N]"}),
 )
 
 

@@ -1,0 +1,121 @@
+"""MoE glue on the GPU around the grouped FP8 GEMM.
+
+An MoE FFN projection, on the device end to end:
+
+    route = moe_route(topk_ids, E)                  # offsets, dest, src_token
+    qx, sx = moe_permute_quant(x, route)            # tokens in expert order, E4M3 per row
+    y = gemm.grouped_fp8_gemm_packed(qx, sx, qw, sw, route.offsets)
+    out = moe_combine(y, route, topk_weights)       # weighted sum over each token's experts
+
+``routed_grouped_gemm`` runs the four steps (registered as
+``moe.routed_grouped_gemm``).  The reference has no MoE glue; its grouped
+GEMM takes rows already sorted by group (cuda/gemm/grouped_gemm.cu:26-32,
+:77-104, triton/gemm/gemm_kernels.py:164-182).  Everything runs in
+``libdsl_gemm.so``; the sorted order is a stable counting sort, so results
+do not depend on scheduling.
+"""
+from __future__ import annotations
+
+from typing import NamedTuple
+
+import torch
+
+from . import _native as N
+from . import gemm as G
+from . import quant as Q
+
+
+class Route(NamedTuple):
+    offsets: torch.Tensor     # int32 [E + 1]
+    dest: torch.Tensor        # int32 [T * topk]: sorted row of assignment t*topk+j, -1 if dropped
+    src_token: torch.Tensor   # int32 [T * topk]: token of sorted row r (r < offsets[E])
+    tokens: int
+    topk: int
+    num_experts: int
+
+
+def _gpu(t: torch.Tensor, name: str):
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        raise ValueError(f"{name} must be a tensor on a GPU device")
+
+
+def moe_route(topk_ids: torch.Tensor, num_experts: int) -> Route:
+    """Group offsets and row maps from ``topk_ids [T, topk]`` (expert ids)."""
+    _gpu(topk_ids, "topk_ids")
+    if topk_ids.dim() != 2:
+        raise ValueError("topk_ids must be [tokens, topk]")
+    ids = topk_ids.to(torch.int32).contiguous()
+    T, k = ids.shape
+    dev = ids.device
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    dest = torch.empty(T * k, dtype=torch.int32, device=dev)
+    src = torch.empty(T * k, dtype=torch.int32, device=dev)
+    nb = N.lib().dsl_moe_route_workspace_bytes(T, k, num_experts)
+    ws = torch.empty(max(nb, 4) // 4, dtype=torch.int32, device=dev)
+    with torch.cuda.device(dev):
+        N.call("dsl_moe_route", N.ptr(ids), T, k, num_experts, N.ptr(offsets), N.ptr(dest),
+               N.ptr(src), N.ptr(ws), ws.numel() * 4, N.stream_of(dev))
+    return Route(offsets, dest, src, T, k, num_experts)
+
+
+def moe_permute_quant(x: torch.Tensor, route: Route):
+    """Token rows of ``x [T, K]`` (bf16) in expert order, E4M3 with one scale
+    per row: ``(qx [T*topk, K] uint8, sx [T*topk] float32)``; rows past the
+    routed total are unused."""
+    _gpu(x, "x")
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] != route.tokens:
+        raise ValueError("x must be bf16 [tokens, K]")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    T, K = x.shape
+    rows = T * route.topk
+    qx = torch.empty((rows, K), dtype=torch.uint8, device=x.device)
+    sx = torch.empty(rows, dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        N.call("dsl_moe_permute_quant", N.ptr(x), T, K, x.stride(0), N.ptr(route.src_token),
+               N.ptr(route.offsets), route.num_experts, rows, N.ptr(qx), N.ptr(sx),
+               N.stream_of(x.device))
+    return qx, sx
+
+
+def moe_combine(y: torch.Tensor, route: Route, topk_weights: torch.Tensor, *,
+                out_dtype=torch.bfloat16) -> torch.Tensor:
+    """``out[t] = sum_j topk_weights[t, j] * y[dest[t*topk + j]]`` (fp32 sum)."""
+    _gpu(y, "y")
+    _gpu(topk_weights, "topk_weights")
+    if y.dtype != torch.bfloat16 or y.dim() != 2 or y.stride(1) != 1:
+        raise ValueError("y must be bf16 [rows, N] with unit column stride")
+    w = topk_weights.to(torch.float32).contiguous()
+    if tuple(w.shape) != (route.tokens, route.topk):
+        raise ValueError(f"topk_weights must be [{route.tokens}, {route.topk}]")
+    rows, n = y.shape
+    out = torch.empty((route.tokens, n), dtype=out_dtype, device=y.device)
+    with torch.cuda.device(y.device):
+        N.call("dsl_moe_combine", N.ptr(y), rows, n, y.stride(0), N.ptr(route.dest), N.ptr(w),
+               route.tokens, route.topk, N.ptr(out), n, G._out_code(out_dtype),
+               N.stream_of(y.device))
+    return out
+
+
+def routed_grouped_gemm(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: torch.Tensor,
+                        w: torch.Tensor, *, out_dtype=torch.bfloat16) -> torch.Tensor:
+    """MoE projection ``out[t] = sum_j w_tj * (x[t] @ W[e_tj])`` for
+    ``x [T, K]`` bf16, ``topk_ids / topk_weights [T, topk]`` and expert
+    weights ``w [E, K, N]`` (the reference's grouped B layout; bf16, quantized
+    here per output channel) or pre-quantized ``(qw [E, N, K] uint8, sw [E, N])``.
+    """
+    if isinstance(w, (tuple, list)):
+        qw, sw = w
+        E = qw.shape[0]
+    else:
+        _gpu(w, "w")
+        if w.dim() != 3:
+            raise ValueError("w must be [E, K, N]")
+        E, K, Nn = w.shape
+        wt = w.transpose(1, 2).reshape(E * Nn, K)       # [E*N, K] K-major rows
+        qw, sw = Q.quant_fp8_blocks(wt, 1, K)
+        qw, sw = qw.reshape(E, Nn, K), sw.reshape(E, Nn)
+    route = moe_route(topk_ids, E)
+    qx, sx = moe_permute_quant(x, route)
+    y = G.grouped_fp8_gemm_packed(qx, sx, qw, sw, route.offsets, out_dtype=torch.bfloat16)
+    return moe_combine(y, route, topk_weights, out_dtype=out_dtype)

@@ -47,6 +47,23 @@ def weights(cfg: int, n: int, k: int) -> torch.Tensor:
     return randn_bf16((n, k), 1000 * cfg + 2, W_STD)
 
 
+def moe_routing(num_experts: int = 64, tokens: int = 4096, top_k: int = 8, zipf_s: float = 1.2,
+                n_empty: int = 4, seed: int = 5004):
+    """Seeded top-k routing (Gumbel-top-k over a Zipf pmf with n_empty experts
+    never chosen): ``(topk_ids int32 [T, k], topk_weights float32 [T, k])``,
+    the weights a softmax over each token's chosen scores."""
+    g = _gen(seed)
+    pmf = torch.arange(1, num_experts + 1, dtype=torch.float64) ** (-zipf_s)
+    empty = torch.randperm(num_experts, generator=g)[:n_empty]
+    pmf[empty] = 0.0
+    pmf = pmf / pmf.sum()
+    u = torch.rand((tokens, num_experts), generator=g, dtype=torch.float64).clamp_min(1e-300)
+    scores = pmf.log() - (-u.log()).log()
+    top = scores.topk(top_k, dim=1)
+    w = torch.softmax(top.values, dim=1).to(torch.float32)
+    return top.indices.to(torch.int32), w
+
+
 def moe_counts(num_experts: int = 64, tokens: int = 4096, top_k: int = 8, zipf_s: float = 1.2,
                n_empty: int = 4, seed: int = 5004) -> torch.Tensor:
     g = _gen(seed)

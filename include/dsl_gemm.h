@@ -183,6 +183,44 @@ int dsl_rmsnorm_quant(const void *x, int64_t rows, int64_t cols, int64_t ldx,
 int dsl_swiglu_quant(const void *x, int64_t rows, int64_t hidden, int64_t ldx,
                      int qfmt, void *q, void *scales, void *y, int64_t ldy, void *stream);
 
+/* ------------------------------------------------------------ MoE glue --
+ * The steps either side of dsl_grouped_fp8_gemm in an MoE layer.  The
+ * reference has no counterpart (its grouped GEMM takes rows already sorted
+ * by group with a host-built descriptor table, cuda/gemm/grouped_gemm.cu:
+ * 26-32, :150-156); these build that input on the device and reduce its
+ * output.  Assignment a = t * topk + j is token t's j-th routed expert.
+ */
+
+/* Workspace bytes dsl_moe_route needs. */
+size_t dsl_moe_route_workspace_bytes(int64_t tokens, int64_t topk, int64_t num_experts);
+
+/* topk_ids [tokens][topk] int32 -> offsets [num_experts+1] (the grouped
+ * GEMM's group_offsets), dest [tokens*topk] (sorted row of each assignment,
+ * -1 for ids outside [0, num_experts), which are dropped) and src_token
+ * [tokens*topk] (token of sorted row r, for r < offsets[num_experts]).
+ * Rows of one expert keep the assignment order (a stable counting sort). */
+int dsl_moe_route(const int32_t *topk_ids, int64_t tokens, int64_t topk, int64_t num_experts,
+                  int32_t *offsets, int32_t *dest, int32_t *src_token,
+                  void *workspace, size_t workspace_bytes, void *stream);
+
+/* Sorted row r < offsets[num_experts] of qx [rows][k] E4M3 and sx [rows]
+ * float: token src_token[r] of x [tokens][ldx] bf16 quantized per row,
+ * scale max(amax/448, 1e-12) (as dsl_quant_fp8_blocks with a 1 x k group).
+ * rows = tokens * topk (rows past the routed total are left untouched).
+ * k % 8 == 0, k <= 32768. */
+int dsl_moe_permute_quant(const void *x, int64_t tokens, int64_t k, int64_t ldx,
+                          const int32_t *src_token, const int32_t *offsets,
+                          int64_t num_experts, int64_t rows, uint8_t *qx, float *sx,
+                          void *stream);
+
+/* out [tokens][ldo] = sum over j of topk_weights[t][j] * y[dest[t*topk+j]]
+ * (y [rows][ldy] bf16, the grouped GEMM's output), in fp32 with slot order j
+ * and a separate multiply and add per term, then bf16 or fp32.  Slots with
+ * dest < 0 or >= rows are skipped.  n % 8 == 0, n <= 32768. */
+int dsl_moe_combine(const void *y, int64_t rows, int64_t n, int64_t ldy, const int32_t *dest,
+                    const float *topk_weights, int64_t tokens, int64_t topk,
+                    void *out, int64_t ldo, int out_dtype, void *stream);
+
 /* Workspace bytes dsl_fp8_gemm / dsl_fp4_gemm / dsl_bf16_gemm need for this
  * shape (op = DSL_OP_FP8, DSL_OP_FP4 or DSL_OP_BF16; for FP8 / FP4 the larger of the plans of the op's two
  * scale modes / FP4 formats; 0 when none is needed).  The kernel choice

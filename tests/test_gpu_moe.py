@@ -1,0 +1,96 @@
+"""MoE glue on the GPU: routing tables, permute + quantize and combine bit
+for bit against the oracle; the routed grouped GEMM end to end within the
+GEMM tolerance."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm as OG
+from oracle import moe as OM
+from dsl_tool_amd import moe as M
+from dsl_tool_amd import workloads as W
+from tests.util import assert_close, np_f32, np_u8
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _ids(T, k, E, seed, drop=False):
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, E, (T, k), generator=g, dtype=torch.int32)
+    if drop:
+        m = torch.rand((T, k), generator=g) < 0.05
+        ids[m] = -1
+        ids[0, 0] = E          # out of range: dropped too
+    return ids
+
+
+ROUTE_CASES = [(4096, 8, 64, False), (37, 3, 5, True), (1, 1, 1, False), (3000, 6, 2048, True),
+               (513, 4, 7, False)]
+
+
+@pytest.mark.parametrize("T,k,E,drop", ROUTE_CASES)
+def test_route_matches_oracle(T, k, E, drop):
+    ids = _ids(T, k, E, 400 + T, drop)
+    r = M.moe_route(ids.to(DEV), E)
+    off, dest, src = OM.route(ids.numpy(), E)
+    assert np.array_equal(r.offsets.cpu().numpy(), off)
+    assert np.array_equal(r.dest.cpu().numpy(), dest)
+    n = int(off[-1])
+    assert np.array_equal(r.src_token.cpu().numpy()[:n], src)
+
+
+def test_route_config5_routing():
+    ids, _ = W.moe_routing()
+    r = M.moe_route(ids.to(DEV), 64)
+    counts = W.moe_counts()
+    assert np.array_equal(np.diff(r.offsets.cpu().numpy()), counts.numpy())
+    assert (np.diff(r.offsets.cpu().numpy()) == 0).sum() >= 4        # forced-empty experts
+
+
+@pytest.mark.parametrize("T,k,E,K", [(300, 4, 9, 2048), (64, 2, 3, 136), (5, 3, 4, 7168)])
+def test_permute_quant_matches_oracle(T, k, E, K):
+    ids = _ids(T, k, E, 410 + T, drop=True)
+    x = W.randn_bf16((T, K), 411) * 3
+    r = M.moe_route(ids.to(DEV), E)
+    qx, sx = M.moe_permute_quant(x.to(DEV), r)
+    off, dest, src = OM.route(ids.numpy(), E)
+    q_ref, s_ref = OM.permute_quant(x.float().numpy(), src)
+    n = int(off[-1])
+    assert np.array_equal(np_u8(qx)[:n], q_ref)
+    assert np.array_equal(np_f32(sx)[:n], s_ref)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_combine_matches_oracle(out_dtype):
+    T, k, E, Nn = 257, 8, 16, 1536
+    ids = _ids(T, k, E, 420, drop=True)
+    wts = torch.softmax(torch.randn((T, k), generator=torch.Generator().manual_seed(421)), 1)
+    r = M.moe_route(ids.to(DEV), E)
+    y = W.randn_bf16((T * k, Nn), 422)
+    out = M.moe_combine(y.to(DEV), r, wts.to(DEV), out_dtype=out_dtype)
+    ref = OM.combine(y.float().numpy(), r.dest.cpu().numpy(), wts.numpy(), T, k,
+                     out_bf16=out_dtype == torch.bfloat16)
+    assert np.array_equal(np_f32(out), ref)
+
+
+def test_routed_grouped_gemm_end_to_end():
+    T, k, E, K, Nn = 512, 4, 16, 1024, 768
+    ids = _ids(T, k, E, 430)
+    wts = torch.softmax(torch.randn((T, k), generator=torch.Generator().manual_seed(431)), 1)
+    x = W.randn_bf16((T, K), 432)
+    w = W.randn_bf16((E, K, Nn), 433, 0.02)
+    out = M.routed_grouped_gemm(x.to(DEV), ids.to(DEV), wts.to(DEV), w.to(DEV),
+                                out_dtype=torch.float32)
+    # oracle chain: route -> permute_quant -> grouped reference -> combine
+    off, dest, src = OM.route(ids.numpy(), E)
+    qx, sx = OM.permute_quant(x.float().numpy(), src)
+    from oracle import quant as OQ
+    wt = w.float().numpy().transpose(0, 2, 1).reshape(E * Nn, K)
+    qw, sw = OQ.quant_fp8_blockwise(wt, 1, K)
+    y = OG.ref_grouped_fp8(qx, sx, qw.reshape(E, Nn, K), sw.reshape(E, Nn), off)
+    ref = OM.combine(y, dest, wts.numpy(), T, k, out_bf16=False)
+    # The combine adds topk bf16-rounded GEMM rows; one bf16 ulp of a large
+    # term (a rounding flip from the GEMM's own fp32 order) lands whole on a
+    # sum that cancels, so only the global north-star bound is meaningful.
+    assert_close(out, ref, what="routed grouped gemm", elem_tol=float("inf"))

@@ -94,6 +94,21 @@ def test_fused_producer_argument_validation(lib):
     assert lib.dsl_swiglu_quant(None, 0, 64, 128, 0, None, None, None, 0, None) == 0
 
 
+def test_moe_glue_argument_validation(lib):
+    fake = 1 << 20
+    rc = lib.dsl_moe_route(fake, 16, 2, 4096, fake, fake, fake, fake, 1 << 20, None)
+    assert rc == N.DSL_ERR_ARG and "num_experts" in _err(lib)
+    need = lib.dsl_moe_route_workspace_bytes(4096, 8, 64)
+    assert need >= 32 * 64 * 4
+    rc = lib.dsl_moe_route(fake, 4096, 8, 64, fake, fake, fake, fake, need - 4, None)
+    assert rc == N.DSL_ERR_WORKSPACE
+    rc = lib.dsl_moe_permute_quant(fake, 16, 100, 104, fake, fake, 4, 32, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "multiple of 8" in _err(lib)
+    rc = lib.dsl_moe_combine(fake, 32, 64, 32, fake, fake, 16, 2, fake, 64, 0, None)
+    assert rc == N.DSL_ERR_ARG and "ldy" in _err(lib)
+    assert lib.dsl_moe_combine(None, 0, 64, 64, None, None, 0, 2, None, 64, 0, None) == 0
+
+
 def test_workspace_query_matches_the_planned_path(lib):
     # skinny M with K a multiple of 1024 takes the single-pass decode kernel
     assert lib.dsl_gemm_workspace_bytes(N.OP_FP8, 16, 8192, 8192) == 0

@@ -302,6 +302,38 @@ def test_swiglu_oracle_against_float64_and_limits():
     assert not np.allclose(OF.swiglu_bf16(np.concatenate([x[:, 128:], x[:, :128]], 1)), y)
 
 
+def test_moe_route_matches_brute_force_stable_sort():
+    from oracle import moe as OM
+    rng = np.random.default_rng(12)
+    T, k, E = 23, 3, 5
+    ids = rng.integers(-1, E + 1, (T, k)).astype(np.int32)      # includes dropped ids -1 and E
+    offsets, dest, src = OM.route(ids, E)
+    rows = []                                                    # brute force: expert by expert
+    for e in range(E):
+        for a in range(T * k):
+            if ids.reshape(-1)[a] == e:
+                rows.append(a)
+    assert list(src) == [a // k for a in rows]
+    for r, a in enumerate(rows):
+        assert dest[a] == r
+    assert (dest[~np.isin(ids.reshape(-1), range(E))] == -1).all()
+    assert list(offsets) == [0] + list(np.cumsum([np.sum(ids == e) for e in range(E)]))
+
+
+def test_moe_combine_closed_forms():
+    from oracle import moe as OM
+    rng = np.random.default_rng(13)
+    y = F.round_to_bf16(rng.standard_normal((12, 16)).astype(np.float32))
+    dest = np.array([3, 7, -1, 0, 11, 5], np.int32)               # 3 tokens x top-2
+    onehot = np.array([[1, 0], [0, 1], [1, 0]], np.float32)
+    out = OM.combine(y, dest, onehot, 3, 2)
+    assert np.array_equal(out, np.stack([y[3], y[0], y[11]]))
+    half = np.full((3, 2), 0.5, np.float32)
+    out2 = OM.combine(y, dest, half, 3, 2)
+    assert np.array_equal(out2[0], F.round_to_bf16(0.5 * y[3] + 0.5 * y[7]))
+    assert np.array_equal(out2[1], F.round_to_bf16(0.5 * y[0]))  # dropped slot skipped
+
+
 def test_grouped_empty_groups_and_permutation():
     rng = np.random.default_rng(7)
     counts = [3, 0, 2, 0]
