@@ -236,6 +236,23 @@ def build_cases(names, dev):
         return Case(name, 0.0, nbytes, PEAK_FP8_TFLOPS, "hbm", launch, 1,
                     f"quantize {kind} [{r}, {k}] bf16 ({passes} read pass{'es' if passes > 1 else ''})")
 
+    def lora_case(name, m, n, k, r, l):
+        x, w = rnd((m, k), 11), rnd((n, k), 12, 0.05)
+        a_t, b_t = rnd((l * r, k), 13, 0.05), rnd((n, l * r), 14, 0.05)
+        s = torch.linspace(0.5, 2.0, l, device=dev)
+        y = torch.empty((m, n), dtype=torch.float32, device=dev)
+        nb = L.dsl_lora_gemm_workspace_bytes(m, n, k, r, l)
+        ws = torch.empty(max(nb, 256) // 4, dtype=torch.float32, device=dev)
+
+        def launch(i, stream):
+            return L.dsl_lora_gemm(x.data_ptr(), w.data_ptr(), a_t.data_ptr(), b_t.data_ptr(),
+                                   s.data_ptr(), y.data_ptr(), m, n, k, r, l, n, ws.data_ptr(), nb,
+                                   stream)
+        flops = 2.0 * m * n * k + 2.0 * m * k * l * r + 2 * 2.0 * m * l * r * n
+        nbytes = 2 * m * k + 2 * n * k + 2 * l * r * (k + n) + 4 * m * n
+        return Case(name, flops, nbytes, PEAK_BF16_TFLOPS, "mfma", launch, 1,
+                    f"LoRA fused GEMM M={m} N={n} K={k}, {l} adapters of rank {r}, fp32 out")
+
     def moe_case(name, stage):
         """BASELINE config 5 routing (4096 tokens, top-8 of 64 experts,
         K=2048, N=1536) through the MoE glue: one stage, or the whole
@@ -354,6 +371,8 @@ def build_cases(names, dev):
         "swiglu_quant_fp8": lambda: producer_case("swiglu_quant_fp8", "swiglu", 4096, 14336),
         "swiglu_then_quant_fp8": lambda: producer_case("swiglu_then_quant_fp8", "swiglu", 4096, 14336,
                                                        fused=False),
+        "lora_m4096": lambda: lora_case("lora_m4096", 4096, 4096, 4096, 16, 4),
+        "bf16_4096": lambda: bf16_case("bf16_4096", 4096, 4096, 4096),
         "moe_route": lambda: moe_case("moe_route", "route"),
         "moe_permute_quant": lambda: moe_case("moe_permute_quant", "permute"),
         "moe_combine": lambda: moe_case("moe_combine", "combine"),
@@ -374,7 +393,7 @@ ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor
              "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe",
              "bf16_8192", "bf16_m4096", "bf16_m16",
              "rmsnorm_quant_fp8", "rmsnorm_then_quant_fp8", "swiglu_quant_fp8", "swiglu_then_quant_fp8",
-             "moe_route", "moe_permute_quant", "moe_combine", "moe_layer_cfg5",
+             "moe_route", "moe_permute_quant", "moe_combine", "moe_layer_cfg5", "lora_m4096", "bf16_4096",
              "quant_fp8_block128_w", "quant_fp8_row128_a", "quant_fp8_tensor_w", "quant_mxfp4_w",
              "quant_nvfp4_w"]
 

@@ -32,7 +32,7 @@ FMT_MXFP4, FMT_NVFP4 = 0, 1
 OP_FP8, OP_FP4, OP_GROUPED_FP8, OP_BF16 = 0, 1, 2, 3
 QFMT_FP8_G128, QFMT_MXFP4 = 0, 1
 W_BF16, W_F32 = 0, 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 
 class DslLibraryError(ImportError):
@@ -69,6 +69,9 @@ SIGNATURES = {
     "dsl_rmsnorm_quant": (_i32, [_vp, _i64, _i64, _i64, _vp, _i32, ctypes.c_float, _i32, _vp, _vp,
                                  _vp, _i64, _vp]),
     "dsl_swiglu_quant": (_i32, [_vp, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _i64, _vp]),
+    "dsl_lora_gemm_workspace_bytes": (_sz, [_i64, _i64, _i64, _i64, _i64]),
+    "dsl_lora_gemm": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp,
+                             _sz, _vp]),
     "dsl_moe_route_workspace_bytes": (_sz, [_i64, _i64, _i64]),
     "dsl_moe_route": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "dsl_moe_permute_quant": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _vp, _vp]),

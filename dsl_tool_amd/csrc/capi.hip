@@ -4,6 +4,7 @@
 // never allocates device memory, never synchronises, never exits; failures
 // return a negative status with a thread-local message.
 #include <cstdarg>
+#include <algorithm>
 #include <cstdio>
 #include <string>
 
@@ -79,7 +80,7 @@ extern "C" {
 
 const char *dsl_last_error(void) { return g_err.c_str(); }
 
-int dsl_abi_version(void) { return 4; }
+int dsl_abi_version(void) { return 5; }
 
 size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
   (void)rows;
@@ -201,6 +202,9 @@ static int run_gemm(const char *fn, int mode, const uint8_t *a, const uint8_t *b
   p.ws = static_cast<float *>(ws);
   p.ksplit = 1;
   p.out_f32 = out_dtype == DSL_OUT_F32;
+  p.accumulate = 0;
+  p.a2 = p.b2 = nullptr;
+  p.Kb2 = 0;
   return hip_status(dsl::launch_gemm(mode, p, static_cast<hipStream_t>(stream)), fn);
 }
 
@@ -347,6 +351,110 @@ int dsl_swiglu_quant(const void *x, int64_t rows, int64_t hidden, int64_t ldx, i
                      void *scales, void *y, int64_t ldy, void *stream) {
   return run_fused("dsl_swiglu_quant", dsl::PROD_SWIGLU, x, rows, hidden, ldx, nullptr,
                    DSL_W_BF16, 0.f, qfmt, q, scales, y, ldy, stream);
+}
+
+}  // extern "C"
+
+namespace {
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct LoraPlan {
+  int64_t ld2;                 // padded columns of hi | lo and of B^T | B^T
+  size_t t32, ws, t2, b2, total;
+};
+
+LoraPlan lora_plan(int64_t m, int64_t n, int64_t k, int64_t lr) {
+  LoraPlan p;
+  p.ld2 = (2 * lr + 63) / 64 * 64;
+  const size_t ws1 = dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, lr, k);
+  const size_t ws3 = dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, n, k);
+  const size_t ws4 = dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, n, p.ld2, true);
+  p.t32 = align256((size_t)(m * lr) * 4);
+  p.ws = align256(std::max(ws1, std::max(ws3, ws4)));
+  p.t2 = align256((size_t)(m * p.ld2) * 2);
+  p.b2 = align256((size_t)(n * p.ld2) * 2);
+  p.total = p.t32 + p.ws + p.t2 + p.b2;
+  return p;
+}
+
+dsl::GemmArgs bf16_args(const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k,
+                        int64_t ldc, bool accumulate, void *ws) {
+  dsl::GemmArgs p;
+  p.a = static_cast<const uint8_t *>(a);
+  p.b = static_cast<const uint8_t *>(b);
+  p.c = c;
+  p.M = (int)m;
+  p.N = (int)n;
+  p.K = (int)k;
+  p.Kb = (int)(2 * k);
+  p.ldc = ldc;
+  p.sa = p.sb = nullptr;
+  p.ga = p.gb = nullptr;
+  p.ws = static_cast<float *>(ws);
+  p.ksplit = 1;
+  p.out_f32 = 1;
+  p.accumulate = accumulate ? 1 : 0;
+  p.a2 = p.b2 = nullptr;
+  p.Kb2 = 0;
+  return p;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t dsl_lora_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int64_t rank,
+                                     int64_t num_loras) {
+  if (m <= 0 || n <= 0 || k <= 0 || rank <= 0 || num_loras <= 0) return 0;
+  return lora_plan(m, n, k, rank * num_loras).total;
+}
+
+int dsl_lora_gemm(const void *x, const void *w, const void *a_t, const void *b_t,
+                  const float *scales, float *y, int64_t m, int64_t n, int64_t k, int64_t rank,
+                  int64_t num_loras, int64_t ldy, void *ws, size_t ws_bytes, void *stream) {
+  const char *fn = "dsl_lora_gemm";
+  if (rank <= 0 || num_loras <= 0) return fail(DSL_ERR_ARG, "%s: rank and num_loras must be > 0", fn);
+  const int64_t lr = rank * num_loras;
+  int rc = check_gemm_dims(fn, m, n, k, ldy, 8, DSL_OUT_F32);
+  if (rc) return rc;
+  if (lr % 8 != 0 || lr >= ((int64_t)1 << 20))
+    return fail(DSL_ERR_ARG, "%s: rank * num_loras = %lld must be a multiple of 8", fn, (long long)lr);
+  if (m == 0 || n == 0) return ok();
+  if ((rc = check_out(fn, x, "x")) || (rc = check_out(fn, w, "w")) || (rc = check_out(fn, a_t, "a_t")) ||
+      (rc = check_out(fn, b_t, "b_t")))
+    return rc;
+  if (!scales || !y) return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
+  if (!aligned(y, 4)) return fail(DSL_ERR_ARG, "%s: y is misaligned", fn);
+  const LoraPlan pl = lora_plan(m, n, k, lr);
+  if (!ws || ws_bytes < pl.total || !aligned(ws, 256))
+    return fail(DSL_ERR_WORKSPACE, "%s: workspace of %zu bytes (256-B aligned) required", fn, pl.total);
+  uint8_t *base = static_cast<uint8_t *>(ws);
+  float *t32 = reinterpret_cast<float *>(base);
+  void *gws = base + pl.t32;
+  uint16_t *t2 = reinterpret_cast<uint16_t *>(base + pl.t32 + pl.ws);
+  uint16_t *b2 = reinterpret_cast<uint16_t *>(base + pl.t32 + pl.ws + pl.t2);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e = dsl::launch_gemm(dsl::MODE_BF16, bf16_args(x, a_t, t32, m, lr, k, lr, false, gws), st);
+  if (e == hipSuccess)
+    e = dsl::launch_lora_split(t32, (int)m, (int)lr, (int)pl.ld2, (int)rank, scales, t2, st);
+  if (e == hipSuccess) e = dsl::launch_lora_dup(static_cast<const uint16_t *>(b_t), (int)n, (int)lr,
+                                                (int)pl.ld2, b2, st);
+  if (e != hipSuccess) return hip_status(e, fn);
+  dsl::GemmArgs g = bf16_args(x, w, y, m, n, k, ldy, false, gws);
+  if (dsl::persist_supported(dsl::MODE_BF16, (int)m, (int)n, (int)k, (int)(2 * (k + pl.ld2)), true) &&
+      (2 * k) % 128 == 0) {
+    // one pass: the adapter columns are a second K segment of every row
+    g.a2 = reinterpret_cast<const uint8_t *>(t2);
+    g.b2 = reinterpret_cast<const uint8_t *>(b2);
+    g.Kb2 = (int)(2 * pl.ld2);
+    e = dsl::launch_gemm(dsl::MODE_BF16, g, st);
+  } else {
+    e = dsl::launch_gemm(dsl::MODE_BF16, g, st);
+    if (e == hipSuccess)
+      e = dsl::launch_gemm(dsl::MODE_BF16, bf16_args(t2, b2, y, m, n, pl.ld2, ldy, true, gws), st);
+  }
+  return hip_status(e, fn);
 }
 
 size_t dsl_moe_route_workspace_bytes(int64_t tokens, int64_t topk, int64_t num_experts) {

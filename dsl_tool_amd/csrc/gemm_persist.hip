@@ -105,6 +105,7 @@ struct PersCfg {
 // many of them exist, and where it lands in C.
 struct TileRef {
   const uint8_t *a, *b;   // first A / W row of the tile (row stride Kb)
+  const uint8_t *a2, *b2; // the same rows of the second K segment (BF16; row stride Kb2)
   int arows, brows;       // rows that exist from there on (>= 1)
   int m0, n0;             // tile origin in C (dense: also in the scale matrices)
   int mend;               // C rows below mend exist (dense: M; grouped: the group's end)
@@ -168,24 +169,29 @@ DSL_DEV int lane_id() {
 template <class Cfg>
 struct Ring {
   const uint8_t *dbase;          // operand rows of the tile, pair 0
+  const uint8_t *dbase2;         // second K segment's rows (pairs nk1 ..), BF16
   const uint8_t *sbase;          // scale rows of the tile, quad 0
   int wrow;                      // the wave's first tile row (uniform)
   int lim;                       // last valid tile row of the operand (uniform)
   int kb;
+  int kb2, nk1;                  // second segment: row stride, first pair
   uint32_t vsub;                 // lane's row within one DMA
   uint32_t vchunk;               // lane's chunk byte offset for even DMAs
   uint32_t soff;                 // lane's scale offset
   int wave;
   bool full;
 
-  DSL_DEV void target(const TileRef &tr, int kb_, int wave_, int lane) {
+  DSL_DEV void target(const TileRef &tr, int kb_, int wave_, int lane, int kb2_ = 0) {
     wave = wave_;
+    kb2 = kb2_;
+    nk1 = kb_ / Cfg::PKB;
     full = Cfg::DS > 0 && wave < Cfg::SC_DMA;
     const bool isA = wave * Cfg::DD < Cfg::A_DMA;
     lim = (isA ? tr.arows : tr.brows) - 1;
     kb = kb_;
     wrow = (isA ? wave * Cfg::DD : wave * Cfg::DD - Cfg::A_DMA) * Cfg::RPI;
     dbase = isA ? tr.a : tr.b;
+    dbase2 = isA ? tr.a2 : tr.b2;
     vsub = lane / Cfg::CH;
     // DMA j covers tile rows wrow + j*RPI + vsub; RPI is even, so the row
     // swizzle only depends on vsub and the parity of wrow/RPI + j
@@ -229,8 +235,16 @@ struct Ring {
     // offset j*RPI only flips bit 2 of the swizzle, by the parity of j
     const uint32_t ch = vchunk ^ (uint32_t)(pipe::swz<Cfg::PKB>(j * Cfg::RPI) * 16);
     // r < 256 and Kb < 2^24 (checked at launch): a full-rate 24-bit multiply
-    dma16(dbase + (int64_t)q * Cfg::PKB, __umul24((uint32_t)r, (uint32_t)kb) + ch,
-          slot + (uint32_t)((wave * Cfg::DD + j) * 1024));
+    if constexpr (Cfg::BF16) {
+      // pairs from nk1 on come from the second segment (selects, no branch)
+      const bool s2 = q >= nk1;
+      const uint8_t *base = s2 ? dbase2 + (int64_t)(q - nk1) * Cfg::PKB : dbase + (int64_t)q * Cfg::PKB;
+      dma16(base, __umul24((uint32_t)r, (uint32_t)(s2 ? kb2 : kb)) + ch,
+            slot + (uint32_t)((wave * Cfg::DD + j) * 1024));
+    } else {
+      dma16(dbase + (int64_t)q * Cfg::PKB, __umul24((uint32_t)r, (uint32_t)kb) + ch,
+            slot + (uint32_t)((wave * Cfg::DD + j) * 1024));
+    }
   }
   // the wave's scale DMA of tile-local quad c into the quad slot at
   // `sslot`, when `on` (uniform)
@@ -515,7 +529,9 @@ void gemm_persist_kernel(const Args p) {
     }
   }
   if (my_tiles <= 0) return;                      // before any copy is issued
-  const int nkp = kb / Cfg::PKB;                  // pairs per tile, >= 1
+  int kb2 = 0;
+  if constexpr (Cfg::BF16) kb2 = p.Kb2;
+  const int nkp = (kb + kb2) / Cfg::PKB;          // pairs per tile, >= 1
 
   auto tile_ref = [&](int t) __attribute__((always_inline)) {
     TileRef tr;
@@ -526,6 +542,11 @@ void gemm_persist_kernel(const Args p) {
       tr.n0 = tn * Cfg::BN;
       tr.a = p.a + (int64_t)tr.m0 * kb;
       tr.b = p.b + (int64_t)tr.n0 * kb;
+      tr.a2 = tr.b2 = nullptr;
+      if constexpr (Cfg::BF16) {
+        tr.a2 = p.a2 + (int64_t)tr.m0 * kb2;
+        tr.b2 = p.b2 + (int64_t)tr.n0 * kb2;
+      }
       tr.arows = p.M - tr.m0;
       tr.mend = p.M;
       tr.e = 0;
@@ -547,6 +568,7 @@ void gemm_persist_kernel(const Args p) {
       tr.mend = __builtin_amdgcn_readfirstlane(hi);
       tr.a = p.x + (int64_t)tr.m0 * kb;
       tr.b = p.w + ((int64_t)e * p.N + tr.n0) * kb;
+      tr.a2 = tr.b2 = nullptr;
       tr.arows = tr.mend - tr.m0;
       tr.e = e;
     }
@@ -564,7 +586,7 @@ void gemm_persist_kernel(const Args p) {
   int it = 0, iq = 0, ig = 0, iqc = -1, ies = 0;
   TileRef itr = tile_ref(0);
   auto retarget = [&]() __attribute__((always_inline)) {
-    ring.target(itr, kb, wave, lane);
+    ring.target(itr, kb, wave, lane, kb2);
     if constexpr (Cfg::SCALED) ring.target_scales(p, itr.m0, itr.n0, lane);
   };
   retarget();

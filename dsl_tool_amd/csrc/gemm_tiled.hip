@@ -67,10 +67,12 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_tiled_kernel(const GemmArgs p) {
         if (row < p.M && col < p.N) {
           float v = acc[tm][tn][i];
           if constexpr (MODE == MODE_FP8_TENSOR || MODE == MODE_NVFP4) v = (v * s1) * s2;
-          if (p.ksplit > 1)
+          if (p.ksplit > 1) {
             unsafeAtomicAdd(p.ws + (int64_t)row * p.N + col, v);
-          else if (p.out_f32)
-            static_cast<float *>(p.c)[(int64_t)row * p.ldc + col] = v;
+          } else if (p.out_f32) {
+            float *d = static_cast<float *>(p.c) + (int64_t)row * p.ldc + col;
+            *d = p.accumulate ? *d + v : v;
+          }
           else
             static_cast<uint16_t *>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16(v);
         }
@@ -85,12 +87,15 @@ __global__ void fill_zero_kernel(float4 *__restrict__ p, int64_t n4) {
 }
 
 __global__ void splitk_finalize_kernel(const float *__restrict__ ws, void *__restrict__ c, int M,
-                                       int N, int64_t ldc, int out_f32) {
+                                       int N, int64_t ldc, int out_f32, int accumulate) {
   const int64_t total = (int64_t)M * N;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t r = i / N, col = i - r * N;
-    if (out_f32) static_cast<float *>(c)[r * ldc + col] = ws[i];
+    if (out_f32) {
+      float *d = static_cast<float *>(c) + r * ldc + col;
+      *d = accumulate ? *d + ws[i] : ws[i];
+    }
     else static_cast<uint16_t *>(c)[r * ldc + col] = f32_to_bf16(ws[i]);
   }
 }
@@ -207,10 +212,11 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   return r;
 }
 
-size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K) {
+size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K, bool accumulate) {
   const int Kb = (mode == MODE_MXFP4 || mode == MODE_NVFP4) ? (int)(K / 2)
                                                             : (mode == MODE_BF16 ? (int)(2 * K) : (int)K);
-  const Route r = route_for(mode, (int)M, (int)N, (int)K, Kb, true, true);
+  Route r = route_for(mode, (int)M, (int)N, (int)K, Kb, true, true);
+  if (accumulate) r.path = PATH_TILED;
   return (r.path == PATH_TILED && r.tiled.ksplit > 1)
              ? (size_t)((M * N + 3) / 4) * 4 * sizeof(float)
              : 0;
@@ -218,7 +224,14 @@ size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K) {
 
 hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
   const uintptr_t sc = reinterpret_cast<uintptr_t>(p.sa) | reinterpret_cast<uintptr_t>(p.sb);
-  const Route r = route_for(mode, p.M, p.N, p.K, p.Kb, (sc & 3) == 0, (sc & 15) == 0);
+  if (p.Kb2 > 0) {   // a second K segment: the persistent BF16 kernel only
+    if (mode != MODE_BF16 || p.accumulate || p.Kb % 128 != 0 || p.Kb2 % 128 != 0 ||
+        !persist_supported(mode, p.M, p.N, p.K, p.Kb + p.Kb2, true))
+      return hipErrorInvalidValue;
+    return launch_gemm_persist(mode, p, st);
+  }
+  Route r = route_for(mode, p.M, p.N, p.K, p.Kb, (sc & 3) == 0, (sc & 15) == 0);
+  if (p.accumulate) r.path = PATH_TILED;   // only the register-staged kernels add into C
   p.ksplit = 1;
   if (r.path == PATH_DECODE) return launch_gemm_decode(mode, p, st);
   if (r.path == PATH_PIPE) return launch_gemm_pipe(mode, p, r.variant, st);
@@ -243,7 +256,7 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
   if (p.ksplit > 1) {
     const int64_t total = (int64_t)p.M * p.N;
     splitk_finalize_kernel<<<(unsigned)std::min<int64_t>((total + 255) / 256, 8192), 256, 0, st>>>(
-        p.ws, p.c, p.M, p.N, p.ldc, p.out_f32);
+        p.ws, p.c, p.M, p.N, p.ldc, p.out_f32, p.accumulate);
     e = hipGetLastError();
   }
   return e;

@@ -39,6 +39,11 @@ struct GemmArgs {
   float *ws;             // split-K fp32 [M][N] accumulation buffer (zeroed by the launcher)
   int ksplit;            // >= 1
   int out_f32;
+  int accumulate;        // fp32 out only: C += result (register-staged kernels)
+  // BF16 on the persistent kernel only: a second K segment, C = A W^T +
+  // A2 W2^T with A2 [M][Kb2], W2 [N][Kb2] (Kb2 % 128 == 0; 0: none)
+  const uint8_t *a2, *b2;
+  int Kb2;
 };
 
 // LDS-DMA pipelined kernel (FP8_TENSOR / MXFP4, Kb % 64 == 0, no split-K);
@@ -64,7 +69,7 @@ hipError_t launch_gemm_decode(int mode, const GemmArgs &p, hipStream_t st);
 // zero-fill / finalize kernels when ksplit > 1).
 hipError_t launch_gemm(int mode, GemmArgs args, hipStream_t st);
 // Workspace the launcher will need for this shape (0 if none).
-size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K);
+size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K, bool accumulate = false);
 
 constexpr int kMaxGroups = 2048;   // groups per grouped launch (LDS tables)
 
@@ -118,5 +123,14 @@ hipError_t launch_moe_permute_quant(const uint16_t *x, int64_t ldx, int k_dim, i
 hipError_t launch_moe_combine(const uint16_t *y, int rows_y, int64_t ldy, int n, const int32_t *dest,
                               const float *w, int tokens, int topk, void *out, int64_t ldo,
                               int out_f32, hipStream_t st);
+
+// -------------------------------------------------------------- LoRA --
+// t32 [M][LR] fp32 -> t2 [M][ld2] bf16: cols [0, LR) hi = bf16(t * s),
+// [LR, 2 LR) lo = bf16(t * s - hi), the rest 0; s = scales[col / rank].
+hipError_t launch_lora_split(const float *t32, int M, int LR, int ld2, int rank,
+                             const float *scales, uint16_t *t2, hipStream_t st);
+// bt [N][LR] -> b2 [N][ld2] = bt | bt | 0.
+hipError_t launch_lora_dup(const uint16_t *bt, int N, int LR, int ld2, uint16_t *b2,
+                           hipStream_t st);
 
 }  // namespace dsl

@@ -111,6 +111,8 @@ class KernelRegistry:
 HIP_GEMM_ENTRIES = (
     ("gemm.bf16_gemm", "bf16_gemm",
      "BF16 GEMM (A[M,K] @ B[K,N], fp32 accumulation and output), gfx950 bf16 MFMA"),
+    ("gemm.lora_fused_gemm", "lora_fused_gemm",
+     "LoRA fused GEMM Y = X@W + Σ scale_l·X@A_l@B_l (bf16 MFMA, fp32 out)"),
     ("gemm.fp8_gemm", "fp8_gemm",
      "FP8 E4M3 GEMM (per-tensor or 1x128/128x128 block scales), gfx950 scaled MFMA"),
     ("gemm.fp4_gemm", "fp4_gemm",
@@ -151,7 +153,10 @@ def gemm_input_schema(kernel_name: str) -> dict:
     registry.py:274-283, extended with this build's keyword arguments)."""
     s = {"A": "Tensor[M, K] bf16/fp16/fp32 (or pre-quantized, see kwargs)",
          "B": "Tensor[K, N] (pass W.t() for a K-major weight W[N, K])"}
-    if kernel_name.endswith("bf16_gemm"):
+    if kernel_name.endswith("lora_fused_gemm"):
+        s = {"X": "Tensor[M, K] bf16", "W": "Tensor[K, N] bf16", "loraA": "Tensor[L, K, R] bf16",
+             "loraB": "Tensor[L, R, N] bf16", "scales": "Tensor[L] fp32 | list of L floats"}
+    elif kernel_name.endswith("bf16_gemm"):
         s = {"A": "Tensor[M, K] bf16", "B": "Tensor[K, N] bf16 (W.t() of a K-major W[N, K] is read in place)",
              "out_dtype": "torch.float32 (default) | torch.bfloat16"}
     elif kernel_name.endswith("fp8_gemm"):
@@ -176,6 +181,8 @@ def gemm_output_schema(kernel_name: str) -> dict:
         return {"C": "Tensor[G, M, N] | Tensor[T, N], bf16 (fp32 for fp32 inputs)"}
     if kernel_name.endswith("bf16_gemm"):
         return {"C": "Tensor[M, N] fp32 (out_dtype=torch.bfloat16 for bf16)"}
+    if kernel_name.endswith("lora_fused_gemm"):
+        return {"Y": "Tensor[M, N] fp32"}
     return {"C": "Tensor[M, N] bf16 (out_dtype=torch.float32 for the reference's fp32)"}
 
 

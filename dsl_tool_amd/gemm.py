@@ -13,6 +13,10 @@ The three registered entry points keep the reference's calling convention
   triton/gemm/gemm_kernels.py:46-65, registered at dispatcher/registry.py:134):
   ``C = A @ B`` of bf16 A [M, K], B [K, N], fp32 accumulation and, as in the
   reference, an fp32 result by default.
+* ``lora_fused_gemm(X, W, loraA, loraB, scales)`` -- ``gemm.lora_fused_gemm``
+  (reference: lora_fused_gemm_kernel, cuda/gemm/grouped_gemm.cu:106-140):
+  ``Y = X @ W + sum_l scales[l] * X @ loraA[l] @ loraB[l]`` in fp32 from bf16
+  operands.
 * ``grouped_gemm(A, B, num_groups)`` -- ``gemm.grouped_gemm``
   (reference: triton/gemm/gemm_kernels.py:164-182).  An int third argument
   means fixed-size groups A [G, M, K], B [G, K, N]; a 1-D integer tensor of
@@ -205,6 +209,44 @@ def bf16_gemm(A: torch.Tensor, B: torch.Tensor, *, out_dtype: torch.dtype = torc
                _out_code(c.dtype), N.ptr(ws), 0 if ws is None else ws.numel() * 4,
                N.stream_of(dev))
     return c
+
+
+def lora_fused_gemm(X: torch.Tensor, W: torch.Tensor, loraA: torch.Tensor, loraB: torch.Tensor,
+                    scales) -> torch.Tensor:
+    """``Y = X @ W + sum_l scales[l] * (X @ loraA[l]) @ loraB[l]``, fp32.
+
+    X [M, K], W [K, N] (``W = Wt.t()`` of a K-major Wt [N, K] is read in
+    place), loraA [L, K, R], loraB [L, R, N], all bf16; scales: L numbers or
+    a float tensor [L].  K % 8 == 0 and L * R % 8 == 0.
+    """
+    for t, nm in ((X, "X"), (W, "W"), (loraA, "loraA"), (loraB, "loraB")):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"lora_fused_gemm: {nm} must be bfloat16 (got {t.dtype})")
+    if X.dim() != 2 or W.dim() != 2 or loraA.dim() != 3 or loraB.dim() != 3:
+        raise ValueError("lora_fused_gemm expects X [M,K], W [K,N], loraA [L,K,R], loraB [L,R,N]")
+    M, K = X.shape
+    K2, Nn = W.shape
+    L, K3, R = loraA.shape
+    if K != K2 or K != K3 or tuple(loraB.shape) != (L, R, Nn):
+        raise ValueError("lora_fused_gemm: shapes do not match")
+    dev = _require_gpu(X, W, loraA, loraB)
+    x = X if X.is_contiguous() else X.contiguous()
+    w = _k_major(W)                                                 # [N, K]
+    a_t = loraA.permute(0, 2, 1).reshape(L * R, K).contiguous()     # row l*R + r = A_l[:, r]
+    b_t = loraB.permute(2, 0, 1).reshape(Nn, L * R).contiguous()    # col l*R + r = B_l[r, :]
+    if isinstance(scales, torch.Tensor):
+        s = scales.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
+    else:
+        s = torch.tensor([float(v) for v in scales], dtype=torch.float32, device=dev)
+    if s.numel() != L:
+        raise ValueError(f"lora_fused_gemm: {L} scales expected")
+    y = torch.empty((M, Nn), dtype=torch.float32, device=dev)
+    nb = N.lib().dsl_lora_gemm_workspace_bytes(M, Nn, K, R, L)
+    ws = torch.empty(max(nb, 256) // 4, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        N.call("dsl_lora_gemm", N.ptr(x), N.ptr(w), N.ptr(a_t), N.ptr(b_t), N.ptr(s), N.ptr(y), M, Nn,
+               K, R, L, Nn, N.ptr(ws), ws.numel() * 4, N.stream_of(dev))
+    return y
 
 
 def fp8_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=1.0, scale_b=1.0, *,

@@ -183,6 +183,22 @@ int dsl_rmsnorm_quant(const void *x, int64_t rows, int64_t cols, int64_t ldx,
 int dsl_swiglu_quant(const void *x, int64_t rows, int64_t hidden, int64_t ldx,
                      int qfmt, void *q, void *scales, void *y, int64_t ldy, void *stream);
 
+/* ---------------------------------------------------------------- LoRA --
+ * y [m][ldy] fp32 = x w^T + sum_l scales[l] * (x a_l^T) b_l^T, bf16
+ * operands, fp32 accumulation: x [m][k], w [n][k], a_t [num_loras*rank][k]
+ * (row l*rank + r is column r of the reference's A_l [k][rank]), b_t
+ * [n][num_loras*rank] (column l*rank + r is row r of B_l [rank][n]).  The
+ * low-rank product t*s is carried as a bf16 pair (hi + lo), so the adapter
+ * term keeps about 16 mantissa bits.  k % 8 == 0, rank*num_loras % 8 == 0.
+ * Replaces lora_fused_gemm_kernel (cuda/gemm/grouped_gemm.cu:106-140).
+ * Needs dsl_lora_gemm_workspace_bytes (256-byte aligned). */
+size_t dsl_lora_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int64_t rank,
+                                     int64_t num_loras);
+int dsl_lora_gemm(const void *x, const void *w, const void *a_t, const void *b_t,
+                  const float *scales, float *y, int64_t m, int64_t n, int64_t k,
+                  int64_t rank, int64_t num_loras, int64_t ldy,
+                  void *workspace, size_t workspace_bytes, void *stream);
+
 /* ------------------------------------------------------------ MoE glue --
  * The steps either side of dsl_grouped_fp8_gemm in an MoE layer.  The
  * reference has no counterpart (its grouped GEMM takes rows already sorted

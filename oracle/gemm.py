@@ -121,6 +121,17 @@ def ref_bf16(a: np.ndarray, w: np.ndarray, f64: bool = True) -> np.ndarray:
     return _mm(a, w, f64)
 
 
+def ref_lora(x, w, a, b, scales) -> np.ndarray:
+    """Y = X @ W + sum_l s_l * (X @ A_l) @ B_l in float64, as float32
+    (cuda/gemm/grouped_gemm.cu:120-137).  x [M, K], w [N, K] (the reference's
+    W [K, N] is w.T), a [L, K, R], b [L, R, N], scales [L]."""
+    x64 = np.asarray(x, np.float64)
+    y = x64 @ np.asarray(w, np.float64).T
+    for l in range(np.asarray(a).shape[0]):
+        y += float(scales[l]) * ((x64 @ np.asarray(a[l], np.float64)) @ np.asarray(b[l], np.float64))
+    return y.astype(np.float32)
+
+
 def tiled_bf16_gemm(a: np.ndarray, w: np.ndarray, block_m=128, block_n=128, block_k=32):
     """The reference's CPU path for bf16 restated: 128x128x32 tiles, fp32
     accumulation over K tiles (tilelang/gemm/gemm_kernels.py:75-95).

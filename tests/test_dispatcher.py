@@ -14,7 +14,7 @@ from dsl_tool_amd.dispatcher import cli as CLI
 from dsl_tool_amd.dispatcher import dispatcher as D
 from dsl_tool_amd.dispatcher.registry import KernelRegistry
 
-NAMES = {"gemm.bf16_gemm", "gemm.fp8_gemm", "gemm.fp4_gemm", "gemm.grouped_gemm",
+NAMES = {"gemm.bf16_gemm", "gemm.lora_fused_gemm", "gemm.fp8_gemm", "gemm.fp4_gemm", "gemm.grouped_gemm",
          "normalization.rmsnorm_quant", "activations.swiglu_quant", "moe.routed_grouped_gemm"}
 
 

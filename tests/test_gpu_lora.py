@@ -1,0 +1,47 @@
+"""LoRA fused GEMM (gemm.lora_fused_gemm) against the float64 formula of
+cuda/gemm/grouped_gemm.cu:106-140 on the same bf16 operands.
+
+The base product accumulates in fp32 and the adapter term is carried as a
+bf16 hi + lo pair, so the result sits within LORA_TOL of max|Y| (measured
+~1e-6; the bound leaves room for K = 4096 sums)."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import gemm as OG
+from dsl_tool_amd import gemm as G
+from dsl_tool_amd import workloads as W
+from tests.util import np_f32
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+LORA_TOL = 2e-5
+
+
+@pytest.mark.parametrize("m,n,k,r,l", [(512, 768, 1024, 16, 2), (300, 520, 264, 8, 3),
+                                       (4096, 4352, 512, 16, 4), (16, 256, 2048, 64, 1)])
+def test_lora_fused_gemm(m, n, k, r, l):
+    x = W.randn_bf16((m, k), 500)
+    w = W.randn_bf16((n, k), 501, 0.05)
+    a = W.randn_bf16((l, k, r), 502, 0.05)
+    b = W.randn_bf16((l, r, n), 503, 0.05)
+    s = [1.5 * (i + 1) * (-1) ** i for i in range(l)]
+    y = G.lora_fused_gemm(x.to(DEV), w.to(DEV).t(), a.to(DEV), b.to(DEV), s)
+    ref = OG.ref_lora(x.float().numpy(), w.float().numpy(), a.float().numpy(), b.float().numpy(), s)
+    glob, _ = OG.rel_errors(np_f32(y), ref)
+    assert glob <= LORA_TOL, f"lora {m}x{n}x{k} r={r} l={l}: {glob:.3g}"
+    # the adapter term is a visible part of the result
+    base = OG.ref_lora(x.float().numpy(), w.float().numpy(), a.float().numpy() * 0, b.float().numpy(), s)
+    assert OG.rel_errors(base, ref)[0] > 100 * LORA_TOL
+
+
+def test_lora_reference_layout_w_and_tensor_scales():
+    x = W.randn_bf16((128, 256), 510)
+    w_kn = W.randn_bf16((256, 384), 511, 0.05)          # contiguous [K, N]
+    a = W.randn_bf16((2, 256, 8), 512, 0.05)
+    b = W.randn_bf16((2, 8, 384), 513, 0.05)
+    s = torch.tensor([0.25, 4.0])
+    y = G.lora_fused_gemm(x.to(DEV), w_kn.to(DEV), a.to(DEV), b.to(DEV), s.to(DEV))
+    ref = OG.ref_lora(x.float().numpy(), w_kn.float().numpy().T, a.float().numpy(), b.float().numpy(),
+                      s.numpy())
+    assert OG.rel_errors(np_f32(y), ref)[0] <= LORA_TOL

@@ -94,6 +94,16 @@ def test_fused_producer_argument_validation(lib):
     assert lib.dsl_swiglu_quant(None, 0, 64, 128, 0, None, None, None, 0, None) == 0
 
 
+def test_lora_argument_validation(lib):
+    fake = 1 << 20
+    rc = lib.dsl_lora_gemm(fake, fake, fake, fake, fake, fake, 64, 64, 64, 3, 1, 64, fake, 1 << 30, None)
+    assert rc == N.DSL_ERR_ARG and "multiple of 8" in _err(lib)
+    need = lib.dsl_lora_gemm_workspace_bytes(256, 256, 512, 16, 2)
+    assert need >= 256 * 32 * 8
+    rc = lib.dsl_lora_gemm(fake, fake, fake, fake, fake, fake, 256, 256, 512, 16, 2, 256, fake, need - 1, None)
+    assert rc == N.DSL_ERR_WORKSPACE
+
+
 def test_moe_glue_argument_validation(lib):
     fake = 1 << 20
     rc = lib.dsl_moe_route(fake, 16, 2, 4096, fake, fake, fake, fake, 1 << 20, None)

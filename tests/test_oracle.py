@@ -260,6 +260,22 @@ def test_ref_bf16_matches_exact_rational_brute_force():
     assert not np.allclose(OG.ref_bf16(sq, sq), OG.ref_bf16(sq, sq.T.copy()), rtol=1e-3)
 
 
+def test_ref_lora_matches_elementwise_loops():
+    rng = np.random.default_rng(14)
+    M, N, K, R, L = 3, 4, 6, 2, 2
+    x, w = rng.standard_normal((M, K)), rng.standard_normal((N, K))
+    a, b = rng.standard_normal((L, K, R)), rng.standard_normal((L, R, N))
+    s = [0.5, -2.0]
+    y = OG.ref_lora(x, w, a, b, s)
+    for i in range(M):
+        for j in range(N):
+            v = sum(x[i, k] * w[j, k] for k in range(K))
+            for l in range(L):
+                v += s[l] * sum(sum(x[i, k] * a[l, k, r] for k in range(K)) * b[l, r, j] for r in range(R))
+            assert abs(y[i, j] - v) <= 1e-5 * (1 + abs(v))
+    assert not np.allclose(OG.ref_lora(x, w, a, b, [0.5, 2.0]), y)        # a dropped sign fails
+
+
 def test_tiled_bf16_reference_cpu_path_matches_dense_oracle():
     rng = np.random.default_rng(9)
     a = F.round_to_bf16(rng.standard_normal((150, 100)).astype(np.float32))
