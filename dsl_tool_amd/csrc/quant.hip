@@ -346,6 +346,45 @@ __global__ __launch_bounds__(256) void quant_fp8_tile_reg_kernel(
   }
 }
 
+// Wide row groups (1 x gc, gc up to 32768, e.g. one scale per row): one
+// workgroup per group, thread t holding chunks t + 256 j of it in registers.
+template <int CPL>
+__global__ __launch_bounds__(256) void quant_fp8_wide_kernel(
+    const uint16_t *__restrict__ x, int64_t cols, int64_t sr, int gc, uint8_t *__restrict__ q,
+    float *__restrict__ scales) {
+  __shared__ float sh[4];
+  const int64_t gpr = (cols + gc - 1) / gc;
+  const int64_t r = blockIdx.x / gpr, gi = blockIdx.x - r * gpr;
+  const int64_t c0 = gi * gc;
+  const int nch = (int)((c0 + gc < cols ? gc : cols - c0) >> 3);
+  const uint16_t *xr = x + r * sr + c0;
+  uint4 d[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    d[j] = c < nch ? reinterpret_cast<const uint4 *>(xr)[c] : make_uint4(0, 0, 0, 0);
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    float f[8];
+    unpack8(d[j], f);
+    m = fmaxf(m, amax8(f));
+  }
+  const float s = fp8_scale_of(block_max(m, sh));
+  const float rs = rcp_approx(s);
+  if (threadIdx.x == 0) scales[blockIdx.x] = s;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = threadIdx.x + 256 * j;
+    if (c < nch) {
+      float f[8];
+      unpack8(d[j], f);
+      *reinterpret_cast<uint2 *>(q + r * cols + c0 + (int64_t)c * 8) = e4m3_quot8(f, s, rs);
+    }
+  }
+}
+
 // One workgroup per gr x gc FP8 tile of any size (two reads of the tile).
 template <bool VEC>
 __global__ __launch_bounds__(256) void quant_fp8_tile_kernel(
@@ -508,6 +547,16 @@ hipError_t launch_quant_fp8_blocks(const uint16_t *x, int64_t rows, int64_t cols
   }
   const int64_t tiles = ((rows + gr - 1) / gr) * ((cols + gc - 1) / gc);
   const bool tvec = vec && (gc % 8) == 0;
+  if (gr == 1 && tvec && gc > 128 && gc <= 32768) {
+    const int per = (int)((gc / 8 + 255) / 256);
+    const unsigned g = (unsigned)tiles;
+    if (per <= 1) quant_fp8_wide_kernel<1><<<g, 256, 0, st>>>(x, cols, sr, (int)gc, q, scales);
+    else if (per <= 2) quant_fp8_wide_kernel<2><<<g, 256, 0, st>>>(x, cols, sr, (int)gc, q, scales);
+    else if (per <= 4) quant_fp8_wide_kernel<4><<<g, 256, 0, st>>>(x, cols, sr, (int)gc, q, scales);
+    else if (per <= 8) quant_fp8_wide_kernel<8><<<g, 256, 0, st>>>(x, cols, sr, (int)gc, q, scales);
+    else quant_fp8_wide_kernel<16><<<g, 256, 0, st>>>(x, cols, sr, (int)gc, q, scales);
+    return hipGetLastError();
+  }
   if (tvec && gr <= 128 && gc <= 128)
     quant_fp8_tile_reg_kernel<<<(unsigned)tiles, 256, 0, st>>>(x, rows, cols, sr, (int)gr, (int)gc, q, scales);
   else if (tvec)

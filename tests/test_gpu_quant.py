@@ -112,7 +112,8 @@ def test_nvfp4_division_near_rounding_boundaries(amax, boost):
     assert np.array_equal(np_u8(q), q_ref)
 
 
-@pytest.mark.parametrize("gr,gc", [(1, 128), (128, 128), (1, 4096), (1, 64), (16, 48)])
+@pytest.mark.parametrize("gr,gc", [(1, 128), (128, 128), (1, 4096), (1, 64), (16, 48), (1, 200), (1, 2048),
+                                   (1, 16384), (1, 32)])
 def test_fp8_blocks_match_oracle(gr, gc):
     x = W.activations(2, 300, 4096, outliers=True)
     q, s = Q.quant_fp8_blocks(x.to(DEV), gr, gc)
