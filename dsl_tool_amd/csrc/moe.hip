@@ -136,6 +136,92 @@ __global__ __launch_bounds__(64) void moe_scatter_kernel(const int32_t *__restri
   }
 }
 
+// Whole route in one workgroup of 16 waves (small n; up to 16 * kOneSteps * 64):
+// wave w ranks its contiguous range of assignments step by step with the
+// ballot scheme of moe_scatter_kernel, keeping per-expert counts in LDS;
+// the expert and wave prefix sums follow in LDS, and each lane then writes
+// the final rows of the assignments it holds in registers.
+constexpr int kOneSteps = 64;          // steps of 64 per wave: up to 65536 assignments
+
+__global__ __launch_bounds__(1024) void moe_route_one_kernel(const int32_t *__restrict__ ids, int n,
+                                                            int E, int topk,
+                                                            int32_t *__restrict__ offsets,
+                                                            int32_t *__restrict__ dest,
+                                                            int32_t *__restrict__ src_token) {
+  extern __shared__ int cnt[];           // [16][E] per-wave counts, then wave bases
+  __shared__ int tot[kMaxGroups + 1];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  for (int i = threadIdx.x; i < 16 * E; i += 1024) cnt[i] = 0;
+  __syncthreads();
+  const int per_wave = (n + 15) / 16;
+  const int steps = (per_wave + 63) / 64;
+  const int a0 = w * per_wave, a1 = min(n, a0 + per_wave);
+  int bits = 0;
+  while ((1 << bits) < E + 1) ++bits;
+  const uint64_t below = (1ull << lane) - 1ull;
+  // key (12 bits, E for dropped) and rank within the wave (20 bits), packed
+  int kr[kOneSteps];
+  int *mine = cnt + w * E;
+#pragma unroll
+  for (int st = 0; st < kOneSteps; ++st) {
+    kr[st] = E;
+    if (st < steps) {                    // uniform
+      const int a = a0 + st * 64 + lane;
+      const int e = a < a1 ? ids[a] : -1;
+      kr[st] = (e >= 0 && e < E) ? e : E;
+    }
+  }
+#pragma unroll
+  for (int st = 0; st < kOneSteps; ++st) {
+    if (st < steps) {                    // uniform
+      const int k = kr[st];
+      uint64_t same = ~0ull;
+      for (int b = 0; b < bits; ++b) {
+        const uint64_t m = __ballot((k >> b) & 1);
+        same &= ((k >> b) & 1) ? m : ~m;
+      }
+      int r = 0;
+      if (k < E) r = mine[k] + __popcll(same & below);
+      __builtin_amdgcn_wave_barrier();
+      if (k < E && (same >> lane) == 1ull) mine[k] = r + 1;
+      kr[st] = k | (r << 12);
+    }
+  }
+  __syncthreads();
+  // per expert: total and the prefix over waves (cnt becomes the wave base)
+  for (int e = threadIdx.x; e < E; e += 1024) {
+    int s = 0;
+    for (int ww = 0; ww < 16; ++ww) {
+      const int c = cnt[ww * E + e];
+      cnt[ww * E + e] = s;
+      s += c;
+    }
+    tot[e] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {                // exclusive scan over experts (E <= 2048)
+    int s = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = tot[e];
+      tot[e] = s;
+      offsets[e] = s;
+      s += c;
+    }
+    offsets[E] = s;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int st = 0; st < kOneSteps; ++st) {
+    const int a = a0 + st * 64 + lane;
+    if (st < steps && a < a1) {
+      const int k = kr[st] & 0xfff, r = kr[st] >> 12;
+      const int row = k < E ? tot[k] + cnt[w * E + k] + r : -1;
+      dest[a] = row;
+      if (row >= 0) src_token[row] = a / topk;
+    }
+  }
+}
+
 // Gather + per-row E4M3: one workgroup per sorted row, thread t holding
 // chunks t + 256 j of the source token's row.  Rows at or past
 // offsets[E] (the routed total; the grid covers every assignment) exit.
@@ -234,6 +320,14 @@ size_t moe_route_workspace_bytes(int64_t assignments, int64_t num_experts) {
 
 hipError_t launch_moe_route(const int32_t *ids, int n, int topk, int E, int32_t *offsets,
                             int32_t *dest, int32_t *src_token, int32_t *ws, hipStream_t st) {
+  // one launch for small batches (decode-time routing); the three-pass form
+  // spreads the scattered row writes over many CUs and wins beyond that
+  // (32768 assignments: 20 us against 38 us in one workgroup)
+  if (n <= 4096 && E <= 2047 && 16 * E * (int)sizeof(int) <= 64 * 1024) {
+    moe_route_one_kernel<<<1, 1024, (size_t)16 * E * sizeof(int), st>>>(ids, n, E, topk, offsets,
+                                                                        dest, src_token);
+    return hipGetLastError();
+  }
   const int nb = n > 0 ? (n + kRouteChunk - 1) / kRouteChunk : 0;
   const size_t lds = (size_t)E * sizeof(int);
   if (nb > 0) moe_count_kernel<<<nb, 256, lds, st>>>(ids, n, E, ws);

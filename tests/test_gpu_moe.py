@@ -25,8 +25,9 @@ def _ids(T, k, E, seed, drop=False):
     return ids
 
 
+# small batches take the one-workgroup route, the others the three-pass one
 ROUTE_CASES = [(4096, 8, 64, False), (37, 3, 5, True), (1, 1, 1, False), (3000, 6, 2048, True),
-               (513, 4, 7, False)]
+               (513, 4, 7, False), (512, 8, 64, True), (1024, 4, 1000, False)]
 
 
 @pytest.mark.parametrize("T,k,E,drop", ROUTE_CASES)
