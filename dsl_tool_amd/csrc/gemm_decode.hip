@@ -1,7 +1,8 @@
 // Skinny-M ("decode") quantized GEMMs for gfx950: C[M,N] = A[M,K] . W[N,K]^T
 // with few activation rows, bound by streaming W from HBM.
 //
-// gemm_decode_kernel (FP8 per-tensor, FP8 1x128/128x128 block, MXFP4; M <= 32)
+// gemm_decode_kernel (FP8 per-tensor, FP8 1x128/128x128 block, MXFP4, bf16;
+// M <= 32)
 //   One workgroup owns 32 rows of W (two 16-row MFMA tiles) over the whole
 //   of K; its four waves split K into contiguous ranges of whole 1 KB chunks
 //   (1 KB of every row: 1024 FP8 or 2048 FP4 elements).  A wave streams a
@@ -27,6 +28,8 @@
 //       sum is unchanged; for block scales a step is exactly one 128-K scale
 //       group, folded as acc += part * sa[m][grp] * sb[n/128][grp], the
 //       group-partial form of cuda/gemm/fp8_gemm.cu:84-97).
+//     bf16: as FP8 per-tensor with 64 elements per 128-byte step; the lane's
+//       32 bytes feed two v_mfma_f32_16x16x32_bf16 (first and second chunk).
 //     MXFP4: K is taken in 512-element superblocks of 4 steps; at step j of
 //       a superblock group g holds the 32-element block 4g+j, so a lane's data
 //       for the superblock is 64 contiguous bytes and its 4 E8M0 scale bytes
@@ -256,6 +259,8 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_decode_kernel(const GemmArgs p) 
               const v4f part = mfma_fp8(st.af[a][s], wf, zero);
               const float sbv = s < 4 ? sb0[s & 3] : sb1[s & 3];
               st.acc[T][a] = part * (st.sa[a][s] * sbv) + st.acc[T][a];
+            } else if constexpr (Cfg::MODE == MODE_BF16) {
+              st.acc[T][a] = mfma_bf16(st.af[a][s], wf, st.acc[T][a]);
             } else {
               st.acc[T][a] = mfma_fp8(st.af[a][s], wf, st.acc[T][a]);
             }
@@ -488,7 +493,7 @@ bool decode_supported(int mode, int M, int K, int Kb, bool scales4, bool scales1
     return scales16 && M <= 4 && (nch == 1 || nch == 2 || nch == 4 || nch == 8) && M * nch <= 8;
   }
   if (M > 32) return false;
-  if (mode == MODE_FP8_TENSOR) return true;
+  if (mode == MODE_FP8_TENSOR || mode == MODE_BF16) return true;
   // block scales and E8M0 rows move by 16-byte direct loads
   if (mode == MODE_FP8_BLOCK) return scales16 && K % 512 == 0;
   if (mode == MODE_MXFP4) return scales16 && K % 512 == 0;
@@ -500,6 +505,7 @@ hipError_t launch_gemm_decode(int mode, const GemmArgs &p, hipStream_t st) {
     case MODE_FP8_TENSOR: return launch_decode_mode<MODE_FP8_TENSOR>(p, st);
     case MODE_FP8_BLOCK: return launch_decode_mode<MODE_FP8_BLOCK>(p, st);
     case MODE_MXFP4: return launch_decode_mode<MODE_MXFP4>(p, st);
+    case MODE_BF16: return launch_decode_mode<MODE_BF16>(p, st);
     default:
       switch (p.M) {
         case 1: return launch_gemv_nv_m<1>(p, st);

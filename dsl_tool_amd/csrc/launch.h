@@ -59,7 +59,7 @@ bool persist_supported(int mode, int M, int N, int K, int Kb, bool scales16);
 hipError_t launch_gemm_persist(int mode, const GemmArgs &p, hipStream_t st);
 
 // Skinny-M kernels, one launch, no workspace (Kb % 1024 == 0):
-//   M <= 32: FP8_TENSOR; FP8_BLOCK and MXFP4 with 16-byte aligned scales
+//   M <= 32: FP8_TENSOR and BF16; FP8_BLOCK and MXFP4 with 16-byte aligned scales
 //            and K % 512 == 0;
 //   M <= 4:  NVFP4 GEMV with 4-byte aligned scales and M * Kb/1024 <= 8.
 bool decode_supported(int mode, int M, int K, int Kb, bool scales4, bool scales16);

@@ -28,7 +28,9 @@ SHAPES = [
     (2048, 2048, 1024),   # register-staged 256x256 tiles
     (300, 520, 264),      # ragged M / N, K % 64 != 0
     (513, 257, 136),
-    (16, 2048, 4096),     # small M: split K over a workspace
+    (16, 2048, 4096),     # small M: the decode kernel (K % 512 == 0)
+    (32, 7168, 1024),
+    (16, 512, 1032),      # small M, other K: split K over a workspace
     (1, 256, 64),
 ]
 

@@ -66,10 +66,12 @@ def test_bf16_gemm_argument_validation(lib):
     assert rc == N.DSL_ERR_ARG and "aligned" in _err(lib)
     rc = lib.dsl_bf16_gemm(fake, fake, fake, 16, 16, 16, 16, 5, None, 0, None)
     assert rc == N.DSL_ERR_ARG and "out_dtype" in _err(lib)
-    # small M splits K over a workspace; without one the call is refused
-    need = lib.dsl_gemm_workspace_bytes(N.OP_BF16, 16, 256, 4096)
+    # small M with K % 512 == 0 takes the one-launch decode kernel (no
+    # workspace); other K split over a workspace, and without one the call is refused
+    assert lib.dsl_gemm_workspace_bytes(N.OP_BF16, 16, 256, 4096) == 0
+    need = lib.dsl_gemm_workspace_bytes(N.OP_BF16, 16, 256, 4104)
     assert need >= 16 * 256 * 4
-    rc = lib.dsl_bf16_gemm(fake, fake, fake, 16, 256, 4096, 256, 0, None, 0, None)
+    rc = lib.dsl_bf16_gemm(fake, fake, fake, 16, 256, 4104, 256, 0, None, 0, None)
     assert rc == N.DSL_ERR_WORKSPACE
     # large problems run on the persistent kernel without workspace
     assert lib.dsl_gemm_workspace_bytes(N.OP_BF16, 4096, 4096, 4096) == 0
