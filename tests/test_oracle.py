@@ -406,3 +406,26 @@ def test_gemm_kat_discriminates_transposed_operand_and_dropped_scale(kat):
                               OG.dequant_fp8_blocks(qw, np.ones_like(sw), 128, 128), True)
     g, _ = OG.rel_errors(bad, kat["fp8b_c"])
     assert g > 1e-2
+
+
+def test_freivalds_check_catches_misplaced_and_misscaled_tiles():
+    """The whole-output check of the full-size GPU tests (C v against
+    A' (W'^T v), row by row) passes a correct bf16 product and fails one
+    with a tile copied from elsewhere, a tile left at zero or a tile off by
+    a 10% scale."""
+    import torch
+
+    from tests.test_gpu_fullsize import _freivalds
+
+    rng = np.random.default_rng(5)
+    a = rng.standard_normal((512, 256)).astype(np.float32)
+    w = (0.02 * rng.standard_normal((384, 256))).astype(np.float32)
+    c = torch.from_numpy(OG.round_to_bf16(a @ w.T))
+    _freivalds(c, a, w, 1, "correct")
+    bad = [c.clone() for _ in range(3)]
+    bad[0][256:512, 128:256] = c[0:256, 128:256]
+    bad[1][0:256, 256:384] = 0
+    bad[2][256:512, 0:128] *= 1.1
+    for i, b in enumerate(bad):
+        with pytest.raises(AssertionError):
+            _freivalds(b, a, w, 1, f"planted {i}")
