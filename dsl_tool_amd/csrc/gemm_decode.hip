@@ -40,7 +40,8 @@
 //   groups.
 //
 // gemv_nvfp4_kernel (NVFP4, M <= 4)
-//   One wave owns RPW consecutive W rows over all of K.  Lane l holds bytes
+//   One wave owns RPW consecutive W rows over all of K (2, 4 or 8 by the
+//   number of activation rows and K).  Lane l holds bytes
 //   [16l, 16l+16) of every 1 KB chunk of a row (32 E2M1 codes = two 16-element
 //   E4M3 blocks), so each load instruction reads one row's 1 KB
 //   contiguously.  The E4M3 scales of the wave's rows are contiguous in
@@ -453,7 +454,11 @@ static hipError_t launch_gemv_nv(const GemmArgs &p, hipStream_t st) {
   if constexpr (MM * NCH > 8) {
     return hipErrorInvalidValue;          // excluded by decode_supported (register budget)
   } else {
-    constexpr int RPW = 4;
+    // W rows per wave (measured at N=14336, K=4096): one activation row
+    // wants more, smaller waves (RPW 2: 9.3 us against 9.7 with 4; K=16384:
+    // 10.7 against 12.0), four rows want fewer, longer ones (RPW 8: 22.5
+    // against 25.2), as long as the W and activation registers fit
+    constexpr int RPW = MM == 1 ? 2 : ((MM * 16 + 32) * NCH <= 192 ? 8 : 4);
     const int waves = (p.N + RPW - 1) / RPW;
     gemv_nvfp4_kernel<MM, NCH, RPW><<<(waves + 3) / 4, 256, 0, st>>>(p);
     return hipGetLastError();
