@@ -86,17 +86,40 @@ __global__ void fill_zero_kernel(float4 *__restrict__ p, int64_t n4) {
     p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
 }
 
+// Split-K finalize: C (bf16, fp32, or fp32 += for accumulate) from the fp32
+// sums in ws [M][N].  Rows over blockIdx.y (grid-stride), four columns per
+// thread; `vec`: N % 4 == 0 and C rows aligned for 16-byte (fp32) / 8-byte
+// (bf16) stores, so a thread moves its four columns with one load and one
+// store (no per-element index division).
 __global__ void splitk_finalize_kernel(const float *__restrict__ ws, void *__restrict__ c, int M,
-                                       int N, int64_t ldc, int out_f32, int accumulate) {
-  const int64_t total = (int64_t)M * N;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / N, col = i - r * N;
-    if (out_f32) {
-      float *d = static_cast<float *>(c) + r * ldc + col;
-      *d = accumulate ? *d + ws[i] : ws[i];
+                                       int N, int64_t ldc, int out_f32, int accumulate, int vec) {
+  const int col = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (col >= N) return;
+  for (int r = blockIdx.y; r < M; r += gridDim.y) {
+    const float *src = ws + (int64_t)r * N + col;
+    if (vec) {
+      float4 v = *reinterpret_cast<const float4 *>(src);
+      if (out_f32) {
+        float4 *d = reinterpret_cast<float4 *>(static_cast<float *>(c) + r * ldc + col);
+        if (accumulate) {
+          const float4 o = *d;
+          v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
+        }
+        *d = v;
+      } else {
+        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(c) + r * ldc + col) =
+            make_uint2(pack_bf16x2(v.x, v.y), pack_bf16x2(v.z, v.w));
+      }
+    } else {
+      for (int t = 0; t < 4 && col + t < N; ++t) {
+        if (out_f32) {
+          float *d = static_cast<float *>(c) + r * ldc + col + t;
+          *d = accumulate ? *d + src[t] : src[t];
+        } else {
+          static_cast<uint16_t *>(c)[r * ldc + col + t] = f32_to_bf16(src[t]);
+        }
+      }
     }
-    else static_cast<uint16_t *>(c)[r * ldc + col] = f32_to_bf16(ws[i]);
   }
 }
 
@@ -254,9 +277,12 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (p.ksplit > 1) {
-    const int64_t total = (int64_t)p.M * p.N;
-    splitk_finalize_kernel<<<(unsigned)std::min<int64_t>((total + 255) / 256, 8192), 256, 0, st>>>(
-        p.ws, p.c, p.M, p.N, p.ldc, p.out_f32, p.accumulate);
+    const int esz = p.out_f32 ? 4 : 2;
+    const int vec = p.N % 4 == 0 && p.ldc % 4 == 0 &&
+                    (reinterpret_cast<uintptr_t>(p.c) % (4 * esz)) == 0;
+    const dim3 fgrid((unsigned)((p.N + 1023) / 1024), (unsigned)std::min(p.M, 4096));
+    splitk_finalize_kernel<<<fgrid, 256, 0, st>>>(p.ws, p.c, p.M, p.N, p.ldc, p.out_f32,
+                                                  p.accumulate, vec);
     e = hipGetLastError();
   }
   return e;
