@@ -197,7 +197,7 @@ def build_cases(names, dev):
             out_b, passes = r * k + sc.numel() * 4, 1
 
             def launch(i, stream):
-                return L.dsl_quant_fp8_blocks(x.data_ptr(), r, k, k, 1, 128, 128, q.data_ptr(),
+                return L.dsl_quant_fp8_blocks(x.data_ptr(), r, k, k, 1, 0, 128, 128, q.data_ptr(),
                                               sc.data_ptr(), stream)
         elif kind == "fp8_row128":
             q = torch.empty((r, k), dtype=torch.uint8, device=dev)
@@ -205,7 +205,7 @@ def build_cases(names, dev):
             out_b, passes = r * k + sc.numel() * 4, 1
 
             def launch(i, stream):
-                return L.dsl_quant_fp8_blocks(x.data_ptr(), r, k, k, 1, 1, 128, q.data_ptr(),
+                return L.dsl_quant_fp8_blocks(x.data_ptr(), r, k, k, 1, 0, 1, 128, q.data_ptr(),
                                               sc.data_ptr(), stream)
         elif kind == "fp8_tensor":
             q = torch.empty((r, k), dtype=torch.uint8, device=dev)
@@ -213,7 +213,7 @@ def build_cases(names, dev):
             out_b, passes = r * k + 4, 2
 
             def launch(i, stream):
-                return L.dsl_quant_fp8_tensor(x.data_ptr(), r, k, k, 1, q.data_ptr(), sc.data_ptr(),
+                return L.dsl_quant_fp8_tensor(x.data_ptr(), r, k, k, 1, 0, q.data_ptr(), sc.data_ptr(),
                                               ws.data_ptr(), ws.numel() * 4, stream)
         elif kind == "mxfp4":
             q = torch.empty((r, k // 2), dtype=torch.uint8, device=dev)
@@ -221,7 +221,7 @@ def build_cases(names, dev):
             out_b, passes = r * k // 2 + r * k // 32, 1
 
             def launch(i, stream):
-                return L.dsl_quant_mxfp4(x.data_ptr(), r, k, k, 1, q.data_ptr(), sc.data_ptr(),
+                return L.dsl_quant_mxfp4(x.data_ptr(), r, k, k, 1, 0, q.data_ptr(), sc.data_ptr(),
                                          stream)
         else:
             q = torch.empty((r, k // 2), dtype=torch.uint8, device=dev)
@@ -230,7 +230,7 @@ def build_cases(names, dev):
             out_b, passes = r * k // 2 + r * k // 16 + 4, 2
 
             def launch(i, stream):
-                return L.dsl_quant_nvfp4(x.data_ptr(), r, k, k, 1, q.data_ptr(), sc.data_ptr(),
+                return L.dsl_quant_nvfp4(x.data_ptr(), r, k, k, 1, 0, q.data_ptr(), sc.data_ptr(),
                                          g.data_ptr(), ws.data_ptr(), ws.numel() * 4, stream)
         nbytes = passes * 2 * r * k + out_b
         return Case(name, 0.0, nbytes, PEAK_FP8_TFLOPS, "hbm", launch, 1,
@@ -342,7 +342,7 @@ def build_cases(names, dev):
             rc = produce(stream)
             if rc or fused:
                 return rc
-            return L.dsl_quant_fp8_blocks(y.data_ptr(), r, c, c, 1, 1, 128, q.data_ptr(),
+            return L.dsl_quant_fp8_blocks(y.data_ptr(), r, c, c, 1, 0, 1, 128, q.data_ptr(),
                                           sc.data_ptr(), stream)
         out_b = r * c + sc.numel() * 4
         nbytes = 2 * r * ncol_in + 2 * c + out_b if fused else 2 * r * ncol_in + 2 * c + 4 * r * c + out_b

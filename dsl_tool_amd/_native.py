@@ -32,7 +32,8 @@ FMT_MXFP4, FMT_NVFP4 = 0, 1
 OP_FP8, OP_FP4, OP_GROUPED_FP8, OP_BF16 = 0, 1, 2, 3
 QFMT_FP8_G128, QFMT_MXFP4 = 0, 1
 W_BF16, W_F32 = 0, 1
-ABI_VERSION = 5
+IN_BF16, IN_F32 = 0, 1
+ABI_VERSION = 6
 
 
 class DslLibraryError(ImportError):
@@ -53,10 +54,10 @@ _vp, _i64, _i32, _sz = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_s
 SIGNATURES = {
     "dsl_last_error": (ctypes.c_char_p, []),
     "dsl_abi_version": (_i32, []),
-    "dsl_quant_fp8_tensor": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _sz, _vp]),
-    "dsl_quant_fp8_blocks": (_i32, [_vp, _i64, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
-    "dsl_quant_mxfp4": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
-    "dsl_quant_nvfp4": (_i32, [_vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "dsl_quant_fp8_tensor": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "dsl_quant_fp8_blocks": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _i64, _i64, _vp, _vp, _vp]),
+    "dsl_quant_mxfp4": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp]),
+    "dsl_quant_nvfp4": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _sz, _vp]),
     "dsl_quant_workspace_bytes": (_sz, [_i64, _i64]),
     "dsl_fp8_gemm": (_i32, [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i32, _vp, _vp,
                             _vp, _sz, _vp]),

@@ -37,14 +37,17 @@ int hip_status(hipError_t e, const char *what) {
 
 bool aligned(const void *p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
-// Common checks of a bf16 input matrix.
+// Common checks of a bf16 / fp32 input matrix.
 int check_input(const char *fn, const void *x, int64_t rows, int64_t cols, int64_t sr,
-                int64_t sc) {
+                int64_t sc, int x_dtype) {
+  if (x_dtype != DSL_IN_BF16 && x_dtype != DSL_IN_F32)
+    return fail(DSL_ERR_ARG, "%s: unknown x_dtype %d", fn, x_dtype);
   if (rows < 0 || cols < 0) return fail(DSL_ERR_ARG, "%s: negative shape (%lld, %lld)", fn,
                                         (long long)rows, (long long)cols);
   if (rows == 0 || cols == 0) return DSL_OK;
   if (!x) return fail(DSL_ERR_ARG, "%s: input pointer is NULL", fn);
-  if (!aligned(x, 2)) return fail(DSL_ERR_ARG, "%s: bf16 input must be 2-byte aligned", fn);
+  if (!aligned(x, x_dtype == DSL_IN_F32 ? 4 : 2))
+    return fail(DSL_ERR_ARG, "%s: input must be aligned to its element size", fn);
   if (sr <= 0 || sc <= 0)
     return fail(DSL_ERR_ARG, "%s: strides must be positive (got %lld, %lld)", fn, (long long)sr,
                 (long long)sc);
@@ -80,7 +83,7 @@ extern "C" {
 
 const char *dsl_last_error(void) { return g_err.c_str(); }
 
-int dsl_abi_version(void) { return 5; }
+int dsl_abi_version(void) { return 6; }
 
 size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
   (void)rows;
@@ -89,9 +92,10 @@ size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
 }
 
 int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
-                         uint8_t *q, float *scale, void *ws, size_t ws_bytes, void *stream) {
+                         int x_dtype, uint8_t *q, float *scale, void *ws, size_t ws_bytes,
+                         void *stream) {
   const char *fn = "dsl_quant_fp8_tensor";
-  int rc = check_input(fn, x, rows, cols, sr, sc);
+  int rc = check_input(fn, x, rows, cols, sr, sc, x_dtype);
   if (rc) return rc;
   if (rows == 0 || cols == 0) return ok();
   if ((rc = check_out(fn, q, "q"))) return rc;
@@ -99,16 +103,17 @@ int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols, int64_t sr, 
   if (!ws || ws_bytes < dsl_quant_workspace_bytes(rows, cols))
     return fail(DSL_ERR_WORKSPACE, "%s: workspace of %zu bytes required", fn,
                 dsl_quant_workspace_bytes(rows, cols));
-  return hip_status(dsl::launch_quant_fp8_tensor(static_cast<const uint16_t *>(x), rows, cols,
-                                                 sr, sc, q, scale, static_cast<float *>(ws),
+  return hip_status(dsl::launch_quant_fp8_tensor(x, x_dtype == DSL_IN_F32, rows, cols, sr, sc, q,
+                                                 scale, static_cast<float *>(ws),
                                                  static_cast<hipStream_t>(stream)),
                     fn);
 }
 
 int dsl_quant_fp8_blocks(const void *x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
-                         int64_t gr, int64_t gc, uint8_t *q, float *scales, void *stream) {
+                         int x_dtype, int64_t gr, int64_t gc, uint8_t *q, float *scales,
+                         void *stream) {
   const char *fn = "dsl_quant_fp8_blocks";
-  int rc = check_input(fn, x, rows, cols, sr, sc);
+  int rc = check_input(fn, x, rows, cols, sr, sc, x_dtype);
   if (rc) return rc;
   if (gr <= 0 || gc <= 0)
     return fail(DSL_ERR_ARG, "%s: group sizes must be positive (got %lld x %lld)", fn,
@@ -116,32 +121,31 @@ int dsl_quant_fp8_blocks(const void *x, int64_t rows, int64_t cols, int64_t sr, 
   if (rows == 0 || cols == 0) return ok();
   if ((rc = check_out(fn, q, "q"))) return rc;
   if (!scales) return fail(DSL_ERR_ARG, "%s: scales is NULL", fn);
-  return hip_status(dsl::launch_quant_fp8_blocks(static_cast<const uint16_t *>(x), rows, cols,
-                                                 sr, sc, gr, gc, q, scales,
-                                                 static_cast<hipStream_t>(stream)),
+  return hip_status(dsl::launch_quant_fp8_blocks(x, x_dtype == DSL_IN_F32, rows, cols, sr, sc, gr,
+                                                 gc, q, scales, static_cast<hipStream_t>(stream)),
                     fn);
 }
 
 int dsl_quant_mxfp4(const void *x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
-                    uint8_t *q, uint8_t *e8m0, void *stream) {
+                    int x_dtype, uint8_t *q, uint8_t *e8m0, void *stream) {
   const char *fn = "dsl_quant_mxfp4";
-  int rc = check_input(fn, x, rows, cols, sr, sc);
+  int rc = check_input(fn, x, rows, cols, sr, sc, x_dtype);
   if (rc) return rc;
   if (cols % 32 != 0)
     return fail(DSL_ERR_ARG, "%s: cols=%lld must be a multiple of 32", fn, (long long)cols);
   if (rows == 0 || cols == 0) return ok();
   if ((rc = check_out(fn, q, "q_packed"))) return rc;
   if (!e8m0) return fail(DSL_ERR_ARG, "%s: e8m0 is NULL", fn);
-  return hip_status(dsl::launch_quant_mxfp4(static_cast<const uint16_t *>(x), rows, cols, sr, sc,
+  return hip_status(dsl::launch_quant_mxfp4(x, x_dtype == DSL_IN_F32, rows, cols, sr, sc,
                                             q, e8m0, static_cast<hipStream_t>(stream)),
                     fn);
 }
 
 int dsl_quant_nvfp4(const void *x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
-                    uint8_t *q, uint8_t *e4m3s, float *gscale, void *ws, size_t ws_bytes,
-                    void *stream) {
+                    int x_dtype, uint8_t *q, uint8_t *e4m3s, float *gscale, void *ws,
+                    size_t ws_bytes, void *stream) {
   const char *fn = "dsl_quant_nvfp4";
-  int rc = check_input(fn, x, rows, cols, sr, sc);
+  int rc = check_input(fn, x, rows, cols, sr, sc, x_dtype);
   if (rc) return rc;
   if (cols % 16 != 0)
     return fail(DSL_ERR_ARG, "%s: cols=%lld must be a multiple of 16", fn, (long long)cols);
@@ -151,7 +155,7 @@ int dsl_quant_nvfp4(const void *x, int64_t rows, int64_t cols, int64_t sr, int64
   if (!ws || ws_bytes < dsl_quant_workspace_bytes(rows, cols))
     return fail(DSL_ERR_WORKSPACE, "%s: workspace of %zu bytes required", fn,
                 dsl_quant_workspace_bytes(rows, cols));
-  return hip_status(dsl::launch_quant_nvfp4(static_cast<const uint16_t *>(x), rows, cols, sr, sc,
+  return hip_status(dsl::launch_quant_nvfp4(x, x_dtype == DSL_IN_F32, rows, cols, sr, sc,
                                             q, e4m3s, gscale, static_cast<float *>(ws),
                                             static_cast<hipStream_t>(stream)),
                     fn);
@@ -200,6 +204,7 @@ static int run_gemm(const char *fn, int mode, const uint8_t *a, const uint8_t *b
   p.ga = ga;
   p.gb = gb;
   p.ws = static_cast<float *>(ws);
+  p.ws_bytes = ws ? ws_bytes : 0;
   p.ksplit = 1;
   p.out_f32 = out_dtype == DSL_OUT_F32;
   p.accumulate = 0;
@@ -379,7 +384,7 @@ LoraPlan lora_plan(int64_t m, int64_t n, int64_t k, int64_t lr) {
 }
 
 dsl::GemmArgs bf16_args(const void *a, const void *b, void *c, int64_t m, int64_t n, int64_t k,
-                        int64_t ldc, bool accumulate, void *ws) {
+                        int64_t ldc, bool accumulate, void *ws, size_t ws_bytes) {
   dsl::GemmArgs p;
   p.a = static_cast<const uint8_t *>(a);
   p.b = static_cast<const uint8_t *>(b);
@@ -392,6 +397,7 @@ dsl::GemmArgs bf16_args(const void *a, const void *b, void *c, int64_t m, int64_
   p.sa = p.sb = nullptr;
   p.ga = p.gb = nullptr;
   p.ws = static_cast<float *>(ws);
+  p.ws_bytes = ws_bytes;
   p.ksplit = 1;
   p.out_f32 = 1;
   p.accumulate = accumulate ? 1 : 0;
@@ -435,13 +441,13 @@ int dsl_lora_gemm(const void *x, const void *w, const void *a_t, const void *b_t
   uint16_t *t2 = reinterpret_cast<uint16_t *>(base + pl.t32 + pl.ws);
   uint16_t *b2 = reinterpret_cast<uint16_t *>(base + pl.t32 + pl.ws + pl.t2);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e = dsl::launch_gemm(dsl::MODE_BF16, bf16_args(x, a_t, t32, m, lr, k, lr, false, gws), st);
+  hipError_t e = dsl::launch_gemm(dsl::MODE_BF16, bf16_args(x, a_t, t32, m, lr, k, lr, false, gws, pl.ws), st);
   if (e == hipSuccess)
     e = dsl::launch_lora_split(t32, (int)m, (int)lr, (int)pl.ld2, (int)rank, scales, t2, st);
   if (e == hipSuccess) e = dsl::launch_lora_dup(static_cast<const uint16_t *>(b_t), (int)n, (int)lr,
                                                 (int)pl.ld2, b2, st);
   if (e != hipSuccess) return hip_status(e, fn);
-  dsl::GemmArgs g = bf16_args(x, w, y, m, n, k, ldy, false, gws);
+  dsl::GemmArgs g = bf16_args(x, w, y, m, n, k, ldy, false, gws, pl.ws);
   if (dsl::persist_supported(dsl::MODE_BF16, (int)m, (int)n, (int)k, (int)(2 * (k + pl.ld2)), true) &&
       (2 * k) % 128 == 0) {
     // one pass: the adapter columns are a second K segment of every row
@@ -452,7 +458,7 @@ int dsl_lora_gemm(const void *x, const void *w, const void *a_t, const void *b_t
   } else {
     e = dsl::launch_gemm(dsl::MODE_BF16, g, st);
     if (e == hipSuccess)
-      e = dsl::launch_gemm(dsl::MODE_BF16, bf16_args(t2, b2, y, m, n, pl.ld2, ldy, true, gws), st);
+      e = dsl::launch_gemm(dsl::MODE_BF16, bf16_args(t2, b2, y, m, n, pl.ld2, ldy, true, gws, pl.ws), st);
   }
   return hip_status(e, fn);
 }

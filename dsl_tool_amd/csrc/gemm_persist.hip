@@ -471,11 +471,14 @@ void gemm_persist_kernel(const Args p) {
   const int nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
 
   // per-tensor scales first: no global load may follow the DMA asm
-  float s12 = 1.f;
+  float s1 = 1.f, s2 = 1.f;
   int kb, my_tiles, ntiles;
   int xbase = 0, xstride = grid;   // local tile t is logical tile xbase + t * xstride
   if constexpr (!GR) {
-    if constexpr (Cfg::MODE == MODE_FP8_TENSOR || Cfg::NV) s12 = *p.ga * *p.gb;
+    if constexpr (Cfg::MODE == MODE_FP8_TENSOR || Cfg::NV) {
+      s1 = *p.ga;
+      s2 = *p.gb;
+    }
     kb = p.Kb;
     ntiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * nbn;
     xbase = b;
@@ -685,7 +688,7 @@ void gemm_persist_kernel(const Args p) {
         x = (x * esx[wm * Cfg::WM + i * 32 + r32]) *
             esw[wn * Cfg::WN + j * 32 + 8 * (r >> 2) + 4 * h + (r & 3)];
       } else if constexpr (Cfg::MODE == MODE_FP8_TENSOR || Cfg::NV) {
-        x = x * s12;
+        x = (x * s1) * s2;   // the reference's order, triton/gemm/gemm_kernels.py:97
       } else if constexpr (Cfg::BLOCK) {
         x = x * sc[i];
       }

@@ -260,7 +260,10 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
   if (r.path == PATH_PIPE) return launch_gemm_pipe(mode, p, r.variant, st);
   if (r.path == PATH_PERSIST) return launch_gemm_persist(mode, p, st);
   const Plan pl = r.tiled;
-  p.ksplit = p.ws ? pl.ksplit : 1;
+  // split-K only into a workspace that holds the whole [M][N] fp32 sum
+  // (rounded up to float4); otherwise one pass over K
+  const size_t need = (size_t)(((int64_t)p.M * p.N + 3) / 4) * 16;
+  p.ksplit = (p.ws && p.ws_bytes >= need) ? pl.ksplit : 1;
   if (p.ksplit > 1) {
     const int64_t n4 = ((int64_t)p.M * p.N + 3) / 4;   // workspace is rounded up to float4
     fill_zero_kernel<<<(unsigned)std::min<int64_t>((n4 + 255) / 256, 4096), 256, 0, st>>>(

@@ -183,6 +183,7 @@ void grouped_pipe_kernel(const GroupedArgs p) {
     sub.sa = sub.sb = nullptr;
     sub.ga = sub.gb = nullptr;
     sub.ws = nullptr;
+    sub.ws_bytes = 0;
     sub.ksplit = 1;
     sub.out_f32 = p.out_f32;
 

@@ -10,15 +10,16 @@ namespace dsl {
 constexpr int kMaxPartials = 1024;   // pass-1 amax partials (floats)
 
 // ------------------------------------------------------------- quantize --
-hipError_t launch_quant_fp8_tensor(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
-                                   int64_t sc, uint8_t *q, float *scale, float *partial,
-                                   hipStream_t st);
-hipError_t launch_quant_fp8_blocks(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
-                                   int64_t sc, int64_t gr, int64_t gc, uint8_t *q,
+// x: bf16 bits (f32 false) or fp32 (f32 true) elements x[r*sr + c*sc].
+hipError_t launch_quant_fp8_tensor(const void *x, bool f32, int64_t rows, int64_t cols,
+                                   int64_t sr, int64_t sc, uint8_t *q, float *scale,
+                                   float *partial, hipStream_t st);
+hipError_t launch_quant_fp8_blocks(const void *x, bool f32, int64_t rows, int64_t cols,
+                                   int64_t sr, int64_t sc, int64_t gr, int64_t gc, uint8_t *q,
                                    float *scales, hipStream_t st);
-hipError_t launch_quant_mxfp4(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
+hipError_t launch_quant_mxfp4(const void *x, bool f32, int64_t rows, int64_t cols, int64_t sr,
                               int64_t sc, uint8_t *q, uint8_t *e8m0, hipStream_t st);
-hipError_t launch_quant_nvfp4(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
+hipError_t launch_quant_nvfp4(const void *x, bool f32, int64_t rows, int64_t cols, int64_t sr,
                               int64_t sc, uint8_t *q, uint8_t *e4m3s, float *gscale,
                               float *partial, hipStream_t st);
 
@@ -37,6 +38,7 @@ struct GemmArgs {
   const float *ga;       // FP8_TENSOR: scale_a; NV: global_a
   const float *gb;       // FP8_TENSOR: scale_b; NV: global_b
   float *ws;             // split-K fp32 [M][N] accumulation buffer (zeroed by the launcher)
+  size_t ws_bytes;       // bytes at ws; split-K runs only when it holds the whole [M][N] sum
   int ksplit;            // >= 1
   int out_f32;
   int accumulate;        // fp32 out only: C += result (register-staged kernels)

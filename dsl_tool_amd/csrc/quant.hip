@@ -1,7 +1,8 @@
-// Quantize/pack kernels: bf16 -> E4M3 (per-tensor, block-scaled),
+// Quantize/pack kernels: bf16 or fp32 -> E4M3 (per-tensor, block-scaled),
 // MXFP4 (E2M1 + E8M0 / 32), NVFP4 (E2M1 + E4M3 / 16 + fp32 global).
 //
-// All kernels read x[r*sr + c*sc] (bf16) and write K-major codes q[r*C + c]
+// All kernels read x[r*sr + c*sc] (bf16; fp32 sources take the strided
+// kernels, which divide with the IEEE division) and write K-major codes q[r*C + c]
 // (FP8) or packed nibbles q[r*C/2 + c/2] (FP4).  Code paths, fastest first:
 //   * packed path (sc == 1, sr == C, C % 8 == 0, 16-B aligned x, fewer than
 //     2^31 chunks; row groups also need C % group == 0): the input is one run
@@ -52,14 +53,15 @@ __global__ __launch_bounds__(256) void amax_packed_kernel(
   if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
-template <bool VEC>
+// T = uint16_t (bf16 bits) or float; VEC (16-byte rows of bf16) only for bf16.
+template <bool VEC, typename T>
 __global__ __launch_bounds__(256) void amax_partial_kernel(
-    const uint16_t *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
+    const T *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
     float *__restrict__ partial) {
   __shared__ float sh[4];
   float m = 0.f;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  if (VEC) {
+  if constexpr (VEC) {
     const int64_t cpr = cols >> 3, total = rows * cpr;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
       const int64_t r = i / cpr, c8 = i - r * cpr;
@@ -73,7 +75,7 @@ __global__ __launch_bounds__(256) void amax_partial_kernel(
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
       int64_t r, c;
       if (rfast) { c = i / rows; r = i - c * rows; } else { r = i / cols; c = i - r * cols; }
-      m = fmaxf(m, __builtin_fabsf(load_bf16(x, r * sr + c * sc)));
+      m = fmaxf(m, __builtin_fabsf(load_in(x, r * sr + c * sc)));
     }
   }
   m = block_max(m, sh);
@@ -169,17 +171,18 @@ __global__ __launch_bounds__(256) void quant_packed_kernel(
 // ---------------------------------------------------------------------------
 // Per-tensor E4M3, pass 2 (non-packed input).
 // ---------------------------------------------------------------------------
-template <bool VEC>
+template <bool VEC, typename T>
 __global__ __launch_bounds__(256) void quant_fp8_tensor_kernel(
-    const uint16_t *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
+    const T *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
     const float *__restrict__ partial, int nparts, uint8_t *__restrict__ q,
     float *__restrict__ scale_out) {
   __shared__ float sh[4];
-  const float scale = fp8_scale_of(reduce_partials(partial, nparts, sh));
+  const float am = reduce_partials(partial, nparts, sh);
+  const float scale = VEC ? fp8_scale_of(am) : fp8_scale_ieee(am);
   const float rscale = rcp_approx(scale);
   if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = scale;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  if (VEC) {
+  if constexpr (VEC) {
     const int64_t cpr = cols >> 3, total = rows * cpr;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
       const int64_t r = i / cpr, c8 = i - r * cpr;
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(256) void quant_fp8_tensor_kernel(
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
       int64_t r, c;
       if (rfast) { c = i / rows; r = i - c * rows; } else { r = i / cols; c = i - r * cols; }
-      q[r * cols + c] = e4m3_encode(load_bf16(x, r * sr + c * sc) / scale);
+      q[r * cols + c] = e4m3_encode(__fdiv_rn(load_in(x, r * sr + c * sc), scale));
     }
   }
 }
@@ -254,15 +257,16 @@ __global__ __launch_bounds__(256) void quant_rowgroup_kernel(
 // ---------------------------------------------------------------------------
 // Strided path: one thread per scale group (group_rows == 1 groups only).
 // ---------------------------------------------------------------------------
-template <int KIND>
+// Every division here is the IEEE one (__fdiv_rn), for bf16 and fp32 sources.
+template <int KIND, typename T>
 __global__ __launch_bounds__(256) void quant_group_scalar_kernel(
-    const uint16_t *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
+    const T *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
     int64_t gsize, uint8_t *__restrict__ q, void *__restrict__ scales,
     const float *__restrict__ partial, int nparts, float *__restrict__ global_out) {
   __shared__ float sh[4];
   float sg = 1.f;
   if (KIND == KIND_NV) {
-    sg = nv_global_of(reduce_partials(partial, nparts, sh));
+    sg = nv_global_ieee(reduce_partials(partial, nparts, sh));
     if (blockIdx.x == 0 && threadIdx.x == 0) *global_out = sg;
   }
   const int64_t gpr = (cols + gsize - 1) / gsize;
@@ -274,30 +278,31 @@ __global__ __launch_bounds__(256) void quant_group_scalar_kernel(
     if (rfast) { gi = t / rows; r = t - gi * rows; } else { r = t / gpr; gi = t - r * gpr; }
     const int64_t c0 = gi * gsize, c1 = (c0 + gsize < cols) ? c0 + gsize : cols;
     float m = 0.f;
-    for (int64_t c = c0; c < c1; ++c) m = fmaxf(m, __builtin_fabsf(load_bf16(x, r * sr + c * sc)));
+    for (int64_t c = c0; c < c1; ++c) m = fmaxf(m, __builtin_fabsf(load_in(x, r * sr + c * sc)));
     const int64_t g = r * gpr + gi;
     if (KIND == KIND_FP8) {
-      const float s = fp8_scale_of(m);
+      const float s = fp8_scale_ieee(m);
       reinterpret_cast<float *>(scales)[g] = s;
-      for (int64_t c = c0; c < c1; ++c) q[r * cols + c] = e4m3_encode(load_bf16(x, r * sr + c * sc) / s);
+      for (int64_t c = c0; c < c1; ++c)
+        q[r * cols + c] = e4m3_encode(__fdiv_rn(load_in(x, r * sr + c * sc), s));
     } else if (KIND == KIND_MX) {
       const int e = mx_exponent(m);
       const float mul = pow2_neg(e);
       reinterpret_cast<uint8_t *>(scales)[g] = (uint8_t)(e + 127);
       for (int64_t c = c0; c < c1; c += 2) {
-        uint32_t lo = e2m1_encode(load_bf16(x, r * sr + c * sc) * mul);
-        uint32_t hi = e2m1_encode(load_bf16(x, r * sr + (c + 1) * sc) * mul);
+        uint32_t lo = e2m1_encode(load_in(x, r * sr + c * sc) * mul);
+        uint32_t hi = e2m1_encode(load_in(x, r * sr + (c + 1) * sc) * mul);
         q[(r * cols + c) >> 1] = (uint8_t)(lo | (hi << 4));
       }
     } else {
-      const uint8_t sb = e4m3_encode((m / 6.0f) / sg);
+      const uint8_t sb = e4m3_encode(__fdiv_rn(__fdiv_rn(m, 6.0f), sg));
       const float d = e4m3_decode(sb) * sg;
       reinterpret_cast<uint8_t *>(scales)[g] = sb;
       for (int64_t c = c0; c < c1; c += 2) {
         uint32_t lo = 0, hi = 0;
         if (d != 0.f) {
-          lo = e2m1_encode(load_bf16(x, r * sr + c * sc) / d);
-          hi = e2m1_encode(load_bf16(x, r * sr + (c + 1) * sc) / d);
+          lo = e2m1_encode(__fdiv_rn(load_in(x, r * sr + c * sc), d));
+          hi = e2m1_encode(__fdiv_rn(load_in(x, r * sr + (c + 1) * sc), d));
         }
         q[(r * cols + c) >> 1] = (uint8_t)(lo | (hi << 4));
       }
@@ -386,9 +391,11 @@ __global__ __launch_bounds__(256) void quant_fp8_wide_kernel(
 }
 
 // One workgroup per gr x gc FP8 tile of any size (two reads of the tile).
-template <bool VEC>
+// VEC (16-byte bf16 rows) divides by the reciprocal quotient; the other path
+// divides with __fdiv_rn and serves fp32 sources too (T = float).
+template <bool VEC, typename T>
 __global__ __launch_bounds__(256) void quant_fp8_tile_kernel(
-    const uint16_t *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
+    const T *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
     int64_t gr, int64_t gc, uint8_t *__restrict__ q, float *__restrict__ scales) {
   __shared__ float sh[4];
   const int64_t ntc = (cols + gc - 1) / gc;
@@ -396,7 +403,7 @@ __global__ __launch_bounds__(256) void quant_fp8_tile_kernel(
   const int64_t r0 = tr * gr, c0 = tc * gc;
   const int64_t nr = (r0 + gr < rows ? gr : rows - r0), nc = (c0 + gc < cols ? gc : cols - c0);
   float m = 0.f;
-  if (VEC) {
+  if constexpr (VEC) {
     const int64_t cpr = nc >> 3, total = nr * cpr;
     for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
       const int64_t r = r0 + i / cpr, c = c0 + (i % cpr) * 8;
@@ -409,12 +416,13 @@ __global__ __launch_bounds__(256) void quant_fp8_tile_kernel(
     for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
       int64_t r, c;
       if (sr == 1) { r = r0 + i % nr; c = c0 + i / nr; } else { r = r0 + i / nc; c = c0 + i % nc; }
-      m = fmaxf(m, __builtin_fabsf(load_bf16(x, r * sr + c * sc)));
+      m = fmaxf(m, __builtin_fabsf(load_in(x, r * sr + c * sc)));
     }
   }
-  const float s = fp8_scale_of(block_max(m, sh));
+  const float am = block_max(m, sh);
+  const float s = VEC ? fp8_scale_of(am) : fp8_scale_ieee(am);
   if (threadIdx.x == 0) scales[blockIdx.x] = s;
-  if (VEC) {
+  if constexpr (VEC) {
     const float rs = rcp_approx(s);
     const int64_t cpr = nc >> 3, total = nr * cpr;
     for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
@@ -428,7 +436,7 @@ __global__ __launch_bounds__(256) void quant_fp8_tile_kernel(
     for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
       int64_t r, c;
       if (sr == 1) { r = r0 + i % nr; c = c0 + i / nr; } else { r = r0 + i / nc; c = c0 + i % nc; }
-      q[r * cols + c] = e4m3_encode(load_bf16(x, r * sr + c * sc) / s);
+      q[r * cols + c] = e4m3_encode(__fdiv_rn(load_in(x, r * sr + c * sc), s));
     }
   }
 }
@@ -472,8 +480,17 @@ static int partial_blocks(int64_t elems) {
   return (int)g;
 }
 
-hipError_t launch_amax_partials(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
-                                int64_t sc, float *partial, int *nparts, hipStream_t st) {
+// fp32 sources (f32) always take the strided kernels.
+static hipError_t launch_amax_partials(const void *xv, bool f32, int64_t rows, int64_t cols,
+                                       int64_t sr, int64_t sc, float *partial, int *nparts,
+                                       hipStream_t st) {
+  if (f32) {
+    *nparts = partial_blocks(rows * cols);
+    amax_partial_kernel<false, float><<<*nparts, 256, 0, st>>>(static_cast<const float *>(xv), rows,
+                                                                 cols, sr, sc, partial);
+    return hipGetLastError();
+  }
+  const uint16_t *x = static_cast<const uint16_t *>(xv);
   if (packed_ok(x, rows, cols, sr, sc, 8)) {
     const uint32_t n = (uint32_t)(rows * cols / 8);
     const int g = (int)((n + 256 * 4 - 1) / (256 * 4) < kMaxPartials ? (n + 256 * 4 - 1) / (256 * 4)
@@ -485,25 +502,31 @@ hipError_t launch_amax_partials(const uint16_t *x, int64_t rows, int64_t cols, i
   const int g = partial_blocks(rows * cols);
   *nparts = g;
   if (vec_ok(x, cols, sr, sc))
-    amax_partial_kernel<true><<<g, 256, 0, st>>>(x, rows, cols, sr, sc, partial);
+    amax_partial_kernel<true, uint16_t><<<g, 256, 0, st>>>(x, rows, cols, sr, sc, partial);
   else
-    amax_partial_kernel<false><<<g, 256, 0, st>>>(x, rows, cols, sr, sc, partial);
+    amax_partial_kernel<false, uint16_t><<<g, 256, 0, st>>>(x, rows, cols, sr, sc, partial);
   return hipGetLastError();
 }
 
-hipError_t launch_quant_fp8_tensor(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
-                                   int64_t sc, uint8_t *q, float *scale, float *partial,
-                                   hipStream_t st) {
+hipError_t launch_quant_fp8_tensor(const void *xv, bool f32, int64_t rows, int64_t cols,
+                                   int64_t sr, int64_t sc, uint8_t *q, float *scale,
+                                   float *partial, hipStream_t st) {
   int np = 0;
-  hipError_t e = launch_amax_partials(x, rows, cols, sr, sc, partial, &np, st);
+  hipError_t e = launch_amax_partials(xv, f32, rows, cols, sr, sc, partial, &np, st);
   if (e != hipSuccess) return e;
+  if (f32) {
+    quant_fp8_tensor_kernel<false, float><<<grid_for(rows * cols, 256 * 16), 256, 0, st>>>(
+        static_cast<const float *>(xv), rows, cols, sr, sc, partial, np, q, scale);
+    return hipGetLastError();
+  }
+  const uint16_t *x = static_cast<const uint16_t *>(xv);
   if (packed_ok(x, rows, cols, sr, sc, 8))
     launch_packed<KIND_TENSOR, 1, 1, 4>(x, rows, cols, q, nullptr, partial, np, scale, st);
   else if (vec_ok(x, cols, sr, sc))
-    quant_fp8_tensor_kernel<true><<<grid_for(rows * cols / 8, 256 * 4), 256, 0, st>>>(
+    quant_fp8_tensor_kernel<true, uint16_t><<<grid_for(rows * cols / 8, 256 * 4), 256, 0, st>>>(
         x, rows, cols, sr, sc, partial, np, q, scale);
   else
-    quant_fp8_tensor_kernel<false><<<grid_for(rows * cols, 256 * 16), 256, 0, st>>>(
+    quant_fp8_tensor_kernel<false, uint16_t><<<grid_for(rows * cols, 256 * 16), 256, 0, st>>>(
         x, rows, cols, sr, sc, partial, np, q, scale);
   return hipGetLastError();
 }
@@ -516,9 +539,21 @@ static void launch_team(const uint16_t *x, int64_t rows, int64_t cols, int64_t s
       x, rows, cols, sr, q, scales, partial, np, gout);
 }
 
-hipError_t launch_quant_fp8_blocks(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
-                                   int64_t sc, int64_t gr, int64_t gc, uint8_t *q,
+hipError_t launch_quant_fp8_blocks(const void *xv, bool f32, int64_t rows, int64_t cols,
+                                   int64_t sr, int64_t sc, int64_t gr, int64_t gc, uint8_t *q,
                                    float *scales, hipStream_t st) {
+  const int64_t tiles = ((rows + gr - 1) / gr) * ((cols + gc - 1) / gc);
+  if (f32) {
+    const float *xf = static_cast<const float *>(xv);
+    if (gr == 1 && gc <= 256)
+      quant_group_scalar_kernel<KIND_FP8, float><<<grid_for(tiles, 256), 256, 0, st>>>(
+          xf, rows, cols, sr, sc, gc, q, scales, nullptr, 0, nullptr);
+    else
+      quant_fp8_tile_kernel<false, float><<<(unsigned)tiles, 256, 0, st>>>(xf, rows, cols, sr, sc, gr,
+                                                                           gc, q, scales);
+    return hipGetLastError();
+  }
+  const uint16_t *x = static_cast<const uint16_t *>(xv);
   const bool vec = vec_ok(x, cols, sr, sc);
   const bool row_team = gc == 32 || gc == 64 || gc == 128 || gc == 256;
   if (gr == 1 && row_team && packed_ok(x, rows, cols, sr, sc, gc)) {
@@ -540,12 +575,10 @@ hipError_t launch_quant_fp8_blocks(const uint16_t *x, int64_t rows, int64_t cols
     return hipGetLastError();
   }
   if (gr == 1 && !vec && gc <= 256) {
-    const int64_t ngroups = rows * ((cols + gc - 1) / gc);
-    quant_group_scalar_kernel<KIND_FP8><<<grid_for(ngroups, 256), 256, 0, st>>>(
+    quant_group_scalar_kernel<KIND_FP8, uint16_t><<<grid_for(tiles, 256), 256, 0, st>>>(
         x, rows, cols, sr, sc, gc, q, scales, nullptr, 0, nullptr);
     return hipGetLastError();
   }
-  const int64_t tiles = ((rows + gr - 1) / gr) * ((cols + gc - 1) / gc);
   const bool tvec = vec && (gc % 8) == 0;
   if (gr == 1 && tvec && gc > 128 && gc <= 32768) {
     const int per = (int)((gc / 8 + 255) / 256);
@@ -560,39 +593,51 @@ hipError_t launch_quant_fp8_blocks(const uint16_t *x, int64_t rows, int64_t cols
   if (tvec && gr <= 128 && gc <= 128)
     quant_fp8_tile_reg_kernel<<<(unsigned)tiles, 256, 0, st>>>(x, rows, cols, sr, (int)gr, (int)gc, q, scales);
   else if (tvec)
-    quant_fp8_tile_kernel<true><<<(unsigned)tiles, 256, 0, st>>>(x, rows, cols, sr, sc, gr, gc, q, scales);
+    quant_fp8_tile_kernel<true, uint16_t><<<(unsigned)tiles, 256, 0, st>>>(x, rows, cols, sr, sc, gr, gc, q, scales);
   else
-    quant_fp8_tile_kernel<false><<<(unsigned)tiles, 256, 0, st>>>(x, rows, cols, sr, sc, gr, gc, q, scales);
+    quant_fp8_tile_kernel<false, uint16_t><<<(unsigned)tiles, 256, 0, st>>>(x, rows, cols, sr, sc, gr, gc, q, scales);
   return hipGetLastError();
 }
 
-hipError_t launch_quant_mxfp4(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
+hipError_t launch_quant_mxfp4(const void *xv, bool f32, int64_t rows, int64_t cols, int64_t sr,
                               int64_t sc, uint8_t *q, uint8_t *e8m0, hipStream_t st) {
+  if (f32) {
+    quant_group_scalar_kernel<KIND_MX, float><<<grid_for(rows * (cols / 32), 256), 256, 0, st>>>(
+        static_cast<const float *>(xv), rows, cols, sr, sc, 32, q, e8m0, nullptr, 0, nullptr);
+    return hipGetLastError();
+  }
+  const uint16_t *x = static_cast<const uint16_t *>(xv);
   if (packed_ok(x, rows, cols, sr, sc, 32)) {
     launch_packed<KIND_MX, 4, 4, 4>(x, rows, cols, q, e8m0, nullptr, 0, nullptr, st);
   } else if (vec_ok(x, cols, sr, sc)) {
     launch_team<KIND_MX, 4>(x, rows, cols, sr, q, e8m0, nullptr, 0, nullptr, st);
   } else {
     const int64_t ngroups = rows * (cols / 32);
-    quant_group_scalar_kernel<KIND_MX><<<grid_for(ngroups, 256), 256, 0, st>>>(
+    quant_group_scalar_kernel<KIND_MX, uint16_t><<<grid_for(ngroups, 256), 256, 0, st>>>(
         x, rows, cols, sr, sc, 32, q, e8m0, nullptr, 0, nullptr);
   }
   return hipGetLastError();
 }
 
-hipError_t launch_quant_nvfp4(const uint16_t *x, int64_t rows, int64_t cols, int64_t sr,
+hipError_t launch_quant_nvfp4(const void *xv, bool f32, int64_t rows, int64_t cols, int64_t sr,
                               int64_t sc, uint8_t *q, uint8_t *e4m3s, float *gscale,
                               float *partial, hipStream_t st) {
   int np = 0;
-  hipError_t e = launch_amax_partials(x, rows, cols, sr, sc, partial, &np, st);
+  hipError_t e = launch_amax_partials(xv, f32, rows, cols, sr, sc, partial, &np, st);
   if (e != hipSuccess) return e;
+  if (f32) {
+    quant_group_scalar_kernel<KIND_NV, float><<<grid_for(rows * (cols / 16), 256), 256, 0, st>>>(
+        static_cast<const float *>(xv), rows, cols, sr, sc, 16, q, e4m3s, partial, np, gscale);
+    return hipGetLastError();
+  }
+  const uint16_t *x = static_cast<const uint16_t *>(xv);
   if (packed_ok(x, rows, cols, sr, sc, 16)) {
     launch_packed<KIND_NV, 2, 1, 2>(x, rows, cols, q, e4m3s, partial, np, gscale, st);
   } else if (vec_ok(x, cols, sr, sc)) {
     launch_team<KIND_NV, 2>(x, rows, cols, sr, q, e4m3s, partial, np, gscale, st);
   } else {
     const int64_t ngroups = rows * (cols / 16);
-    quant_group_scalar_kernel<KIND_NV><<<grid_for(ngroups, 256), 256, 0, st>>>(
+    quant_group_scalar_kernel<KIND_NV, uint16_t><<<grid_for(ngroups, 256), 256, 0, st>>>(
         x, rows, cols, sr, sc, 16, q, e4m3s, partial, np, gscale);
   }
   return hipGetLastError();

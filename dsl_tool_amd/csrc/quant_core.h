@@ -64,6 +64,22 @@ DSL_DEV float amax8(const float *f) {
 
 DSL_DEV float load_bf16(const uint16_t *x, int64_t idx) { return bf16_to_f32(x[idx]); }
 
+// One source element as fp32: bf16 bits (uint16_t) or fp32 (float).
+DSL_DEV float load_in(const uint16_t *x, int64_t idx) { return bf16_to_f32(x[idx]); }
+DSL_DEV float load_in(const float *x, int64_t idx) { return x[idx]; }
+
+// The scales with the IEEE division itself (the strided kernels, which also
+// serve fp32 sources: the reciprocal quotient below is only shown exact for
+// bf16 amax values).
+DSL_DEV float fp8_scale_ieee(float amax) {
+  const float s = __fdiv_rn(amax, kE4M3Max);
+  return s < kScaleFloor ? kScaleFloor : s;
+}
+DSL_DEV float nv_global_ieee(float amax) {
+  const float s = __fdiv_rn(amax, kNvGlobalDiv);
+  return s < kScaleFloor ? kScaleFloor : s;
+}
+
 // Reduce the pass-1 partial maxima (n <= kMaxPartials) inside one block.
 DSL_DEV float reduce_partials(const float *partial, int n, float *sh) {
   float m = 0.f;

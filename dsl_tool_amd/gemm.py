@@ -44,7 +44,26 @@ _HIGH = (torch.bfloat16, torch.float16, torch.float32)
 _FP8 = torch.float8_e4m3fn
 
 
-def _out_code(dtype: torch.dtype) -> int:
+_OUT_NAMES = {"bfloat16": torch.bfloat16, "bf16": torch.bfloat16,
+              "float32": torch.float32, "fp32": torch.float32, "float": torch.float32}
+
+
+def _as_dtype(dtype) -> torch.dtype:
+    """An output dtype given as a torch.dtype or by name ("float32", "fp32",
+    "bfloat16", "bf16", optionally prefixed "torch."), as scalar params arrive
+    over the REST / CLI wire (dispatcher.py:285-294 passes them unchanged)."""
+    if isinstance(dtype, torch.dtype):
+        return dtype
+    if isinstance(dtype, str):
+        name = dtype.strip().lower()
+        name = name[6:] if name.startswith("torch.") else name
+        if name in _OUT_NAMES:
+            return _OUT_NAMES[name]
+    raise ValueError(f"unsupported out_dtype {dtype!r}; use bfloat16 or float32")
+
+
+def _out_code(dtype) -> int:
+    dtype = _as_dtype(dtype)
     if dtype == torch.bfloat16:
         return N.OUT_BF16
     if dtype == torch.float32:
@@ -109,7 +128,7 @@ def fp8_gemm_packed(qa, qw, scale_a, scale_b, *, block: bool = False,
         nkg = -(-K // 128)
         if tuple(scale_a.shape) != (M, nkg) or tuple(scale_b.shape) != (-(-Nn // 128), nkg):
             raise ValueError("block scales must be [M, ceil(K/128)] and [ceil(N/128), ceil(K/128)]")
-    c = out if out is not None else torch.empty((M, Nn), dtype=out_dtype, device=dev)
+    c = out if out is not None else torch.empty((M, Nn), dtype=_as_dtype(out_dtype), device=dev)
     ws = _gemm_ws(N.OP_FP8, M, Nn, K, dev)
     with torch.cuda.device(dev):
         N.call("dsl_fp8_gemm", N.ptr(qa), N.ptr(qw), N.ptr(c), M, Nn, K, c.stride(0),
@@ -144,7 +163,7 @@ def fp4_gemm_packed(qa, sa, qw, sw, *, fmt: str = "mxfp4", global_a=None, global
         raise ValueError(f"{fmt} scales must be [M, K/{blk}] and [N, K/{blk}]")
     ga = _dev_scalar(global_a, dev) if global_a is not None else None
     gw = _dev_scalar(global_w, dev) if global_w is not None else None
-    c = out if out is not None else torch.empty((M, Nn), dtype=out_dtype, device=dev)
+    c = out if out is not None else torch.empty((M, Nn), dtype=_as_dtype(out_dtype), device=dev)
     ws = _gemm_ws(N.OP_FP4, M, Nn, K, dev)
     with torch.cuda.device(dev):
         N.call("dsl_fp4_gemm", N.ptr(qa), N.ptr(qw), N.ptr(c), M, Nn, K, c.stride(0),
@@ -173,7 +192,7 @@ def grouped_fp8_gemm_packed(qx, sx, qw, sw, offsets, *, out_dtype=torch.bfloat16
     sw = sw.reshape(G, Nn).float().contiguous()
     if sx.numel() != T:
         raise ValueError("scale_x must have one entry per row")
-    y = out if out is not None else torch.empty((T, Nn), dtype=out_dtype, device=dev)
+    y = out if out is not None else torch.empty((T, Nn), dtype=_as_dtype(out_dtype), device=dev)
     with torch.cuda.device(dev):
         N.call("dsl_grouped_fp8_gemm", N.ptr(qx), N.ptr(qw), N.ptr(y), N.ptr(offsets), G, T, Nn,
                K, y.stride(0), _out_code(y.dtype), N.ptr(sx), N.ptr(sw), N.stream_of(dev))
@@ -202,7 +221,7 @@ def bf16_gemm(A: torch.Tensor, B: torch.Tensor, *, out_dtype: torch.dtype = torc
     dev = _require_gpu(A, B)
     a = A if A.is_contiguous() else A.contiguous()
     w = _k_major(B)
-    c = out if out is not None else torch.empty((M, Nn), dtype=out_dtype, device=dev)
+    c = out if out is not None else torch.empty((M, Nn), dtype=_as_dtype(out_dtype), device=dev)
     ws = _gemm_ws(N.OP_BF16, M, Nn, K, dev)
     with torch.cuda.device(dev):
         N.call("dsl_bf16_gemm", N.ptr(a), N.ptr(w), N.ptr(c), M, Nn, K, c.stride(0),
@@ -299,16 +318,20 @@ def fp8_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=1.0, scale_b=1.0, *,
     raise TypeError(f"fp8_gemm: unsupported dtypes {A.dtype}, {B.dtype}")
 
 
-def fp4_gemm(A: torch.Tensor, B: torch.Tensor, *, fmt: str = "mxfp4", scale_a=None,
-             scale_b=None, global_a=None, global_b=None,
+def fp4_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=None, scale_b=None, *,
+             fmt: str = "mxfp4", global_a=None, global_b=None,
              out_dtype: torch.dtype = torch.bfloat16):
     """FP4 (E2M1) GEMM ``C = A @ B`` with MXFP4 or NVFP4 block scales.
 
     * A [M, K], B [K, N] in bf16/fp16/fp32: quantized on the GPU with ``fmt``.
     * Pre-packed: A uint8 [M, K/2] and B uint8 [K/2, N] (the ``.t()`` view of
       packed weights W [N, K/2]) with scale_a / scale_b bytes ([M, K/32] /
-      [N, K/32] E8M0 for MXFP4, [M, K/16] / [N, K/16] E4M3 for NVFP4) and,
-      for NVFP4, global_a / global_b.
+      [N, K/32] E8M0 for MXFP4, [M, K/16] / [N, K/16] E4M3 for NVFP4; uint8,
+      float8_e8m0fnu or float8_e4m3fn) and, for NVFP4, global_a / global_b
+      (numbers or 1-element tensors).
+    The scale tensors are positional after B, so ``run_from_spec`` can pass a
+    pre-quantized problem as four tensor specs (dispatcher.py:285-294), with
+    ``fmt`` and the NVFP4 global scales as scalar params.
     """
     if A.dim() != 2 or B.dim() != 2:
         raise ValueError("fp4_gemm expects 2-D A and B")
@@ -329,14 +352,14 @@ def fp4_gemm(A: torch.Tensor, B: torch.Tensor, *, fmt: str = "mxfp4", scale_a=No
         return fp4_gemm_packed(qa, sa, qw, sw, fmt="nvfp4", global_a=ga, global_w=gw,
                                out_dtype=out_dtype)
     if A.dtype == torch.uint8 and B.dtype == torch.uint8:
-        if scale_a is None or scale_b is None:
-            raise ValueError("pre-packed fp4 inputs need scale_a and scale_b")
+        if not (isinstance(scale_a, torch.Tensor) and isinstance(scale_b, torch.Tensor)):
+            raise ValueError("pre-packed fp4 inputs need scale_a and scale_b tensors")
         return fp4_gemm_packed(A, scale_a, _k_major(B), scale_b, fmt=fmt, global_a=global_a,
                                global_w=global_b, out_dtype=out_dtype)
     raise TypeError(f"fp4_gemm: unsupported dtypes {A.dtype}, {B.dtype}")
 
 
-def grouped_gemm(A: torch.Tensor, B: torch.Tensor, num_groups, *, scale_a=None, scale_b=None,
+def grouped_gemm(A: torch.Tensor, B: torch.Tensor, num_groups, scale_a=None, scale_b=None, *,
                  out_dtype: torch.dtype | None = None):
     """Grouped FP8 GEMM (MoE experts / LoRA adapters), one W per group.
 
@@ -348,7 +371,10 @@ def grouped_gemm(A: torch.Tensor, B: torch.Tensor, num_groups, *, scale_a=None, 
     High-precision inputs are quantized to E4M3 with per-row activation and
     per-channel weight scales.  float8_e4m3fn inputs need scale_a [T] and
     scale_b [G, N].  The output dtype defaults to A.dtype (bf16 for fp8
-    and fp16 inputs).
+    and fp16 inputs).  scale_a / scale_b are positional after the third
+    argument, so a pre-quantized problem travels over ``run_from_spec`` as
+    five tensor specs [X, B, offsets, scale_a, scale_b]
+    (dispatcher.py:285-294).
     """
     if isinstance(num_groups, torch.Tensor):
         offsets = num_groups
@@ -376,6 +402,7 @@ def grouped_gemm(A: torch.Tensor, B: torch.Tensor, num_groups, *, scale_a=None, 
         raise ValueError(f"K mismatch: A has {K}, B has {K2}")
     if out_dtype is None:
         out_dtype = torch.float32 if A.dtype == torch.float32 else torch.bfloat16
+    out_dtype = _as_dtype(out_dtype)
     Wt = B.transpose(1, 2).reshape(G * Nn, K)          # W[g, n, k] rows
     if X.dtype in _HIGH and B.dtype in _HIGH:
         qx, sx = Q.quant_fp8_blocks(X, 1, K)

@@ -44,6 +44,7 @@ enum { DSL_FMT_MXFP4 = 0, DSL_FMT_NVFP4 = 1 };
 enum { DSL_OP_FP8 = 0, DSL_OP_FP4 = 1, DSL_OP_GROUPED_FP8 = 2, DSL_OP_BF16 = 3 };
 enum { DSL_QFMT_FP8_G128 = 0, DSL_QFMT_MXFP4 = 1 };
 enum { DSL_W_BF16 = 0, DSL_W_F32 = 1 };
+enum { DSL_IN_BF16 = 0, DSL_IN_F32 = 1 };
 
 /* Last error message of the calling thread ("" when none). */
 const char *dsl_last_error(void);
@@ -52,16 +53,19 @@ const char *dsl_last_error(void);
 int dsl_abi_version(void);
 
 /* ------------------------------------------------------------ quantize --
- * Input x is a bf16 matrix read as x[r*stride_row + c*stride_col], rows R,
+ * Input x is a bf16 (x_dtype DSL_IN_BF16) or fp32 (DSL_IN_F32, the
+ * reference's own input type, cuda/gemm/fp8_gemm.cu:118-144,
+ * fp4_gemm.cu:49-90) matrix read as x[r*stride_row + c*stride_col], rows R,
  * cols C, with C the GEMM reduction axis (A[M,K] directly; the reference's
- * B[K,N] as its [N,K] view).  Outputs are K-major: q[r*C + c].
+ * B[K,N] as its [N,K] view).  Outputs are K-major: q[r*C + c].  Codes are
+ * those of the IEEE quotient x / scale for either source type.
  */
 
 /* Per-tensor E4M3.  scale = max(amax/448, 1e-12); q = e4m3(x / scale).
  * Replaces quantize_to_fp8_kernel (cuda/gemm/fp8_gemm.cu:118-144).
  * Writes one float to *scale.  Needs dsl_quant_workspace_bytes(R, C). */
 int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols,
-                         int64_t stride_row, int64_t stride_col,
+                         int64_t stride_row, int64_t stride_col, int x_dtype,
                          uint8_t *q, float *scale,
                          void *workspace, size_t workspace_bytes, void *stream);
 
@@ -71,7 +75,7 @@ int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols,
  * Replaces the scale layout read by fp8_gemm_groupwise_kernel
  * (cuda/gemm/fp8_gemm.cu:67-99), which ships no quantizer of its own. */
 int dsl_quant_fp8_blocks(const void *x, int64_t rows, int64_t cols,
-                         int64_t stride_row, int64_t stride_col,
+                         int64_t stride_row, int64_t stride_col, int x_dtype,
                          int64_t group_rows, int64_t group_cols,
                          uint8_t *q, float *scales, void *stream);
 
@@ -81,7 +85,7 @@ int dsl_quant_fp8_blocks(const void *x, int64_t rows, int64_t cols,
  * Replaces quantize_fp32_to_nvfp4 (cuda/gemm/fp4_gemm.cu:49-90), whose
  * flat fp32 amax/6 scales are not MXFP4. */
 int dsl_quant_mxfp4(const void *x, int64_t rows, int64_t cols,
-                    int64_t stride_row, int64_t stride_col,
+                    int64_t stride_row, int64_t stride_col, int x_dtype,
                     uint8_t *q_packed, uint8_t *e8m0, void *stream);
 
 /* NVFP4: s_g = max(amax_T/2688, 1e-12); per row and 16 K elements
@@ -90,7 +94,7 @@ int dsl_quant_mxfp4(const void *x, int64_t rows, int64_t cols,
  * e4m3_scales [R][C/16], *global_scale = s_g.  C % 16 == 0.
  * Same reference function replaced as dsl_quant_mxfp4. */
 int dsl_quant_nvfp4(const void *x, int64_t rows, int64_t cols,
-                    int64_t stride_row, int64_t stride_col,
+                    int64_t stride_row, int64_t stride_col, int x_dtype,
                     uint8_t *q_packed, uint8_t *e4m3_scales, float *global_scale,
                     void *workspace, size_t workspace_bytes, void *stream);
 

@@ -18,14 +18,14 @@ timed CPU baseline.  The product path (``dsl_tool_amd``) never imports it and
 fails loudly when its HIP library is missing.
 
 Pinning (each function's docstring names its pins; the tests under
-``tests/test_oracle_*.py`` enforce them):
+``tests/test_oracle.py`` enforce them):
 
 * E4M3 encode  -- torch's ``Tensor.to(float8_e4m3fn)`` (an independent
   library routine) over every bf16 bit pattern and a dense fp32 sweep, plus
   the OCP 8-bit FP spec's special values.
 * E2M1 encode  -- exhaustive brute force over all 65 536 bf16 patterns
   against a nearest-value search with the OCP tie rule, and a committed
-  golden table (``tests/golden/e2m1_rne_bf16.npy``).
+  golden table (``tests/golden/e2m1_bf16.npy``).
 * E8M0 encode  -- ``math.frexp`` over every positive finite bf16 value.
 * quantizers   -- closed forms (power-of-two invariance, amax element maps to
   +-448 / +-6, zero blocks), brute-force loops on tiny inputs.

@@ -68,7 +68,7 @@ def e4m3_encode(x: np.ndarray) -> np.ndarray:
     the integer bit pattern and re-bias the exponent (127 -> 7).  Subnormal
     range: RNE of |x| * 2**9 to an integer 0..8 (8 is the smallest normal,
     code 0x08, so the carry is automatically correct).
-    Pinned against torch's float8_e4m3fn cast (tests/test_oracle_formats.py).
+    Pinned against torch's float8_e4m3fn cast (tests/test_oracle.py, tests/golden/e4m3_bf16.npy).
     """
     x = np.ascontiguousarray(x, dtype=np.float32)
     bits = x.view(np.uint32)
@@ -111,7 +111,7 @@ def e2m1_encode(v: np.ndarray) -> np.ndarray:
     <3.5 -> 3, <=5 -> 4, else 6.  The sign bit is kept (so -0.1 -> 0x8).
     NaN maps to the saturated code (+-6); inputs on the path are finite.
     Pinned by exhaustive brute force over all bf16 patterns
-    (tests/test_oracle_formats.py, tests/golden/e2m1_rne_bf16.npy).
+    (tests/test_oracle.py, tests/golden/e2m1_bf16.npy).
     """
     v = np.ascontiguousarray(v, dtype=np.float32)
     sign = ((v.view(np.uint32) >> 31).astype(np.uint8) << 3).astype(np.uint8)

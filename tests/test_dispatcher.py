@@ -197,3 +197,19 @@ def test_cli_param_coercion():
     assert p == {"num_groups": 8, "scale_a": 0.5, "x": True, "fmt": "nvfp4"}
     with pytest.raises(ValueError):
         CLI.parse_params(["novalue"])
+
+
+def test_out_dtype_names_map_to_torch_dtypes():
+    """JSON scalar params carry dtypes as strings (dispatcher.py:285-294)."""
+    import torch
+
+    from dsl_tool_amd import gemm as G
+    for name in ("float32", "fp32", "torch.float32", "FLOAT32", "float"):
+        assert G._as_dtype(name) == torch.float32
+    for name in ("bfloat16", "bf16", "torch.bfloat16"):
+        assert G._as_dtype(name) == torch.bfloat16
+    assert G._as_dtype(torch.float32) == torch.float32
+    with pytest.raises(ValueError):
+        G._as_dtype("int8")
+    with pytest.raises(ValueError):
+        G._out_code(torch.float16)

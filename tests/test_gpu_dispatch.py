@@ -61,3 +61,88 @@ def test_rest_run_grouped_with_offsets():
     ref = OG.ref_grouped_fp8(qx, sx[:, 0], qw.reshape(3, 32, 128), sw.reshape(3, 32), off)
     glob, elem = OG.rel_errors(y, ref)
     assert glob <= 1e-2 and elem <= 1e-2
+
+
+def _raw(arr: np.ndarray, dtype: str) -> dict:
+    """Spec carrying raw bytes (1-byte dtypes) or little-endian values."""
+    return {"shape": list(arr.shape), "dtype": dtype,
+            "data": base64.b64encode(np.ascontiguousarray(arr).tobytes()).decode()}
+
+
+def _out(res_json: dict) -> np.ndarray:
+    out = res_json["output"]
+    return np.frombuffer(base64.b64decode(out["data"]), np.float32).reshape(out["shape"])
+
+
+def test_run_from_spec_out_dtype_by_name():
+    """Scalar params arrive as JSON strings: out_dtype='float32' gives the
+    reference's fp32 output (triton/gemm/gemm_kernels.py:109)."""
+    d = KernelDispatcher()
+    a, w = _seeded((32, 256), 911), _seeded((64, 256), 912, 0.02)
+    res = d.run_from_spec("gemm.fp8_gemm", "hip", [_spec(a), _spec(w.t().contiguous())],
+                          {"out_dtype": "float32"})
+    assert res.output.dtype == torch.float32
+    qa, sa = OQ.quant_fp8_per_tensor(a.float().numpy())
+    qw, sw = OQ.quant_fp8_per_tensor(w.float().numpy())
+    assert_close(res.output, OG.ref_fp8_per_tensor(qa, sa, qw, sw), what="fp32 out by name")
+    assert res.to_dict()["output"]["dtype"] == "float32"
+    res = d.run_from_spec("gemm.bf16_gemm", "hip", [_spec(a), _spec(w.t().contiguous())],
+                          {"out_dtype": "bfloat16"})
+    assert res.output.dtype == torch.bfloat16
+
+
+def test_rest_prequantized_mxfp4_and_nvfp4():
+    """Packed E2M1 codes with E8M0 (MXFP4) or E4M3 (NVFP4) scale bytes, posted
+    as tensor specs in the reference's positional order A, B, scale_a,
+    scale_b; fmt and the NVFP4 global scales as scalar params."""
+    from fastapi.testclient import TestClient
+
+    from dsl_tool_amd.dispatcher.api import app
+    a, w = _seeded((48, 512), 913).float().numpy(), _seeded((96, 512), 914, 0.02).float().numpy()
+    qa, ea = OQ.quant_mxfp4(a)
+    qw, ew = OQ.quant_mxfp4(w)
+    req = {"kernel_name": "gemm.fp4_gemm", "backend": "hip",
+           "inputs": [_raw(qa, "uint8"), _raw(qw.T, "uint8"), _raw(ea, "float8_e8m0fnu"),
+                      _raw(ew, "uint8")],
+           "params": {"fmt": "mxfp4", "out_dtype": "float32"}}
+    pa, sba, ga = OQ.quant_nvfp4(a)
+    pw, sbw, gw = OQ.quant_nvfp4(w)
+    req_nv = {"kernel_name": "gemm.fp4_gemm", "backend": "hip",
+              "inputs": [_raw(pa, "uint8"), _raw(pw.T, "uint8"), _raw(sba, "float8_e4m3fn"),
+                         _raw(sbw, "uint8")],
+              "params": {"fmt": "nvfp4", "global_a": float(ga), "global_b": float(gw),
+                         "out_dtype": "float32"}}
+    with TestClient(app) as c:
+        r = c.post("/api/v1/kernels/run", json=req)
+        r_nv = c.post("/api/v1/kernels/run", json=req_nv)
+    assert r.status_code == 200, r.text
+    assert r_nv.status_code == 200, r_nv.text
+    glob, elem = OG.rel_errors(_out(r.json()), OG.ref_mxfp4(qa, ea, qw, ew))
+    assert glob <= 1e-2 and elem <= 1e-2, (glob, elem)
+    glob, elem = OG.rel_errors(_out(r_nv.json()), OG.ref_nvfp4(pa, sba, ga, pw, sbw, gw))
+    assert glob <= 1e-2 and elem <= 1e-2, (glob, elem)
+
+
+def test_rest_prequantized_grouped_fp8():
+    """E4M3 codes for X and W with per-row / per-channel scale tensors,
+    posted as [X, B, offsets, scale_x, scale_w] (empty group included)."""
+    from fastapi.testclient import TestClient
+
+    from dsl_tool_amd.dispatcher.api import app
+    k, n = 256, 64
+    off = np.array([0, 20, 20, 57], np.int32)
+    x = _seeded((57, k), 915).float().numpy()
+    w = _seeded((3 * n, k), 916, 0.02).float().numpy()          # W [G*N, K]
+    qx, sx = OQ.quant_fp8_blockwise(x, 1, k)
+    qw, sw = OQ.quant_fp8_blockwise(w, 1, k)
+    b = qw.reshape(3, n, k).transpose(0, 2, 1)                 # B [G, K, N] codes
+    req = {"kernel_name": "gemm.grouped_gemm", "backend": "hip",
+           "inputs": [_raw(qx, "float8_e4m3fn"), _raw(b, "float8_e4m3fn"), _raw(off, "int32"),
+                      _raw(sx[:, 0], "float32"), _raw(sw.reshape(3, n), "float32")],
+           "params": {"out_dtype": "float32"}}
+    with TestClient(app) as c:
+        r = c.post("/api/v1/kernels/run", json=req)
+    assert r.status_code == 200, r.text
+    ref = OG.ref_grouped_fp8(qx, sx[:, 0], qw.reshape(3, n, k), sw.reshape(3, n), off)
+    glob, elem = OG.rel_errors(_out(r.json()), ref)
+    assert glob <= 1e-2 and elem <= 1e-2, (glob, elem)

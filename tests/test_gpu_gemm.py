@@ -446,3 +446,80 @@ def test_nvfp4_pipelined(m, n, k):
     c = G.fp4_gemm_packed(qa, sa, qw, sw, fmt="nvfp4", global_a=ga, global_w=gw)
     ref = OG.ref_nvfp4(np_u8(qa), np_u8(sa), np_f32(ga)[0], np_u8(qw), np_u8(sw), np_f32(gw)[0])
     assert_close(c, ref, what=f"nvfp4 pipelined {m}x{n}x{k}")
+
+
+# ------------------------------------ BASELINE config 1 and mid-size M --
+# Config 1 is the shape the reference quotes for its registered fp8_gemm
+# (triton/gemm/gemm_kernels.py:104-122): FP8 per-tensor, A [128, 4096]
+# ~N(0,1), W [4096, 4096] ~N(0, 0.02).  The neighbouring M cover the
+# boundary between the decode kernel (M <= 32) and the larger tiles.
+MID_SHAPES = [(128, 4096, 4096), (33, 4096, 4096), (64, 4096, 4096), (256, 4096, 4096),
+              (96, 1000, 2048), (200, 2056, 1024), (128, 512, 16384)]
+
+
+@pytest.mark.parametrize("m,n,k", MID_SHAPES)
+def test_fp8_per_tensor_config1_and_mid_m(m, n, k):
+    a = W.activations(1, m, k)
+    w = W.weights(1, n, k)
+    qa, sa = Q.quant_fp8_tensor(a.to(DEV))
+    qw, sw = Q.quant_fp8_tensor(w.to(DEV))
+    qa_ref, sa_ref = OQ.quant_fp8_per_tensor(_f32(a))
+    qw_ref, sw_ref = OQ.quant_fp8_per_tensor(_f32(w))
+    assert np.array_equal(np_u8(qa), qa_ref) and np.array_equal(np_u8(qw), qw_ref)
+    ref = OG.ref_fp8_per_tensor(qa_ref, sa_ref, qw_ref, sw_ref)
+    for out_dtype in (torch.bfloat16, torch.float32):
+        c = G.fp8_gemm_packed(qa, qw, sa, sw, out_dtype=out_dtype)
+        assert c.dtype == out_dtype
+        assert_close(c, ref, what=f"fp8 per-tensor {m}x{n}x{k} {out_dtype}")
+
+
+@pytest.mark.parametrize("mode", ["tensor", "block", "mxfp4"])
+def test_config1_shape_is_deterministic(mode):
+    """Two launches of the same problem give the same bytes (no order of
+    floating-point additions depends on scheduling)."""
+    m, n, k = 128, 4096, 4096
+    a, w = W.activations(1, m, k).to(DEV), W.weights(1, n, k).to(DEV)
+    if mode == "tensor":
+        qa, sa = Q.quant_fp8_tensor(a)
+        qw, sw = Q.quant_fp8_tensor(w)
+        run = lambda: G.fp8_gemm_packed(qa, qw, sa, sw, out_dtype=torch.float32)
+    elif mode == "block":
+        qa, sa = Q.quant_fp8_blocks(a, 1, 128)
+        qw, sw = Q.quant_fp8_blocks(w, 128, 128)
+        run = lambda: G.fp8_gemm_packed(qa, qw, sa, sw, block=True, out_dtype=torch.float32)
+    else:
+        qa, sa = Q.quant_mxfp4(a)
+        qw, sw = Q.quant_mxfp4(w)
+        run = lambda: G.fp4_gemm_packed(qa, sa, qw, sw, fmt="mxfp4", out_dtype=torch.float32)
+    c1 = run()
+    c2 = run()
+    torch.cuda.synchronize()
+    assert torch.equal(c1.view(torch.int32), c2.view(torch.int32))
+
+
+def test_misaligned_scales_with_small_workspace():
+    """MXFP4 with scale arrays one byte off 16-byte alignment leave the
+    persistent kernel for the register-staged one; a workspace too small for
+    split-K must then be left alone (one pass over K), not overrun."""
+    m, n, k = 2048, 2048, 4096
+    from dsl_tool_amd import _native as NN
+    a = W.randn_bf16((m, k), 331)
+    w = W.randn_bf16((n, k), 332, 0.02)
+    qa, ea = Q.quant_mxfp4(a.to(DEV))
+    qw, ew = Q.quant_mxfp4(w.to(DEV))
+    buf_a = torch.zeros(ea.numel() + 32, dtype=torch.uint8, device=DEV)
+    buf_w = torch.zeros(ew.numel() + 32, dtype=torch.uint8, device=DEV)
+    ea_mis = buf_a[1:1 + ea.numel()]
+    ew_mis = buf_w[1:1 + ew.numel()]
+    ea_mis.copy_(ea.reshape(-1))
+    ew_mis.copy_(ew.reshape(-1))
+    guard = torch.full((4096,), 7.0, dtype=torch.float32, device=DEV)
+    ws = guard[:64]                      # 256 bytes, far below an [M][N] fp32 sum
+    c = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    NN.call("dsl_fp4_gemm", NN.ptr(qa), NN.ptr(qw), NN.ptr(c), m, n, k, n, NN.OUT_BF16,
+            NN.FMT_MXFP4, NN.ptr(ea_mis), NN.ptr(ew_mis), None, None, NN.ptr(ws), 256,
+            NN.stream_of(c.device))
+    torch.cuda.synchronize()
+    assert torch.all(guard[64:] == 7.0), "the GEMM wrote past the workspace it was given"
+    ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
+    assert_close(c, ref, what="mxfp4 misaligned scales")

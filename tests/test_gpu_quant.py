@@ -245,3 +245,114 @@ def test_nvfp4_strided_input_matches():
     assert np_f32(sg)[0] == sg_ref
     assert np.array_equal(np_u8(sb), sb_ref)
     assert np.array_equal(np_u8(q), q_ref)
+
+
+# ------------------------------------------------------- fp32 / fp16 sources --
+# The reference quantizers read fp32 (cuda/gemm/fp8_gemm.cu:118-144,
+# cuda/gemm/fp4_gemm.cu:49-90).  fp32 sources are quantized from their own
+# values: codes of the IEEE quotient of the fp32 element by the fp32 scale.
+# The inputs sit one ulp either side of the E4M3 / E2M1 rounding midpoints,
+# and the amax is not a bf16 value, so rounding the source to bf16 first (or
+# dividing by a reciprocal) changes codes; each test checks that it would.
+
+def _near(vals: np.ndarray) -> np.ndarray:
+    """vals and their fp32 neighbours one ulp below and above."""
+    v = vals.astype(np.float32)
+    return np.concatenate([np.nextafter(v, np.float32(-np.inf)), v,
+                           np.nextafter(v, np.float32(np.inf))]).astype(np.float32)
+
+
+E4M3_MIDS = np.array([0.5 * (a + b) for a, b in
+                      zip(F.e4m3_decode(np.arange(0, 0x7E, dtype=np.uint8)),
+                          F.e4m3_decode(np.arange(1, 0x7F, dtype=np.uint8)))], np.float32)
+E2M1_MIDS = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], np.float32)
+
+
+def _fp32_rows(body: np.ndarray, cols: int, pin: float) -> np.ndarray:
+    """body laid out in rows of `cols` (zero padded), every row led by `pin`."""
+    per = cols - 1
+    n = -(-len(body) // per)
+    flat = np.zeros(n * per, np.float32)
+    flat[:len(body)] = body
+    return np.concatenate([np.full((n, 1), pin, np.float32), flat.reshape(n, per)], axis=1)
+
+
+def _signed(v: np.ndarray) -> np.ndarray:
+    return np.concatenate([v, -v]).astype(np.float32)
+
+
+def test_fp8_tensor_fp32_source_near_midpoints():
+    amax = np.float32(1.2345678)                 # not a bf16 value
+    s = np.float32(amax / np.float32(448.0))
+    x = _fp32_rows(_signed(_near((E4M3_MIDS[E4M3_MIDS < 448] * s).astype(np.float32))), 128, amax)
+    q, sc = Q.quant_fp8_tensor(torch.from_numpy(x).to(DEV))
+    q_ref, s_ref = OQ.quant_fp8_per_tensor(x)
+    assert np_f32(sc)[0] == s_ref
+    assert np.array_equal(np_u8(q), q_ref)
+    # the bf16-rounded source would encode differently
+    q_bf, _ = OQ.quant_fp8_per_tensor(torch.from_numpy(x).bfloat16().float().numpy())
+    assert not np.array_equal(q_bf, q_ref)
+
+
+@pytest.mark.parametrize("gr,gc", [(1, 128), (128, 128)])
+def test_fp8_blocks_fp32_source(gr, gc):
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((256, 384)) * 3).astype(np.float32)
+    x[::7, ::5] *= np.float32(1.0009765)        # mantissa bits bf16 does not hold
+    q, s = Q.quant_fp8_blocks(torch.from_numpy(x).to(DEV), gr, gc)
+    q_ref, s_ref = OQ.quant_fp8_blockwise(x, gr, gc)
+    assert np.array_equal(np_f32(s), s_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+    # strided fp32 view (the reference's B[K, N] orientation)
+    xt = torch.from_numpy(np.ascontiguousarray(x.T)).to(DEV).t()
+    q2, s2 = Q.quant_fp8_blocks(xt, gr, gc)
+    assert np.array_equal(np_f32(s2), s_ref) and np.array_equal(np_u8(q2), q_ref)
+
+
+def test_mxfp4_fp32_source_near_midpoints():
+    # blocks of 32 whose amax 5.5 * 2^k fixes the shared exponent k, the other
+    # 31 elements one ulp around the E2M1 midpoints of that exponent
+    rows = []
+    for k in (-3, 0, 4):
+        body = _signed(_near(E2M1_MIDS * np.float32(2.0 ** k)))
+        rows.append(_fp32_rows(body, 32, np.float32(5.5 * 2.0 ** k)))
+    x = np.concatenate(rows, axis=0)
+    x = np.concatenate([x, np.zeros((x.shape[0], 32), np.float32)], axis=1)   # zero blocks
+    q, e = Q.quant_mxfp4(torch.from_numpy(x).to(DEV))
+    q_ref, e_ref = OQ.quant_mxfp4(x)
+    assert np.array_equal(np_u8(e), e_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+    q_bf, _ = OQ.quant_mxfp4(torch.from_numpy(x).bfloat16().float().numpy())
+    assert not np.array_equal(q_bf, q_ref)
+
+
+def test_nvfp4_fp32_source_near_midpoints():
+    amax_t = np.float32(7.654321)                # global scale amax / 2688 from an fp32 amax
+    sg = np.float32(amax_t / np.float32(2688.0))
+    rows = []
+    for bmax in (np.float32(7.654321), np.float32(0.3141593), np.float32(2.7182817)):
+        sb = F.e4m3_decode(F.e4m3_encode(np.float32(np.float32(bmax / np.float32(6.0)) / sg)))
+        d = np.float32(np.float32(sb) * sg)
+        body = _signed(_near((E2M1_MIDS * d).astype(np.float32)))
+        body = body[np.abs(body) <= bmax]
+        rows.append(_fp32_rows(body, 16, bmax))
+    x = np.concatenate(rows, axis=0)
+    q, sbc, g = Q.quant_nvfp4(torch.from_numpy(x).to(DEV))
+    q_ref, sb_ref, g_ref = OQ.quant_nvfp4(x)
+    assert np_f32(g)[0] == g_ref
+    assert np.array_equal(np_u8(sbc), sb_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+    q_bf, _, _ = OQ.quant_nvfp4(torch.from_numpy(x).bfloat16().float().numpy())
+    assert not np.array_equal(q_bf, q_ref)
+
+
+def test_fp16_source_is_widened_exactly():
+    rng = np.random.default_rng(6)
+    x16 = torch.from_numpy((rng.standard_normal((64, 256)) * 5).astype(np.float16))
+    x32 = x16.float().numpy()
+    q, s = Q.quant_fp8_tensor(x16.to(DEV))
+    q_ref, s_ref = OQ.quant_fp8_per_tensor(x32)
+    assert np_f32(s)[0] == s_ref and np.array_equal(np_u8(q), q_ref)
+    q, e = Q.quant_mxfp4(x16.to(DEV))
+    q_ref, e_ref = OQ.quant_mxfp4(x32)
+    assert np.array_equal(np_u8(e), e_ref) and np.array_equal(np_u8(q), q_ref)

@@ -169,30 +169,39 @@ def test_grouped_gemm_argument_validation(lib):
 
 def test_quantizer_argument_validation(lib):
     fake = 1 << 20
-    rc = lib.dsl_quant_mxfp4(fake, 4, 48, 48, 1, fake, fake, None)
+    rc = lib.dsl_quant_mxfp4(fake, 4, 48, 48, 1, 0, fake, fake, None)
     assert rc == N.DSL_ERR_ARG and "multiple of 32" in _err(lib)
-    rc = lib.dsl_quant_nvfp4(fake, 4, 40, 40, 1, fake, fake, fake, fake, 1 << 20, None)
+    rc = lib.dsl_quant_nvfp4(fake, 4, 40, 40, 1, 0, fake, fake, fake, fake, 1 << 20, None)
     assert rc == N.DSL_ERR_ARG and "multiple of 16" in _err(lib)
-    rc = lib.dsl_quant_fp8_tensor(fake, 4, 64, 64, 1, fake, fake, fake, 4, None)
+    rc = lib.dsl_quant_fp8_tensor(fake, 4, 64, 64, 1, 0, fake, fake, fake, 4, None)
     assert rc == N.DSL_ERR_WORKSPACE
-    rc = lib.dsl_quant_fp8_blocks(fake, 4, 64, 64, 1, 0, 128, fake, fake, None)
+    rc = lib.dsl_quant_fp8_blocks(fake, 4, 64, 64, 1, 0, 0, 128, fake, fake, None)
     assert rc == N.DSL_ERR_ARG and "group" in _err(lib)
-    rc = lib.dsl_quant_fp8_blocks(fake + 1, 4, 64, 64, 1, 1, 128, fake, fake, None)
+    rc = lib.dsl_quant_fp8_blocks(fake + 1, 4, 64, 64, 1, 0, 1, 128, fake, fake, None)
     assert rc == N.DSL_ERR_ARG and "aligned" in _err(lib)
-    rc = lib.dsl_quant_fp8_blocks(fake, 4, 64, -3, 1, 1, 128, fake, fake, None)
+    rc = lib.dsl_quant_fp8_blocks(fake, 4, 64, -3, 1, 0, 1, 128, fake, fake, None)
     assert rc == N.DSL_ERR_ARG and "stride" in _err(lib)
     # an empty input is a successful no-op
-    assert lib.dsl_quant_mxfp4(None, 0, 64, 64, 1, None, None, None) == 0
+    assert lib.dsl_quant_mxfp4(None, 0, 64, 64, 1, 0, None, None, None) == 0
 
 
 def test_error_message_is_cleared_on_success(lib):
-    lib.dsl_quant_mxfp4(1 << 20, 4, 48, 48, 1, 1 << 20, 1 << 20, None)
+    lib.dsl_quant_mxfp4(1 << 20, 4, 48, 48, 1, 0, 1 << 20, 1 << 20, None)
     assert _err(lib)
-    assert lib.dsl_quant_mxfp4(None, 0, 64, 64, 1, None, None, None) == 0
+    assert lib.dsl_quant_mxfp4(None, 0, 64, 64, 1, 0, None, None, None) == 0
     assert _err(lib) == ""
 
 
 def test_python_wrappers_raise_dslerror(lib):
     with pytest.raises(N.DslError) as ei:
-        N.call("dsl_quant_mxfp4", 1 << 20, 4, 48, 48, 1, 1 << 20, 1 << 20, None)
+        N.call("dsl_quant_mxfp4", 1 << 20, 4, 48, 48, 1, 0, 1 << 20, 1 << 20, None)
     assert ei.value.status == N.DSL_ERR_ARG
+
+
+def test_quantizer_source_dtype_validation(lib):
+    fake = 1 << 20
+    rc = lib.dsl_quant_mxfp4(fake, 4, 64, 64, 1, 7, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "x_dtype" in _err(lib)
+    # fp32 sources must be 4-byte aligned
+    rc = lib.dsl_quant_fp8_blocks(fake + 2, 4, 64, 64, 1, N.IN_F32, 1, 128, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "aligned" in _err(lib)
