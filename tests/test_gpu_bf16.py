@@ -32,6 +32,8 @@ SHAPES = [
     (32, 7168, 1024),
     (16, 512, 1032),      # small M, other K: split K over a workspace
     (1, 256, 64),
+    (128, 4096, 2048),    # mid M (32 < M <= 256, K % 256 == 0): the mid-M kernel
+    (72, 1000, 512),
 ]
 
 

@@ -523,3 +523,29 @@ def test_misaligned_scales_with_small_workspace():
     assert torch.all(guard[64:] == 7.0), "the GEMM wrote past the workspace it was given"
     ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
     assert_close(c, ref, what="mxfp4 misaligned scales")
+
+
+# The mid-M kernel (32 < M <= 256) in its other modes: two W tiles per
+# workgroup (config-1-sized N) and one (small N), ragged M and N edges, and
+# M blocks whose last rows repeat the edge row.
+MID_MODE_SHAPES = [(128, 4096, 4096), (256, 7168, 4096), (40, 512, 2048), (97, 1000, 1024),
+                   (200, 2056, 3072)]
+
+
+@pytest.mark.parametrize("m,n,k", MID_MODE_SHAPES)
+@pytest.mark.parametrize("mode", ["block", "mxfp4"])
+def test_mid_m_block_and_mxfp4(m, n, k, mode):
+    w = W.randn_bf16((n, k), 152, 0.02)
+    if mode == "block":
+        a = W.activations(2, m, k, outliers=True)
+        qa, sa = Q.quant_fp8_blocks(a.to(DEV), 1, 128)
+        qw, sw = Q.quant_fp8_blocks(w.to(DEV), 128, 128)
+        ref = OG.ref_fp8_groupwise(np_u8(qa), np_f32(sa), np_u8(qw), np_f32(sw))
+        c = G.fp8_gemm_packed(qa, qw, sa, sw, block=True)
+    else:
+        a = W.randn_bf16((m, k), 151)
+        qa, ea = Q.quant_mxfp4(a.to(DEV))
+        qw, ew = Q.quant_mxfp4(w.to(DEV))
+        ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
+        c = G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4")
+    assert_close(c, ref, what=f"mid-M {mode} {m}x{n}x{k}")
