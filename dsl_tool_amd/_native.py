@@ -55,6 +55,7 @@ SIGNATURES = {
     "dsl_last_error": (ctypes.c_char_p, []),
     "dsl_abi_version": (_i32, []),
     "dsl_quant_fp8_tensor": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _sz, _vp]),
+    "dsl_quant_fp8_tensor_noalloc": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp]),
     "dsl_quant_fp8_blocks": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _i64, _i64, _vp, _vp, _vp]),
     "dsl_quant_mxfp4": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp]),
     "dsl_quant_nvfp4": (_i32, [_vp, _i64, _i64, _i64, _i64, _i32, _vp, _vp, _vp, _vp, _sz, _vp]),

@@ -109,6 +109,26 @@ int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols, int64_t sr, 
                     fn);
 }
 
+int dsl_quant_fp8_tensor_noalloc(const void *x, int64_t rows, int64_t cols, int64_t sr,
+                                 int64_t sc, int x_dtype, uint8_t *q, float *scale,
+                                 void *stream) {
+  const char *fn = "dsl_quant_fp8_tensor_noalloc";
+  int rc = check_input(fn, x, rows, cols, sr, sc, x_dtype);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return ok();
+  if ((rc = check_out(fn, q, "q"))) return rc;
+  if (!scale) return fail(DSL_ERR_ARG, "%s: scale is NULL", fn);
+  if (dsl_quant_workspace_bytes(rows, cols) > dsl::quant_scratch_bytes())
+    return fail(DSL_ERR_WORKSPACE, "%s: %zu bytes of amax partials exceed the %zu held by the library",
+                fn, dsl_quant_workspace_bytes(rows, cols), dsl::quant_scratch_bytes());
+  hipError_t e = hipSuccess;
+  float *partials = dsl::quant_scratch(&e);
+  if (!partials) return hip_status(e, fn);
+  return hip_status(dsl::launch_quant_fp8_tensor(x, x_dtype == DSL_IN_F32, rows, cols, sr, sc, q,
+                                                 scale, partials, static_cast<hipStream_t>(stream)),
+                    fn);
+}
+
 int dsl_quant_fp8_blocks(const void *x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
                          int x_dtype, int64_t gr, int64_t gc, uint8_t *q, float *scales,
                          void *stream) {

@@ -22,6 +22,10 @@ hipError_t launch_quant_mxfp4(const void *x, bool f32, int64_t rows, int64_t col
 hipError_t launch_quant_nvfp4(const void *x, bool f32, int64_t rows, int64_t cols, int64_t sr,
                               int64_t sc, uint8_t *q, uint8_t *e4m3s, float *gscale,
                               float *partial, hipStream_t st);
+// Device address of the library-held amax partials on the current device
+// (looked up once per device); nullptr and *err set on failure.
+float *quant_scratch(hipError_t *err);
+size_t quant_scratch_bytes();
 
 // ---------------------------------------------------------------- GEMMs --
 enum GemmMode { MODE_FP8_TENSOR = 0, MODE_FP8_BLOCK = 1, MODE_MXFP4 = 2, MODE_NVFP4 = 3, MODE_BF16 = 4 };

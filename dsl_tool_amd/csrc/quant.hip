@@ -22,6 +22,8 @@
 // the gfx950 converters and the corrected reciprocal quotient of common.h
 // (quot), which give the same codes; the strided path divides and encodes in
 // software.
+#include <mutex>
+
 #include "launch.h"
 #include "quant_core.h"
 
@@ -507,6 +509,42 @@ static hipError_t launch_amax_partials(const void *xv, bool f32, int64_t rows, i
     amax_partial_kernel<false, uint16_t><<<g, 256, 0, st>>>(x, rows, cols, sr, sc, partial);
   return hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// Library-held amax partials for the entry point that allocates nothing
+// (dsl_quant_fp8_tensor_noalloc).  One copy per GPU, for the life of the
+// process; pass 1 writes every partial that pass 2 reads, so nothing in it
+// has to start at zero.  Host code reaches it through the address that
+// hipGetSymbolAddress returns on each device, never through its name.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[kMaxPartials];
+
+float *quant_scratch(hipError_t *err) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static float *ptr[kMaxDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e == hipSuccess && (dev < 0 || dev >= kMaxDevices)) e = hipErrorInvalidDevice;
+  if (e != hipSuccess) {
+    *err = e;
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(mu);
+  if (!ptr[dev]) {
+    void *p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));   // with `dev` current
+    if (e != hipSuccess || !p) {
+      *err = e != hipSuccess ? e : hipErrorInvalidSymbol;
+      return nullptr;
+    }
+    ptr[dev] = static_cast<float *>(p);
+  }
+  *err = hipSuccess;
+  return ptr[dev];
+}
+
+size_t quant_scratch_bytes() { return sizeof(scratch); }
 
 hipError_t launch_quant_fp8_tensor(const void *xv, bool f32, int64_t rows, int64_t cols,
                                    int64_t sr, int64_t sc, uint8_t *q, float *scale,

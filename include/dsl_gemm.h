@@ -69,6 +69,19 @@ int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols,
                          uint8_t *q, float *scale,
                          void *workspace, size_t workspace_bytes, void *stream);
 
+/* dsl_quant_fp8_tensor without the workspace argument and without any
+ * allocation: the amax partials live in a library-held device array of
+ * 4 KB per GPU (1024 floats, kept until the process ends), which covers
+ * every size.  No counterpart in the reference; for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Results are identical to dsl_quant_fp8_tensor.
+ * Every call on one GPU uses that GPU's array, so calls that overlap on one
+ * GPU (different streams, threads or graph replays in flight together) race
+ * and must be serialized by the caller. */
+int dsl_quant_fp8_tensor_noalloc(const void *x, int64_t rows, int64_t cols,
+                                 int64_t stride_row, int64_t stride_col, int x_dtype,
+                                 uint8_t *q, float *scale, void *stream);
+
 /* Block-scaled E4M3 over group_rows x group_cols tiles (1x128 activations,
  * 128x128 weights, 1xC per-row / per-channel).  scales is
  * [ceil(R/group_rows)][ceil(C/group_cols)] fp32, each max(amax/448, 1e-12).

@@ -205,3 +205,14 @@ def test_quantizer_source_dtype_validation(lib):
     # fp32 sources must be 4-byte aligned
     rc = lib.dsl_quant_fp8_blocks(fake + 2, 4, 64, 64, 1, N.IN_F32, 1, 128, fake, fake, None)
     assert rc == N.DSL_ERR_ARG and "aligned" in _err(lib)
+
+
+def test_noalloc_quantizer_validation(lib):
+    """Argument checks of the allocation-free quantizer run before any HIP
+    call, so they are testable without a GPU."""
+    fake = 1 << 20
+    rc = lib.dsl_quant_fp8_tensor_noalloc(fake, 4, 64, 64, 1, 9, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "x_dtype" in _err(lib)
+    rc = lib.dsl_quant_fp8_tensor_noalloc(fake, 4, 64, 64, 1, N.IN_BF16, fake, None, None)
+    assert rc == N.DSL_ERR_ARG and "scale" in _err(lib)
+    assert lib.dsl_quant_fp8_tensor_noalloc(None, 0, 64, 64, 1, N.IN_BF16, None, None, None) == 0
