@@ -18,7 +18,9 @@ Cache cannot serve them, and are timed as a captured HIP graph of K launches
 so host launch latency does not enter the kernel time.
 
 ``cpu_baseline`` times the CPU oracle (dequantize -> fp32 torch matmul) on
-the headline workload, on the host's cores.
+the headline workload, on the host's cores, and in ``legs`` the reference's
+own tiled CPU path (restated) on BASELINE config 1 and config 5; it states
+the threads used, ``os.cpu_count()`` and the CPU model.
 
 ``roofline.traffic`` is the headline kernel's HBM bytes per launch from two
 ``rocprofv3 --pmc`` runs (FETCH_SIZE, then WRITE_SIZE) of
@@ -491,13 +493,48 @@ def profile_traffic(steps: int) -> int:
     return 0
 
 
-def cpu_baseline(sample_rows: int, min_seconds: float = 10.0):
-    """The oracle (dequantize -> fp32 CPU matmul -> bf16) on the headline
-    workload restricted to its first `sample_rows` activation rows, repeated
-    until at least `min_seconds` of CPU work have been timed (mean rate)."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
+def _repeat(fn, min_seconds: float):
+    """Run fn until at least min_seconds of it have been timed: (out, runs, seconds)."""
+    reps, dt, out = 0, 0.0, None
+    while reps == 0 or dt < min_seconds:
+        t0 = time.perf_counter()
+        out = fn()
+        dt += time.perf_counter() - t0
+        reps += 1
+    return out, reps, dt
+
+
+def cpu_baseline(sample_rows: int, min_seconds: float = 10.0, leg_seconds: float = 5.0):
+    """CPU paths timed on the host's cores, each repeated until enough CPU
+    work is timed (mean rate):
+
+    * the headline: the oracle (dequantize -> fp32 CPU matmul -> bf16) on
+      the M=4096 block-scaled workload restricted to its first `sample_rows`
+      activation rows (``value``);
+    * ``legs``: the reference's own CPU path restated tile for tile
+      (64x64x32 tiles, fp32 accumulation, tilelang/gemm/gemm_kernels.py:
+      96-113 and :116-133), on BASELINE config 1 in full and on a sample of
+      config 5's expert groups.
+
+    The tiled legs' operand codes come from the GPU quantizers (bit-exact
+    with the oracle's, tests/test_gpu_quant_fullsize.py) to keep the setup
+    short; only the CPU GEMMs are timed."""
     import numpy as np
     import torch
 
+    from dsl_tool_amd import quant as Q
     from dsl_tool_amd import workloads as W
     from oracle import gemm as OG
     from oracle import quant as OQ
@@ -507,18 +544,58 @@ def cpu_baseline(sample_rows: int, min_seconds: float = 10.0):
     w = W.weights(2, n, k).float().numpy()
     qa, sa = OQ.quant_fp8_blockwise(a, 1, 128)
     qw, sw = OQ.quant_fp8_blockwise(w, 128, 128)
-    reps, dt = 0, 0.0
-    while reps == 0 or dt < min_seconds:
-        t0 = time.perf_counter()
-        out = OG.ref_fp8_groupwise(qa, sa, qw, sw)
-        dt += time.perf_counter() - t0
-        reps += 1
+    out, reps, dt = _repeat(lambda: OG.ref_fp8_groupwise(qa, sa, qw, sw), min_seconds)
     assert np.isfinite(out).all()
-    return {"value": round(reps * 2.0 * m * n * k / dt / 1e12, 5), "unit": "TFLOP/s",
+    head = {"value": round(reps * 2.0 * m * n * k / dt / 1e12, 5), "unit": "TFLOP/s",
             "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"oracle ref_fp8_groupwise (numpy dequant + torch fp32 matmul) on rows "
                       f"0..{m - 1} of the M=4096 headline, full N={n} K={k}; {reps} runs, "
-                      f"{dt:.1f} s in total"}
+                      f"{dt:.1f} s in total",
+            "threads": torch.get_num_threads(), "cpu_count": os.cpu_count(),
+            "cpu_model": _cpu_model()}
+    del a, w, qa, qw, out
+
+    dev = torch.device("cuda:0")
+    legs = []
+    # config 1 in full: FP8 per-tensor, A [128, 4096], W [4096, 4096]
+    a1 = W.activations(1, 128, 4096).to(dev)
+    w1 = W.weights(1, 4096, 4096).to(dev)
+    qa1, sa1 = Q.quant_fp8_tensor(a1)
+    qw1, sw1 = Q.quant_fp8_tensor(w1)
+    qa1, qw1 = qa1.cpu().numpy(), qw1.cpu().numpy()
+    sa1, sw1 = float(sa1.cpu()[0]), float(sw1.cpu()[0])
+    _, reps, dt = _repeat(lambda: OG.tiled_fp8_gemm(qa1, qw1, sa1, sw1), leg_seconds)
+    legs.append({"value": round(reps * 2.0 * 128 * 4096 * 4096 / dt / 1e12, 6), "unit": "TFLOP/s",
+                 "ms_per_gemm": round(dt / reps * 1e3, 2), "kind": "port",
+                 "sample": f"tiled_fp8_gemm (64x64x32 tiles, the reference's fp8_gemm_tiled "
+                           f"restated) on BASELINE config 1 in full, M=128 N=4096 K=4096; "
+                           f"{reps} runs, {dt:.1f} s"})
+    del a1, w1
+    # config 5: grouped MoE, per-row / per-channel E4M3, a sample of the groups
+    x5, w5, off5, _ = W.moe_problem(5)
+    e5, n5, k5 = w5.shape
+    qx, sx = Q.quant_fp8_blocks(x5.to(dev), 1, k5)
+    qw5, sw5 = Q.quant_fp8_blocks(w5.reshape(e5 * n5, k5).to(dev), 1, k5)
+    qx, sx = qx.cpu().numpy(), sx.cpu().numpy()[:, 0]
+    qw5, sw5 = qw5.cpu().numpy().reshape(e5, n5, k5), sw5.cpu().numpy().reshape(e5, n5)
+    off = off5.numpy()
+    groups, rows = [], 0
+    for g in reversed(range(e5)):          # the smallest (last Zipf-rank) non-empty groups, >= 512 rows
+        cnt = int(off[g + 1] - off[g])
+        if cnt and rows < 512:
+            groups.append(g)
+            rows += cnt
+    groups.sort()
+    _, reps, dt = _repeat(lambda: OG.tiled_grouped_fp8_gemm(qx, sx, qw5, sw5, off, groups=groups),
+                          leg_seconds)
+    legs.append({"value": round(reps * 2.0 * rows * n5 * k5 / dt / 1e12, 6), "unit": "TFLOP/s",
+                 "ms_per_gemm": round(dt / reps * 1e3, 2), "kind": "port",
+                 "sample": f"tiled_grouped_fp8_gemm (64x64x32 tiles per group, the reference's "
+                           f"grouped_gemm_tiled restated) on config 5 groups {groups} "
+                           f"({rows} of {int(off[-1])} routed rows), N={n5} K={k5}; "
+                           f"{reps} runs, {dt:.1f} s"})
+    head["legs"] = legs
+    return head
 
 
 def main(argv=None):

@@ -168,6 +168,37 @@ def tiled_fp8_gemm(a_codes, w_codes, sa, sw, block_m=64, block_n=64, block_k=32)
     return c.numpy()
 
 
+def tiled_grouped_fp8_gemm(qx, sx, qw, sw, offsets, block_m=64, block_n=64, block_k=32,
+                           groups=None):
+    """The reference's grouped CPU path restated (tilelang/gemm/gemm_kernels.py:
+    116-133): per group, 64x64x32 tiles with fp32 accumulation over K tiles,
+    here over the variable-size groups of cuda/gemm/grouped_gemm.cu:26-32
+    (rows offsets[g]..offsets[g+1] of qx times W_g), each finished tile
+    scaled per row and per channel as (acc * sx[r]) * sw[g, n].
+    qx [T, K], qw [G, N, K] E4M3 codes, sx [T], sw [G, N]; `groups` limits
+    the work to those group indices (rows of other groups stay 0).
+    Returns fp32 [T, N]."""
+    x = torch.from_numpy(e4m3_decode(qx))
+    G, N, K = qw.shape
+    c = torch.zeros(x.shape[0], N, dtype=torch.float32)
+    sxt = torch.from_numpy(np.asarray(sx, np.float32))
+    swt = torch.from_numpy(np.asarray(sw, np.float32))
+    for g in (range(G) if groups is None else groups):
+        r0, r1 = int(offsets[g]), int(offsets[g + 1])
+        if r1 <= r0:
+            continue
+        w = torch.from_numpy(e4m3_decode(qw[g]))
+        for bm in range(r0, r1, block_m):
+            be = min(bm + block_m, r1)
+            for bn in range(0, N, block_n):
+                acc = torch.zeros(be - bm, min(block_n, N - bn))
+                for bk in range(0, K, block_k):
+                    acc += x[bm:be, bk:bk + block_k] @ w[bn:bn + block_n, bk:bk + block_k].T
+                c[bm:be, bn:bn + block_n] = ((acc * sxt[bm:be, None])
+                                             * swt[g, None, bn:bn + block_n])
+    return c.numpy()
+
+
 # ------------------------------ tolerance ---------------------------------
 
 def rel_errors(c: np.ndarray, r: np.ndarray):

@@ -213,6 +213,32 @@ def test_ref_grouped_kat(kat):
     assert np.allclose(y, kat["grp_y"], rtol=2 ** -8, atol=1e-30)
 
 
+def test_tiled_grouped_reference_cpu_path(kat):
+    """The grouped tiled restatement (64x64x32 tiles per group,
+    tilelang/gemm/gemm_kernels.py:116-133) against the float64 triple-loop
+    known answer, and against the dense grouped oracle on groups that span
+    several 64-row tiles, a ragged N and an empty group; restricting it to
+    some groups leaves the other rows at zero."""
+    y = OG.tiled_grouped_fp8_gemm(kat["grp_qx"], kat["grp_sx"], kat["grp_qw"], kat["grp_sw"],
+                                  kat["grp_off"])
+    assert np.allclose(y, kat["grp_y"], rtol=2 ** -8, atol=1e-30)
+    rng = np.random.default_rng(17)
+    counts = [70, 0, 130, 5]
+    off = np.concatenate([[0], np.cumsum(counts)]).astype(np.int32)
+    qx = F.e4m3_encode(rng.standard_normal((205, 96)).astype(np.float32))
+    qw = F.e4m3_encode(rng.standard_normal((4, 72, 96)).astype(np.float32))
+    sx = np.float32(rng.uniform(0.5, 2, 205))
+    sw = np.float32(rng.uniform(0.5, 2, (4, 72)))
+    tiled = OG.tiled_grouped_fp8_gemm(qx, sx, qw, sw, off)
+    dense = np.concatenate([
+        (F.e4m3_decode(qx[off[g]:off[g + 1]]).astype(np.float64)
+         @ F.e4m3_decode(qw[g]).astype(np.float64).T) * sx[off[g]:off[g + 1], None] * sw[g][None, :]
+        for g in range(4)])
+    assert np.allclose(tiled, dense, rtol=1e-5, atol=1e-6)
+    part = OG.tiled_grouped_fp8_gemm(qx, sx, qw, sw, off, groups=[2])
+    assert np.array_equal(part[70:200], tiled[70:200]) and not part[:70].any() and not part[200:].any()
+
+
 def test_groupwise_partial_form_equals_dequant_form():
     # sum_g sa[m,g] sb[n/128,g] sum_{k in g} a w  (cuda/gemm/fp8_gemm.cu:84-97)
     rng = np.random.default_rng(5)
