@@ -51,6 +51,9 @@ PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 HEADLINE = "fp8_block_m4096"
 MALL_BYTES = 256 << 20
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "fp8_block_m4096_traffic.txt")
+# algorithmic bytes of one headline GEMM: A and W codes, fp32 1x128 / 128x128
+# scales and the bf16 C, each once
+HEADLINE_BYTES = 4096 * 4096 + 7168 * 4096 + 4096 * 32 * 4 + 56 * 32 * 4 + 4096 * 7168 * 2
 COPY_BYTES = 256 << 20          # calibration copy for the HBM byte counters
 WARM_MS = 50.0                  # per-case warm-up time on the GPU before timing
 
@@ -178,16 +181,21 @@ def build_cases(names, dev):
         qw, sw = Q.quant_fp8_blocks(w.reshape(E * Nn, K).to(dev), 1, K)
         off = offsets.to(dev)
         y = torch.empty((T, Nn), dtype=torch.bfloat16, device=dev)
+        # the experts' weights (~190 MB) fit the 256 MB Infinity Cache: rotate
+        # copies (> 2 x 256 MB in all) so every launch reads them from HBM
+        rot = _rotations(qw.numel())
+        qws = [qw] + [qw.clone() for _ in range(rot - 1)]
 
         def launch(i, stream):
-            return L.dsl_grouped_fp8_gemm(qx.data_ptr(), qw.data_ptr(), y.data_ptr(),
+            return L.dsl_grouped_fp8_gemm(qx.data_ptr(), qws[i % rot].data_ptr(), y.data_ptr(),
                                           off.data_ptr(), E, T, Nn, K, Nn, N.OUT_BF16,
                                           sx.data_ptr(), sw.data_ptr(), stream)
         nonempty = int((counts > 0).sum())
         flops = 2.0 * T * Nn * K
         nbytes = T * K + nonempty * Nn * K + 4 * T + 4 * nonempty * Nn + 2 * T * Nn
-        return Case(name, flops, nbytes, PEAK_FP8_TFLOPS, "mfma", launch, 1,
-                    f"grouped fp8 MoE E={E} T={T} N={Nn} K={K} ({E - nonempty} empty)")
+        return Case(name, flops, nbytes, PEAK_FP8_TFLOPS, "mfma", launch, rot,
+                    f"grouped fp8 MoE E={E} T={T} N={Nn} K={K} ({E - nonempty} empty), "
+                    f"{rot} weight copies rotated")
 
     def quant_case(name, kind, r, k):
         """One quantize/pack pass over a bf16 [r, k] operand resident in HBM."""
@@ -493,6 +501,184 @@ def profile_traffic(steps: int) -> int:
     return 0
 
 
+# Kernels profiled with hardware counters: the headline, the north-star
+# targets (FP8 and MXFP4 8192^3, decode M=16), the grouped MoE GEMM and
+# BASELINE config 1.
+PROFILE_CASES = ["fp8_block_m4096", "fp8_tensor_8192", "mxfp4_8192", "grouped_moe",
+                 "fp8_block_m16", "mxfp4_m16", "fp8_tensor_cfg1"]
+PROFILE_PASSES = [
+    ["MfmaUtil", "GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_LDS",
+     "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_F8",
+     "SQ_INSTS_VALU_MFMA_MOPS_F6F4"],
+    ["FETCH_SIZE"],
+    ["WRITE_SIZE", "TCC_HIT_sum", "TCC_MISS_sum"],
+    ["TCP_TCC_READ_REQ_sum", "TCP_TCC_READ_REQ_LATENCY_sum"],
+]
+
+
+def profile_counters(steps: int) -> int:
+    """Workload for the ``rocprofv3 --pmc`` passes: the calibration copy,
+    then for each PROFILE_CASES entry `steps` launches bracketed by two
+    one-element fill kernels that mark where the case's dispatches begin and
+    end in the counter CSV."""
+    import torch
+
+    dev = torch.device("cuda:0")
+    src = torch.empty(COPY_BYTES, dtype=torch.uint8, device=dev).random_(0, 255)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    del src, dst
+    marker = torch.empty(1, dtype=torch.int64, device=dev)   # FillFunctor<long> dispatches
+    torch.cuda.synchronize(dev)
+    for i, nm in enumerate(PROFILE_CASES):
+        case = build_cases([nm], dev)[nm]
+        torch.cuda.synchronize(dev)
+        marker.fill_(i + 1)
+        s = torch.cuda.Stream(device=dev)
+        with torch.cuda.stream(s):
+            for j in range(steps):
+                rc = case.launch(j, s.cuda_stream)
+                if rc != 0:
+                    raise RuntimeError(f"{nm}: launch failed with status {rc}")
+        torch.cuda.synchronize(dev)
+        marker.fill_(-(i + 1))
+        torch.cuda.synchronize(dev)
+        log(f"profile-counters: {nm}, {steps} launches")
+        del case
+        torch.cuda.empty_cache()
+    return 0
+
+
+def _counter_rows(csv_dir: str):
+    """{dispatch id: (kernel name, {counter: value})} from a rocprofv3 csv dir."""
+    import csv
+    import glob
+
+    files = glob.glob(os.path.join(csv_dir, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise FileNotFoundError(f"no counter_collection.csv under {csv_dir}")
+    out = {}
+    for row in csv.DictReader(open(files[0])):
+        d = int(row["Dispatch_Id"])
+        name, vals = out.setdefault(d, (row["Kernel_Name"], {}))
+        vals[row["Counter_Name"]] = vals.get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    return out
+
+
+def summarize_counters(dirs, commands) -> int:
+    """Write profiles/<case>_counters.txt from the PROFILE_PASSES csv dirs:
+    per case, the mean over its launches (the first one dropped) of every
+    counter, with FETCH_SIZE / WRITE_SIZE scaled by what they read for the
+    256 MiB calibration copy."""
+    import statistics
+
+    per_case = {nm: {} for nm in PROFILE_CASES}
+    kname = {}
+    calib = {}
+    for d in dirs:
+        rows = _counter_rows(d)
+        ids = sorted(rows)
+        marks = [i for i in ids if "FillFunctor<long" in rows[i][0]]
+        # calibration: the three copies before the first marker
+        first = marks[0] if marks else ids[-1]
+        copies = [i for i in ids if i < first and "copy" in rows[i][0].lower()][:3]
+        for cn in ("FETCH_SIZE", "WRITE_SIZE"):
+            vals = [rows[i][1][cn] for i in copies if cn in rows[i][1]]
+            if vals:
+                calib[cn] = (COPY_BYTES / 1024.0) / statistics.mean(vals[1:] or vals)
+        for c, nm in enumerate(PROFILE_CASES):
+            if 2 * c + 1 >= len(marks):
+                break
+            lo, hi = marks[2 * c], marks[2 * c + 1]
+            disp = [i for i in ids if lo < i < hi]
+            if not disp:
+                continue
+            main = max(set(rows[i][0] for i in disp), key=lambda k: sum(rows[i][0] == k for i in disp))
+            kname[nm] = main
+            use = [i for i in disp if rows[i][0] == main]
+            use = use[1:] or use
+            for cn in rows[use[0]][1]:
+                per_case[nm][cn] = statistics.mean(rows[i][1][cn] for i in use)
+    os.makedirs(os.path.join(ROOT, "profiles"), exist_ok=True)
+    for nm, vals in per_case.items():
+        if not vals:
+            continue
+        lines = [f"# {nm}: hardware counters of its main kernel, mean per launch",
+                 f"# kernel: {kname.get(nm, '?')}",
+                 "# commands (run from the repository root on one MI355X):"]
+        lines += [f"#   {c}" for c in commands]
+        lines.append("")
+        for cn in sorted(vals):
+            lines.append(f"{cn}: {vals[cn]:.6g}")
+        fs, ws = vals.get("FETCH_SIZE"), vals.get("WRITE_SIZE")
+        if fs is not None and "FETCH_SIZE" in calib:
+            lines.append(f"hbm_read_bytes (FETCH_SIZE x {calib['FETCH_SIZE']:.4f}, the factor that "
+                         f"maps a {COPY_BYTES >> 20} MiB device copy to its true bytes): "
+                         f"{fs * 1024 * calib['FETCH_SIZE']:.4g}")
+        if ws is not None and "WRITE_SIZE" in calib:
+            lines.append(f"hbm_write_bytes (WRITE_SIZE x {calib['WRITE_SIZE']:.4f}): "
+                         f"{ws * 1024 * calib['WRITE_SIZE']:.4g}")
+        if "TCC_HIT_sum" in vals and "TCC_MISS_sum" in vals:
+            tot = vals["TCC_HIT_sum"] + vals["TCC_MISS_sum"]
+            lines.append(f"l2_hit_rate: {vals['TCC_HIT_sum'] / tot:.4f}" if tot else "l2_hit_rate: -")
+        if vals.get("TCP_TCC_READ_REQ_sum"):
+            lines.append(f"l1_to_l2_read_latency_cycles (LATENCY_sum / READ_REQ_sum): "
+                         f"{vals.get('TCP_TCC_READ_REQ_LATENCY_sum', 0) / vals['TCP_TCC_READ_REQ_sum']:.1f}")
+        if vals.get("SQ_LDS_IDX_ACTIVE"):
+            lines.append(f"lds_bank_conflict_ratio (SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE): "
+                         f"{vals.get('SQ_LDS_BANK_CONFLICT', 0) / vals['SQ_LDS_IDX_ACTIVE']:.4f}")
+        with open(os.path.join(ROOT, "profiles", f"{nm}_counters.txt"), "w") as f:
+            f.write("\n".join(lines) + "\n")
+        log(f"wrote profiles/{nm}_counters.txt")
+        if nm == HEADLINE and fs is not None and ws is not None and "FETCH_SIZE" in calib \
+                and "WRITE_SIZE" in calib:
+            rd = fs * 1024 * calib["FETCH_SIZE"]
+            wr = ws * 1024 * calib["WRITE_SIZE"]
+            t = ["# HBM traffic of the headline kernel (fp8 block-scaled M=4096 N=7168 K=4096)",
+                 f"# kernel: {kname.get(nm, '?')}",
+                 f"# from the FETCH_SIZE / WRITE_SIZE passes of profiles/{nm}_counters.txt "
+                 "(commands there)",
+                 f"hbm_read_bytes: {rd:.0f}", f"hbm_write_bytes: {wr:.0f}",
+                 f"algorithmic_bytes: {HEADLINE_BYTES}",
+                 f"measured_over_algorithmic: {(rd + wr) / HEADLINE_BYTES:.3f}",
+                 f"traffic_bytes_per_launch: {int(round(rd + wr))}"]
+            with open(TRAFFIC_FILE, "w") as f:
+                f.write("\n".join(t) + "\n")
+            log(f"wrote {os.path.relpath(TRAFFIC_FILE, ROOT)}")
+    return 0
+
+
+def summarize_trace(trace_dir: str, bench_log: str, command: str) -> int:
+    """Write profiles/bench_default_kernel_trace.txt from a rocprofv3
+    --kernel-trace --stats csv dir of a bench run and that run's stderr."""
+    import csv
+    import glob
+    import re
+
+    stats = glob.glob(os.path.join(trace_dir, "**", "*kernel_stats.csv"), recursive=True)
+    rows = list(csv.DictReader(open(stats[0])))
+    out = ["# rocprofv3 kernel-trace summary: default bench run (all cases)",
+           f"# command (run from the repository root on one MI355X): {command}",
+           "", "Per-kernel durations (microseconds, every launch of the run incl. warm-up):", "",
+           f"{'kernel':100s} {'calls':>6s} {'avg':>9s} {'min':>9s} {'max':>9s}"]
+    for r in rows:
+        n = r["Name"]
+        if "dsl::" not in n:
+            continue
+        n = re.sub(r"\(.*\)$", "", n.replace("void ", ""))[:100]
+        out.append(f"{n:100s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
+                   f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f}")
+    text = open(bench_log).read()
+    cases = re.findall(r"\[bench\] case (\S+): \{'us': ([\d.]+), 'tflops': ([\d.]+).*?'what': '([^']*)'", text)
+    out += ["", "bench.py timings of every case in the same (profiled) run, microseconds:"]
+    out += [f"    {c[0]:26s} {float(c[1]):9.2f}   {c[3]}" for c in cases]
+    with open(os.path.join(ROOT, "profiles", "bench_default_kernel_trace.txt"), "w") as f:
+        f.write("\n".join(out) + "\n")
+    log("wrote profiles/bench_default_kernel_trace.txt")
+    return 0
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -609,7 +795,19 @@ def main(argv=None):
     ap.add_argument("--cpu-rows", type=int, default=4096)
     ap.add_argument("--profile-traffic", action="store_true",
                     help="run only the copy calibration and headline launches for rocprofv3 --pmc")
+    ap.add_argument("--profile-counters", action="store_true",
+                    help="run the copy calibration and launches of each counter-profiled case")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="CSV_DIR",
+                    help="write profiles/<case>_counters.txt from rocprofv3 --pmc output dirs")
+    ap.add_argument("--commands", nargs="*", default=[],
+                    help="with --summarize-counters: the commands to record in the summaries")
+    ap.add_argument("--summarize-trace", nargs=2, metavar=("TRACE_DIR", "BENCH_LOG"),
+                    help="write profiles/bench_default_kernel_trace.txt from a kernel-trace run")
     args = ap.parse_args(argv)
+    if args.summarize_counters:
+        return summarize_counters(args.summarize_counters, args.commands)
+    if args.summarize_trace:
+        return summarize_trace(*args.summarize_trace, " ".join(args.commands))
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the quantized GEMM "
               "path has no multi-GPU component in this build", file=sys.stderr)
@@ -625,6 +823,8 @@ def main(argv=None):
     N.lib()
     if args.profile_traffic:
         return profile_traffic(args.steps)
+    if args.profile_counters:
+        return profile_counters(args.steps)
 
     extra = ALL_CASES[1:] if args.cases == "all" else (
         [] if args.cases == "none" else [c for c in args.cases.split(",") if c and c != HEADLINE])
