@@ -1,0 +1,396 @@
+// Streaming quantized GEMMs for gfx950 at skinny and mid M (M <= 256):
+// C[M,N] = A[M,K] . W[N,K]^T, FP8 per-tensor, FP8 1x128/128x128 block,
+// MXFP4 and bf16, one launch, deterministic.  BASELINE config 1 (M=128,
+// N=K=4096) and the decode shapes (M=16) run here.
+//
+// At these shapes the work per W byte is small (M flops per byte) and the
+// output has too few large tiles to fill 256 CUs, so the kernel is laid out
+// for streaming W once with every CU busy:
+//   * a workgroup owns BM = 16*TMA activation rows and BN = 16*TN W rows of
+//     C over all of K, TN chosen so that about a CU's worth of workgroups
+//     cover C (the per-CU traffic (BM + BN) x K is then near its least);
+//   * its four waves split that range into contiguous runs of CHUNK-byte
+//     chunks.  For each chunk a wave streams its TN W tiles and then its TMA
+//     activation tiles (16 rows x CHUNK bytes each, one direct-to-LDS load
+//     per 1 KB) through NR private LDS regions, NR-1 items in flight behind
+//     the one being consumed.  W tiles go into registers; each activation
+//     tile is multiplied against them as it is read.  A wave waits for its
+//     own loads only (no barrier until the final reduction);
+//   * the waves' partial tiles are summed through LDS in a fixed order and
+//     laid out row-major in LDS for 16-byte stores;
+//   * one launch, no workspace, no atomics: the same bytes on every run;
+//   * the M blocks of one W slice are launched 8 apart (same XCD, about the
+//     same time), so the second reader finds the slice in that XCD's L2; W
+//     loads carry the non-temporal hint, activations stay cached.
+//
+// MFMA: v_mfma_scale_f32_16x16x128_f8f6f4 (bf16: two v_mfma_f32_16x16x32_bf16),
+// activation tile in the first operand: output register i of lane l is
+// C[4*(l/16) + i][l%16], rows from the activation tile, columns from the W
+// tile.  FP8 / bf16: lane group g holds 16-byte chunks g and g+4 of each
+// 128-byte step; MXFP4: 512-element superblocks whose step j gives lane
+// group g the 32-element block 4g+j (one u32 of 4 E8M0 bytes per lane and
+// superblock, op_sel j picks the byte).  A and W share the order, so the
+// sum is unchanged.  FP8 block: each 128-byte step is one 128-K group,
+// folded as acc += part * (sa[m][grp] * sb[n/128][grp]), the group-partial
+// form of cuda/gemm/fp8_gemm.cu:84-97.
+// LDS rows are CHUNK bytes; row r's 16-byte chunk c sits in slot c ^ r
+// (r < 16), so the 16 lanes that read one logical chunk of 16 rows hit
+// distinct bank groups.
+#include <cstdlib>
+
+#include "stream_core.h"
+
+namespace dsl {
+
+template <int MODE_, int TMA_, int TN_, int CHUNK_, int NR_>
+struct StreamCfg {
+  static constexpr int MODE = MODE_;
+  static constexpr int TMA = TMA_, TN = TN_;         // 16-row activation / W tiles
+  static constexpr int BM = 16 * TMA, BN = 16 * TN;
+  static constexpr int NW = 4, NT = NW * 64;         // waves split K
+  static constexpr bool MX = MODE == MODE_MXFP4;
+  static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;
+  static constexpr int CHUNK = CHUNK_;               // bytes of one row per item
+  static constexpr int STEPS = CHUNK / 128;          // 128-byte MFMA steps (FP8 block: groups)
+  static constexpr int SBK = CHUNK / 256;            // MXFP4 512-element superblocks
+  static constexpr int SPR = CHUNK / 16;             // 16-byte slots per row
+  static constexpr int RPD = 1024 / CHUNK;           // rows per direct load
+  static constexpr int DATA_DMA = 16 / RPD;          // direct loads per 16-row item
+  // scale bytes per row per chunk: E8M0 per 32 elements, fp32 per 128-K group
+  static constexpr int SROW = MX ? CHUNK / 16 : (BLOCK ? 4 * STEPS : 0);
+  static constexpr bool SC16 = SROW >= 16;           // scales move 16 (else 4) bytes per lane
+  static constexpr int AUX = SROW ? (SC16 ? 1024 : 256) : 0;
+  static constexpr int DPI = DATA_DMA + (AUX ? 1 : 0);   // direct loads per item
+  static constexpr int REGION = 16 * CHUNK + AUX;
+  static constexpr int NR = NR_;                     // regions per wave
+  static constexpr int P = TN + TMA;                 // items per chunk: W tiles, then A tiles
+  static constexpr int RING = NW * NR * REGION;
+  static constexpr int RED = NW * TN * TMA * 64 * 16;   // the waves' partial tiles
+  static constexpr int TLD = BN + 4;                 // row pitch (floats) of the summed tile
+  static constexpr int TILE = BM * TLD * 4;
+  static constexpr int LDS = RING > RED + TILE ? RING : RED + TILE;
+  static constexpr int CPT = BM * BN / NT;           // output columns per thread
+  static_assert(CHUNK == 256 || CHUNK == 512, "chunk bytes");
+  static_assert(!MX || CHUNK >= 256, "whole MXFP4 superblocks");
+  static_assert(LDS <= 160 * 1024, "LDS budget");
+  static_assert(NR >= 2 && (NR - 1) * DPI < 64, "vmcnt range");
+  static_assert(CPT >= 1 && BN % CPT == 0, "epilogue mapping");
+};
+
+template <class Cfg>
+struct StreamRegs {
+  v8i wf[Cfg::TN][Cfg::STEPS];      // FP8 / bf16 W fragments of the current chunk
+  v4i wq[Cfg::TN][Cfg::SBK][4];     // MXFP4 W fragments (16 bytes per step)
+  int ws[Cfg::TN][Cfg::SBK];        // MXFP4 W E8M0 words
+  float sb[Cfg::STEPS];             // FP8 block: weight scales of the chunk's groups
+  v4f acc[Cfg::TN][Cfg::TMA];
+};
+
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) {
+  constexpr int TMA = Cfg::TMA, TN = Cfg::TN, NW = Cfg::NW, P = Cfg::P, DPI = Cfg::DPI;
+  constexpr int NR = Cfg::NR, CHUNK = Cfg::CHUNK, SROW = Cfg::SROW;
+  __shared__ __align__(16) uint8_t lds[Cfg::LDS];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, g = lane >> 4;
+  // workgroup -> (M block, N block); the M blocks of one W slice are 8 apart
+  const int nmb = (p.M + Cfg::BM - 1) / Cfg::BM;
+  const int nnb = (p.N + Cfg::BN - 1) / Cfg::BN;
+  const int local = blockIdx.x >> 3;
+  const int mblk = local % nmb, nblk = (local / nmb) * 8 + (blockIdx.x & 7);
+  if (nblk >= nnb) return;                   // whole workgroup: no barrier reached
+  const int m0 = mblk * Cfg::BM, n0 = nblk * Cfg::BN;
+  const int nchunks = p.Kb / CHUNK;
+  const int c_begin = nchunks * wave / NW, c_end = nchunks * (wave + 1) / NW;
+  const int nitems = (c_end - c_begin) * P;
+  uint8_t *my = lds + wave * NR * Cfg::REGION;
+  const uint32_t R0 = dec::lds_addr(my);
+  const int nkg = p.K / 128;                 // FP8 block: scale groups per row
+  const int64_t sld = p.K / 32;              // MXFP4: E8M0 bytes per row
+
+  // item it: chunk c_begin + it / P; kind it % P (< TN: W tile, else
+  // activation tile kind - TN); region it % NR
+  auto issue = [&](int it) {
+    const int ch = c_begin + it / P, kind = it % P;
+    const uint32_t dst = R0 + (uint32_t)((it % NR) * Cfg::REGION);
+    const int64_t kb0 = (int64_t)ch * CHUNK;
+    const bool isW = kind < TN;
+    const int rbase = isW ? n0 + kind * 16 : m0 + (kind - TN) * 16;
+    const int rlim = isW ? p.N - 1 : p.M - 1;
+    const uint8_t *src = isW ? p.b : p.a;
+    const int sub = lane / Cfg::SPR, slot = lane % Cfg::SPR;
+#pragma unroll
+    for (int j = 0; j < Cfg::DATA_DMA; ++j) {  // rows RPD*j + sub
+      const int r = Cfg::RPD * j + sub;
+      const int row = min(rbase + r, rlim);    // rows past the edge re-read the last row
+      const uint8_t *s = src + (int64_t)row * p.Kb + kb0 + ((slot ^ r) << 4);
+      if (isW) dec::dma16_nt(s, dst + j * 1024);
+      else dec::dma16(s, dst + j * 1024);
+    }
+    if constexpr (Cfg::AUX) {
+      // the item's scales, row r at aux + r*SROW: 16-byte parts (lanes past
+      // 16 rows repeat) or, with 8 bytes per row, 4-byte words
+      constexpr int PARTS = Cfg::SC16 ? SROW / 16 : SROW / 4;
+      const int sr = (lane / PARTS) & 15, part = lane % PARTS;
+      const int row = isW ? (Cfg::BLOCK ? n0 : min(rbase + sr, rlim)) : min(rbase + sr, rlim);
+      const uint8_t *sc;
+      if constexpr (Cfg::MX) {
+        sc = static_cast<const uint8_t *>(isW ? p.sb : p.sa) + row * sld + kb0 / 16;
+      } else {   // fp32 group scales of the chunk: sa[row][.], sb[n0/128][.]
+        sc = reinterpret_cast<const uint8_t *>(
+            isW ? static_cast<const float *>(p.sb) + (int64_t)(row / 128) * nkg
+                : static_cast<const float *>(p.sa) + (int64_t)row * nkg) +
+             (int64_t)ch * Cfg::STEPS * 4;
+      }
+      if constexpr (Cfg::SC16) dec::dma16(sc + part * 16, dst + 16 * CHUNK);
+      else dec::dma4(sc + part * 4, dst + 16 * CHUNK);
+    }
+  };
+
+  StreamRegs<Cfg> st;
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+#pragma unroll
+    for (int a = 0; a < TMA; ++a) st.acc[t][a] = (v4f){0.f, 0.f, 0.f, 0.f};
+
+  auto chunk16 = [&](const uint8_t *base, int c) {      // row r16's logical chunk c
+    return *reinterpret_cast<const v4i *>(base + r16 * CHUNK + ((c ^ r16) << 4));
+  };
+
+  auto consume = [&](auto kind_tag, const uint8_t *base) {
+    constexpr int KIND = decltype(kind_tag)::value;
+    const uint8_t *aux = base + 16 * CHUNK;
+    if constexpr (KIND < TN) {                  // W tile -> registers
+      if constexpr (Cfg::MX) {
+#pragma unroll
+        for (int b = 0; b < Cfg::SBK; ++b) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) st.wq[KIND][b][j] = chunk16(base, b * 16 + 4 * g + j);
+          st.ws[KIND][b] = *reinterpret_cast<const int *>(aux + r16 * SROW + b * 16 + g * 4);
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < Cfg::STEPS; ++s) {
+          const v4i lo = chunk16(base, s * 8 + g), hi = chunk16(base, s * 8 + g + 4);
+          st.wf[KIND][s] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        }
+        if constexpr (Cfg::BLOCK) {
+#pragma unroll
+          for (int s = 0; s < Cfg::STEPS; ++s) st.sb[s] = reinterpret_cast<const float *>(aux)[s];
+        }
+      }
+    } else {                                    // activation tile x the W tiles
+      constexpr int A = KIND - TN;
+      if constexpr (Cfg::MX) {
+#pragma unroll
+        for (int b = 0; b < Cfg::SBK; ++b) {
+          const int asv = *reinterpret_cast<const int *>(aux + r16 * SROW + b * 16 + g * 4);
+          v4i ad[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) ad[j] = chunk16(base, b * 16 + 4 * g + j);
+#pragma unroll
+          for (int t = 0; t < TN; ++t) {
+            st.acc[t][A] = mfma_mx<0>(ad[0], st.wq[t][b][0], st.acc[t][A], asv, st.ws[t][b]);
+            st.acc[t][A] = mfma_mx<1>(ad[1], st.wq[t][b][1], st.acc[t][A], asv, st.ws[t][b]);
+            st.acc[t][A] = mfma_mx<2>(ad[2], st.wq[t][b][2], st.acc[t][A], asv, st.ws[t][b]);
+            st.acc[t][A] = mfma_mx<3>(ad[3], st.wq[t][b][3], st.acc[t][A], asv, st.ws[t][b]);
+          }
+        }
+      } else {
+        float sa[4][Cfg::STEPS];                // FP8 block: rows 4g+i, the chunk's groups
+        if constexpr (Cfg::BLOCK) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int s = 0; s < Cfg::STEPS; ++s)
+              sa[i][s] = reinterpret_cast<const float *>(aux + (4 * g + i) * SROW)[s];
+        }
+#pragma unroll
+        for (int s = 0; s < Cfg::STEPS; ++s) {
+          const v4i lo = chunk16(base, s * 8 + g), hi = chunk16(base, s * 8 + g + 4);
+          const v8i af = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+          for (int t = 0; t < TN; ++t) {
+            if constexpr (Cfg::BLOCK) {
+              const v4f zero = {0.f, 0.f, 0.f, 0.f};
+              const v4f part = mfma_fp8(af, st.wf[t][s], zero);
+              const v4f sc = (v4f){sa[0][s], sa[1][s], sa[2][s], sa[3][s]} * st.sb[s];
+              st.acc[t][A] = part * sc + st.acc[t][A];
+            } else if constexpr (Cfg::MODE == MODE_BF16) {
+              st.acc[t][A] = mfma_bf16(af, st.wf[t][s], st.acc[t][A]);
+            } else {
+              st.acc[t][A] = mfma_fp8(af, st.wf[t][s], st.acc[t][A]);
+            }
+          }
+        }
+      }
+    }
+  };
+
+  // wait until at most `after` items (issued after the current one) are
+  // outstanding: the current item has landed
+  auto wait_item = [&](int after) {
+    if (after >= NR - 1) {
+      dec::wait_vm<(NR - 1) * DPI>();
+    } else {
+      dec::static_for<0, NR - 1>([&](auto q) {
+        if (after == decltype(q)::value) dec::wait_vm<decltype(q)::value * DPI>();
+      });
+    }
+  };
+
+#pragma unroll
+  for (int i = 0; i < NR - 1; ++i)
+    if (i < nitems) issue(i);
+  for (int base_it = 0; base_it < nitems; base_it += P) {
+    auto step = [&](auto kind_tag) {
+      constexpr int K = decltype(kind_tag)::value;
+      const int it = base_it + K;
+      // the region of item it-1 is free (its reads returned): refill it
+      if (it + NR - 1 < nitems) issue(it + NR - 1);
+      wait_item(nitems - 1 - it);
+      consume(kind_tag, my + (it % NR) * Cfg::REGION);
+      dec::wait_lds();
+    };
+    dec::static_for<0, P>(step);
+  }
+
+  // ---- sum the waves' partial tiles (wave order 0..3) into a row-major
+  // tile T [BM][TLD] in LDS
+  __syncthreads();                              // every wave is done with its regions
+  float *red = reinterpret_cast<float *>(lds);  // [NW][TN][TMA][64 lanes][4]
+  float *T = reinterpret_cast<float *>(lds + Cfg::RED);
+#pragma unroll
+  for (int t = 0; t < TN; ++t)
+#pragma unroll
+    for (int a = 0; a < TMA; ++a)
+      *reinterpret_cast<v4f *>(red + (((wave * TN + t) * TMA + a) * 64 + lane) * 4) = st.acc[t][a];
+  __syncthreads();
+  for (int sl = threadIdx.x; sl < TN * TMA * 64; sl += Cfg::NT) {
+    const int combo = sl >> 6, ln = sl & 63;   // combo = t * TMA + a
+    v4f v = *reinterpret_cast<const v4f *>(red + (combo * 64 + ln) * 4);
+#pragma unroll
+    for (int w = 1; w < NW; ++w)
+      v += *reinterpret_cast<const v4f *>(red + ((w * TN * TMA + combo) * 64 + ln) * 4);
+    const int t = combo / TMA, a = combo % TMA;
+    const int col = t * 16 + (ln & 15), row0 = a * 16 + 4 * (ln >> 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) T[(row0 + i) * Cfg::TLD + col] = v[i];
+  }
+  __syncthreads();
+
+  constexpr int CPT = Cfg::CPT, GPR = Cfg::BN / CPT;
+  const int lrow = threadIdx.x / GPR, lcol = (threadIdx.x % GPR) * CPT;
+  float v[CPT];
+#pragma unroll
+  for (int c = 0; c < CPT; ++c) v[c] = T[lrow * Cfg::TLD + lcol + c];
+
+  const int row = m0 + lrow, col0 = n0 + lcol;
+  if (row >= p.M) return;
+  if constexpr (Cfg::MODE == MODE_FP8_TENSOR) {
+    const float s1 = *p.ga, s2 = *p.gb;
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) v[c] = (v[c] * s1) * s2;
+  }
+  if (p.out_f32) {
+    float *dst = static_cast<float *>(p.c) + (int64_t)row * p.ldc + col0;
+    if (CPT % 4 == 0 && col0 + CPT <= p.N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+#pragma unroll
+      for (int c = 0; c + 3 < CPT; c += 4)
+        *reinterpret_cast<v4f *>(dst + c) = (v4f){v[c], v[c + 1], v[c + 2], v[c + 3]};
+    } else {
+      for (int c = 0; c < CPT && col0 + c < p.N; ++c) dst[c] = v[c];
+    }
+  } else {
+    uint16_t *dst = static_cast<uint16_t *>(p.c) + (int64_t)row * p.ldc + col0;
+    if (CPT % 8 == 0 && col0 + CPT <= p.N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+#pragma unroll
+      for (int c = 0; c + 7 < CPT; c += 8)
+        *reinterpret_cast<uint4 *>(dst + c) =
+            make_uint4(pack_bf16x2(v[c], v[c + 1]), pack_bf16x2(v[c + 2], v[c + 3]),
+                       pack_bf16x2(v[c + 4], v[c + 5]), pack_bf16x2(v[c + 6], v[c + 7]));
+    } else if (CPT == 4 && col0 + 4 <= p.N && (reinterpret_cast<uintptr_t>(dst) & 7) == 0) {
+      *reinterpret_cast<uint2 *>(dst) = make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+    } else {
+      for (int c = 0; c < CPT && col0 + c < p.N; ++c) dst[c] = f32_to_bf16(v[c]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------- plans --
+namespace {
+
+struct StreamPlan {
+  int tma, tn;
+};
+
+// Activation tiles by M (16, 32 or 64 rows per workgroup; 256-byte chunks
+// for the skinny ones, 512-byte chunks otherwise), and the most W tiles
+// per workgroup (4, 2, 1) that still leave >= 192 workgroups: fewer but
+// larger workgroups read A and W fewer times (measured at M = 96..256), as
+// long as they cover most CUs.  DSL_GEMM_STREAM_TN overrides it (tuning).
+StreamPlan plan_for(int mode, int M, int N) {
+  StreamPlan pl;
+  pl.tma = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  const int64_t nmb = (M + 16 * pl.tma - 1) / (16 * pl.tma);
+  pl.tn = 1;
+  for (int tn = 4; tn >= 2; tn /= 2)
+    if (nmb * ((N + 16 * tn - 1) / (16 * tn)) >= 192) {
+      pl.tn = tn;
+      break;
+    }
+  const char *e = getenv("DSL_GEMM_STREAM_TN");
+  if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && !e[1]) pl.tn = e[0] - '0';
+  if (pl.tn == 4 && mode == MODE_FP8_BLOCK && pl.tma == 4) pl.tn = 2;   // register budget
+  return pl;
+}
+
+template <int MODE, int TMA, int TN, int CHUNK>
+hipError_t launch_cfg(const GemmArgs &p, hipStream_t st) {
+  using Cfg = StreamCfg<MODE, TMA, TN, CHUNK, 4>;
+  const int nmb = (p.M + Cfg::BM - 1) / Cfg::BM;
+  const int nnb = (p.N + Cfg::BN - 1) / Cfg::BN;
+  const int grid = 8 * nmb * ((nnb + 7) / 8);
+  gemm_stream_kernel<Cfg><<<grid, Cfg::NT, 0, st>>>(p);
+  return hipGetLastError();
+}
+
+template <int MODE, int TMA, int CHUNK>
+hipError_t launch_tn(const GemmArgs &p, int tn, hipStream_t st) {
+  if (tn == 1) return launch_cfg<MODE, TMA, 1, CHUNK>(p, st);
+  if (tn == 4) return launch_cfg<MODE, TMA, 4, CHUNK>(p, st);
+  return launch_cfg<MODE, TMA, 2, CHUNK>(p, st);
+}
+
+template <int MODE>
+hipError_t launch_mode(const GemmArgs &p, const StreamPlan &pl, hipStream_t st) {
+  if (pl.tma == 1) return launch_tn<MODE, 1, 256>(p, pl.tn, st);
+  if (pl.tma == 2) return launch_tn<MODE, 2, 256>(p, pl.tn, st);
+  return launch_tn<MODE, 4, 512>(p, pl.tn, st);
+}
+
+}  // namespace
+
+bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
+  if (M < 1 || M > 256 || N < 1) return false;
+  const int chunk = M <= 32 ? 256 : 512;
+  if (Kb % chunk != 0) return false;
+  if (mode == MODE_FP8_TENSOR || mode == MODE_BF16) return true;
+  // block scales and E8M0 rows move by 16-byte direct loads (K % 512)
+  if (mode == MODE_FP8_BLOCK || mode == MODE_MXFP4) return scales16 && K % 512 == 0;
+  return false;
+}
+
+hipError_t launch_gemm_stream(int mode, const GemmArgs &p, hipStream_t st) {
+  const StreamPlan pl = plan_for(mode, p.M, p.N);
+  switch (mode) {
+    case MODE_FP8_TENSOR: return launch_mode<MODE_FP8_TENSOR>(p, pl, st);
+    case MODE_FP8_BLOCK: return launch_mode<MODE_FP8_BLOCK>(p, pl, st);
+    case MODE_MXFP4: return launch_mode<MODE_MXFP4>(p, pl, st);
+    case MODE_BF16: return launch_mode<MODE_BF16>(p, pl, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace dsl

@@ -188,12 +188,14 @@ static bool env_off(const char *name) {
 // scales are aligned; with misaligned scales the launch may fall back to
 // the register-staged kernels, split-K only if a workspace was passed.
 //   DSL_GEMM_DECODE = 0/off    never use the skinny-M kernel
-//   DSL_GEMM_MID    = 0/off    never use the mid-M kernel
+//   DSL_GEMM_STREAM = 0/off    never use the streaming kernel (M <= 256)
+//   DSL_GEMM_SKINNY = stream   2 <= M <= 16 on the streaming kernel too
+//                              (default: the skinny-M decode kernel there)
 //   DSL_GEMM_PIPE   = 0/off    never use the LDS-DMA pipelined kernels
 //   DSL_GEMM_PIPE   = 1..9     force that pipelined variant for large problems
 //   DSL_GEMM_PERSIST = 0/off   use the per-tile pipelined kernels instead of
 //                              the persistent one for large problems
-enum { PATH_DECODE = 0, PATH_PIPE = 1, PATH_TILED = 2, PATH_PERSIST = 3, PATH_MID = 4 };
+enum { PATH_DECODE = 0, PATH_PIPE = 1, PATH_TILED = 2, PATH_PERSIST = 3, PATH_STREAM = 4 };
 struct Route {
   int path;
   int variant;    // PATH_PIPE variant
@@ -202,7 +204,9 @@ struct Route {
 
 static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc16) {
   static const bool decode_on = !env_off("DSL_GEMM_DECODE");
-  static const bool mid_on = !env_off("DSL_GEMM_MID");
+  static const bool stream_on = !env_off("DSL_GEMM_STREAM");
+  const char *skinny = getenv("DSL_GEMM_SKINNY");      // read per launch (tests switch it)
+  const bool skinny_stream = skinny && strcmp(skinny, "stream") == 0;
   static const bool persist_on = !env_off("DSL_GEMM_PERSIST");
   static const int pipe_forced = [] {
     if (env_off("DSL_GEMM_PIPE")) return -2;
@@ -210,12 +214,17 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
     return (e && e[0] >= '1' && e[0] <= '9' && !e[1]) ? e[0] - '0' : -1;
   }();
   Route r{PATH_TILED, -1, plan_for(M, N, Kb)};
-  if (decode_on && decode_supported(mode, M, K, Kb, sc4, sc16)) {
+  const bool streamable = stream_on && stream_supported(mode, M, N, K, Kb, sc16);
+  // the decode kernel holds M <= 16 rows of A in registers and was the
+  // faster one there (M = 16: 7.8 against 8.1 us); the streaming kernel
+  // wins at M = 1 (11.7 against 13.5) and 17..32 (8.7 against 10.9)
+  const bool prefer_stream = skinny_stream || M == 1 || M > 16;
+  if (decode_on && !(prefer_stream && streamable) && decode_supported(mode, M, K, Kb, sc4, sc16)) {
     r.path = PATH_DECODE;
     return r;
   }
-  if (mid_on && mid_supported(mode, M, N, K, Kb, sc16)) {
-    r.path = PATH_MID;
+  if (streamable) {
+    r.path = PATH_STREAM;
     return r;
   }
   if (mode == MODE_BF16) {   // persistent kernel or the register-staged tiles
@@ -263,7 +272,7 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
   if (p.accumulate) r.path = PATH_TILED;   // only the register-staged kernels add into C
   p.ksplit = 1;
   if (r.path == PATH_DECODE) return launch_gemm_decode(mode, p, st);
-  if (r.path == PATH_MID) return launch_gemm_mid(mode, p, st);
+  if (r.path == PATH_STREAM) return launch_gemm_stream(mode, p, st);
   if (r.path == PATH_PIPE) return launch_gemm_pipe(mode, p, r.variant, st);
   if (r.path == PATH_PERSIST) return launch_gemm_persist(mode, p, st);
   const Plan pl = r.tiled;

@@ -71,11 +71,11 @@ hipError_t launch_gemm_persist(int mode, const GemmArgs &p, hipStream_t st);
 bool decode_supported(int mode, int M, int K, int Kb, bool scales4, bool scales16);
 hipError_t launch_gemm_decode(int mode, const GemmArgs &p, hipStream_t st);
 
-// Mid-M kernel, one launch, no workspace, deterministic (32 < M <= 256,
-// Kb % 512 == 0): FP8_TENSOR and BF16; FP8_BLOCK and MXFP4 with 16-byte
-// aligned scales (Kb % 512 == 0 gives K % 512 / K % 1024 for them).
-bool mid_supported(int mode, int M, int N, int K, int Kb, bool scales16);
-hipError_t launch_gemm_mid(int mode, const GemmArgs &p, hipStream_t st);
+// Streaming kernel for M <= 256 (gemm_stream.hip), one launch, no
+// workspace, deterministic: FP8_TENSOR and BF16; FP8_BLOCK and MXFP4 with
+// 16-byte aligned scales and K % 512 == 0; Kb % 256 (M <= 32) or % 512.
+bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16);
+hipError_t launch_gemm_stream(int mode, const GemmArgs &p, hipStream_t st);
 
 // Picks a kernel variant for the shape and launches it (plus the split-K
 // zero-fill / finalize kernels when ksplit > 1).

@@ -24,7 +24,13 @@ DSL_DEV void dma16(const void *src, uint32_t lds) {
                "s"(lds)
                : "memory", "m0");
 }
-// Same, with the non-temporal hint (streamed data, read once).
+// 4 bytes per lane from `src` into LDS at m0 + lane*4.
+DSL_DEV void dma4(const void *src, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" ::"v"(src),
+               "s"(lds)
+               : "memory", "m0");
+}
+// Same as dma16, with the non-temporal hint (streamed data, read once).
 DSL_DEV void dma16_nt(const void *src, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" ::"v"(src),
                "s"(lds)

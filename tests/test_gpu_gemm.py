@@ -561,3 +561,48 @@ def test_mid_m_block_and_mxfp4(m, n, k, mode):
         ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
         c = G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4")
     assert_close(c, ref, what=f"mid-M {mode} {m}x{n}x{k}")
+
+
+# The streaming kernel on every tile shape: 16-, 32- and 64-row activation
+# blocks with one, two or four 16-row W tiles per workgroup, ragged M and N.
+# DSL_GEMM_SKINNY=stream moves 2 <= M <= 16 onto it as well, and
+# DSL_GEMM_STREAM_TN forces the W tiles (both read at every launch).
+STREAM_SHAPES = [("tensor", 16, 7168, 4096), ("block", 16, 7168, 4096), ("mxfp4", 16, 8192, 8192),
+                 ("tensor", 1, 1000, 4096), ("block", 32, 1040, 2048), ("mxfp4", 7, 2048, 1024),
+                 ("tensor", 96, 7168, 4096), ("block", 200, 1000, 2048), ("mxfp4", 256, 2056, 3072),
+                 ("bf16", 24, 1000, 2048)]
+
+
+@pytest.mark.parametrize("tn", ["1", "2", "4"])
+@pytest.mark.parametrize("mode,m,n,k", STREAM_SHAPES)
+def test_stream_kernel_tile_shapes(mode, m, n, k, tn, monkeypatch):
+    monkeypatch.setenv("DSL_GEMM_SKINNY", "stream")
+    monkeypatch.setenv("DSL_GEMM_STREAM_TN", tn)
+    w = W.randn_bf16((n, k), 162, 0.02)
+    if mode == "block":
+        a = W.activations(2, m, k, outliers=True)
+        qa, sa = Q.quant_fp8_blocks(a.to(DEV), 1, 128)
+        qw, sw = Q.quant_fp8_blocks(w.to(DEV), 128, 128)
+        ref = OG.ref_fp8_groupwise(np_u8(qa), np_f32(sa), np_u8(qw), np_f32(sw))
+        run = lambda: G.fp8_gemm_packed(qa, qw, sa, sw, block=True, out_dtype=torch.float32)
+    elif mode == "tensor":
+        a = W.randn_bf16((m, k), 161)
+        qa, sa = Q.quant_fp8_tensor(a.to(DEV))
+        qw, sw = Q.quant_fp8_tensor(w.to(DEV))
+        ref = OG.ref_fp8_per_tensor(np_u8(qa), np_f32(sa)[0], np_u8(qw), np_f32(sw)[0])
+        run = lambda: G.fp8_gemm_packed(qa, qw, sa, sw, out_dtype=torch.float32)
+    elif mode == "mxfp4":
+        a = W.randn_bf16((m, k), 163)
+        qa, ea = Q.quant_mxfp4(a.to(DEV))
+        qw, ew = Q.quant_mxfp4(w.to(DEV))
+        ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
+        run = lambda: G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4", out_dtype=torch.float32)
+    else:
+        a = W.randn_bf16((m, k), 164)
+        ref = OG.ref_bf16(a.float().numpy(), w.float().numpy()).astype(np.float32)
+        run = lambda: G.bf16_gemm(a.to(DEV), w.to(DEV).t())
+    c1 = run()
+    c2 = run()
+    torch.cuda.synchronize()
+    assert_close(c1, ref, what=f"stream {mode} {m}x{n}x{k} tn={tn}")
+    assert torch.equal(c1.view(torch.int32), c2.view(torch.int32)), "not reproducible"
