@@ -15,7 +15,7 @@
 
 namespace dsl {
 
-constexpr int kRouteChunk = 1024;     // assignments per block in the count/scatter passes
+constexpr int kRouteChunk = 256;      // assignments per block in the count/scatter passes
 
 // Pass 1: per-block expert histograms, counts[b][e].
 __global__ __launch_bounds__(256) void moe_count_kernel(const int32_t *__restrict__ ids, int n,
@@ -32,55 +32,58 @@ __global__ __launch_bounds__(256) void moe_count_kernel(const int32_t *__restric
   for (int e = threadIdx.x; e < E; e += 256) counts[(int64_t)blockIdx.x * E + e] = hist[e];
 }
 
-// Pass 2 (one block): offsets[e] = rows of experts < e; counts[b][e] is
-// replaced by the first sorted row of block b's expert-e assignments.  The
-// count matrix is staged in LDS when it fits (all loads in flight at once);
-// otherwise it is walked in global memory.
-constexpr int kScanLds = 12288;        // ints of the count matrix held in LDS
-
+// Pass 2 (one block of 16 x 64 threads): offsets[e] = rows of experts < e;
+// counts[b][e] is replaced by the first sorted row of block b's expert-e
+// assignments.  Experts go in runs of 64; thread (part, l) owns expert
+// e0 + l over a contiguous range of blocks, so the column sums, the prefix
+// over the 16 ranges, the wave scan over the 64 experts and the rewrite
+// are each a few steps deep however many blocks there are.
 __global__ __launch_bounds__(1024) void moe_scan_kernel(int32_t *__restrict__ counts, int nb, int E,
                                                        int32_t *__restrict__ offsets) {
-  __shared__ int tot[kMaxGroups];
-  __shared__ int part[1024];
-  __shared__ int cm[kScanLds];
-  const int total_c = nb * E;
-  const bool in_lds = total_c <= kScanLds;
-  if (in_lds) {
-    for (int i = threadIdx.x; i < total_c; i += 1024) cm[i] = counts[i];
-    __syncthreads();
-  }
-  auto cnt = [&](int b, int e) { return in_lds ? cm[b * E + e] : counts[(int64_t)b * E + e]; };
-  for (int e = threadIdx.x; e < E; e += 1024) {
+  constexpr int PARTS = 16;
+  __shared__ int psum[PARTS][64];      // a range's count of each expert, then its prefix
+  __shared__ int first[64];            // first sorted row of each expert of the run
+  const int l = threadIdx.x & 63, part = threadIdx.x >> 6;
+  const int bpp = (nb + PARTS - 1) / PARTS;
+  const int b0 = part * bpp, b1 = min(nb, b0 + bpp);
+  int carry = 0;                       // wave 0: rows of the experts of earlier runs
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + l;
     int s = 0;
-    for (int b = 0; b < nb; ++b) s += cnt(b, e);
-    tot[e] = s;
-  }
-  __syncthreads();
-  // exclusive scan of tot over experts: each thread sums a contiguous run
-  const int per = (E + 1023) / 1024;
-  const int e0 = threadIdx.x * per, e1 = min(E, e0 + per);
-  int local = 0;
-  for (int e = e0; e < e1; ++e) local += tot[e];
-  part[threadIdx.x] = local;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const int v = threadIdx.x >= off ? part[threadIdx.x - off] : 0;
+    if (e < E)
+      for (int b = b0; b < b1; ++b) s += counts[(int64_t)b * E + e];
+    psum[part][l] = s;
     __syncthreads();
-    part[threadIdx.x] += v;
-    __syncthreads();
-  }
-  int run = part[threadIdx.x] - local;     // rows before expert e0
-  for (int e = e0; e < e1; ++e) {
-    offsets[e] = run;
-    int r = run;
-    for (int b = 0; b < nb; ++b) {
-      const int c = cnt(b, e);
-      counts[(int64_t)b * E + e] = r;
-      r += c;
+    if (part == 0) {
+      // exclusive prefix over the ranges, then over the experts (one wave)
+      int tot = 0;
+      for (int q = 0; q < PARTS; ++q) {
+        const int c = psum[q][l];
+        psum[q][l] = tot;
+        tot += c;
+      }
+      int incl = tot;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d, 64);
+        incl += l >= d ? v : 0;
+      }
+      first[l] = carry + incl - tot;
+      if (e < E) offsets[e] = first[l];
+      carry += __shfl(incl, 63, 64);
     }
-    run += tot[e];
+    __syncthreads();
+    if (e < E) {
+      int r = first[l] + psum[part][l];
+      for (int b = b0; b < b1; ++b) {
+        const int c = counts[(int64_t)b * E + e];
+        counts[(int64_t)b * E + e] = r;
+        r += c;
+      }
+    }
+    __syncthreads();                   // first[] and psum are rewritten by the next run
   }
-  if (threadIdx.x == 1023) offsets[E] = part[1023];
+  if (threadIdx.x == 0) offsets[E] = carry;
 }
 
 // Pass 3: stable scatter, one wave per chunk.  The wave walks its chunk 64
