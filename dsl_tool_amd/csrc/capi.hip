@@ -461,9 +461,17 @@ int dsl_lora_gemm(const void *x, const void *w, const void *a_t, const void *b_t
   uint16_t *t2 = reinterpret_cast<uint16_t *>(base + pl.t32 + pl.ws);
   uint16_t *b2 = reinterpret_cast<uint16_t *>(base + pl.t32 + pl.ws + pl.t2);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  hipError_t e = dsl::launch_gemm(dsl::MODE_BF16, bf16_args(x, a_t, t32, m, lr, k, lr, false, gws, pl.ws), st);
+  // T = X A^T.  With at most 256 adapter columns it is computed as
+  // T^T = A^T X^T: the adapter rows are then the skinny M of the streaming
+  // (or decode) kernel, which reads X once in one launch; otherwise (and
+  // when K does not suit those kernels) T comes from the register-staged
+  // tiles over the workspace.
+  const bool tt = lr <= 256 && dsl::stream_supported(dsl::MODE_BF16, (int)lr, (int)m, (int)k,
+                                                     (int)(2 * k), true);
+  hipError_t e = tt ? dsl::launch_gemm(dsl::MODE_BF16, bf16_args(a_t, x, t32, lr, m, k, m, false, nullptr, 0), st)
+                    : dsl::launch_gemm(dsl::MODE_BF16, bf16_args(x, a_t, t32, m, lr, k, lr, false, gws, pl.ws), st);
   if (e == hipSuccess)
-    e = dsl::launch_lora_split(t32, (int)m, (int)lr, (int)pl.ld2, (int)rank, scales, t2, st);
+    e = dsl::launch_lora_split(t32, (int)m, (int)lr, (int)pl.ld2, (int)rank, tt, scales, t2, st);
   if (e == hipSuccess) e = dsl::launch_lora_dup(static_cast<const uint16_t *>(b_t), (int)n, (int)lr,
                                                 (int)pl.ld2, b2, st);
   if (e != hipSuccess) return hip_status(e, fn);

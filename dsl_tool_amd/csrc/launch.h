@@ -137,9 +137,10 @@ hipError_t launch_moe_combine(const uint16_t *y, int rows_y, int64_t ldy, int n,
                               int out_f32, hipStream_t st);
 
 // -------------------------------------------------------------- LoRA --
-// t32 [M][LR] fp32 -> t2 [M][ld2] bf16: cols [0, LR) hi = bf16(t * s),
-// [LR, 2 LR) lo = bf16(t * s - hi), the rest 0; s = scales[col / rank].
-hipError_t launch_lora_split(const float *t32, int M, int LR, int ld2, int rank,
+// t32 [M][LR] fp32 (tt: its transpose [LR][M]) -> t2 [M][ld2] bf16:
+// cols [0, LR) hi = bf16(t * s), [LR, 2 LR) lo = bf16(t * s - hi), the rest
+// 0; s = scales[col / rank].
+hipError_t launch_lora_split(const float *t32, int M, int LR, int ld2, int rank, bool tt,
                              const float *scales, uint16_t *t2, hipStream_t st);
 // bt [N][LR] -> b2 [N][ld2] = bt | bt | 0.
 hipError_t launch_lora_dup(const uint16_t *bt, int N, int LR, int ld2, uint16_t *b2,

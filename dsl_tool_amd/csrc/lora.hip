@@ -2,7 +2,9 @@
 // path (reference: lora_fused_gemm_kernel, cuda/gemm/grouped_gemm.cu:106-140,
 // Y = X @ W + sum_l scale_l * X @ A_l @ B_l in fp32).
 //
-// T = X A^T for all adapters at once (A^T = [L*R][K], fp32), then T*s is
+// T = X A^T for all adapters at once (A^T = [L*R][K], fp32; computed as
+// T^T = A^T X^T on the skinny-M kernels when L*R <= 256, which read X once
+// in one launch), then T*s is
 // split into bf16 hi + lo (hi + lo carries 16 mantissa bits of T*s, so the
 // low-rank term loses almost nothing to the bf16 MFMA).  The adapter term is
 // then a K extension of the base GEMM: Y = [X | hi | lo] [W | B^T | B^T]^T,
@@ -14,9 +16,10 @@
 
 namespace dsl {
 
-// t32 [M][LR] -> t2 [M][ld2]: cols [0, LR) hi, [LR, 2 LR) lo, the rest 0.
+// t32 [M][LR] (or [LR][M] with tt) -> t2 [M][ld2]: cols [0, LR) hi,
+// [LR, 2 LR) lo, the rest 0.
 __global__ __launch_bounds__(256) void lora_split_kernel(const float *__restrict__ t32, int M,
-                                                         int LR, int ld2, int rank,
+                                                         int LR, int ld2, int rank, bool tt,
                                                          const float *__restrict__ scales,
                                                          uint16_t *__restrict__ t2) {
   const int64_t n = (int64_t)M * ld2;
@@ -27,7 +30,7 @@ __global__ __launch_bounds__(256) void lora_split_kernel(const float *__restrict
     uint16_t o = 0;
     if (col < 2 * LR) {
       const int c = col < LR ? col : col - LR;
-      const float v = t32[r * LR + c] * scales[c / rank];
+      const float v = (tt ? t32[(int64_t)c * M + r] : t32[r * LR + c]) * scales[c / rank];
       const uint16_t h = f32_to_bf16(v);
       o = col < LR ? h : f32_to_bf16(v - bf16_to_f32(h));
     }
@@ -53,10 +56,11 @@ static unsigned grid_of(int64_t n) {
   return (unsigned)(g < 1 ? 1 : (g > 8192 ? 8192 : g));
 }
 
-hipError_t launch_lora_split(const float *t32, int M, int LR, int ld2, int rank,
+hipError_t launch_lora_split(const float *t32, int M, int LR, int ld2, int rank, bool tt,
                              const float *scales, uint16_t *t2, hipStream_t st) {
   if (M == 0) return hipSuccess;
-  lora_split_kernel<<<grid_of((int64_t)M * ld2), 256, 0, st>>>(t32, M, LR, ld2, rank, scales, t2);
+  lora_split_kernel<<<grid_of((int64_t)M * ld2), 256, 0, st>>>(t32, M, LR, ld2, rank, tt, scales,
+                                                               t2);
   return hipGetLastError();
 }
 
