@@ -28,11 +28,12 @@ SHAPES = [
     (2048, 2048, 1024),   # register-staged 256x256 tiles
     (300, 520, 264),      # ragged M / N, K % 64 != 0
     (513, 257, 136),
-    (16, 2048, 4096),     # small M: the decode kernel (K % 512 == 0)
-    (32, 7168, 1024),
+    (16, 2048, 4096),     # 2 <= M <= 16: the decode kernel
+    (12, 7168, 1024),
+    (32, 7168, 1024),     # 17 <= M <= 256: the streaming kernel
     (16, 512, 1032),      # small M, other K: split K over a workspace
     (1, 256, 64),
-    (128, 4096, 2048),    # mid M (32 < M <= 256, K % 256 == 0): the mid-M kernel
+    (128, 4096, 2048),
     (72, 1000, 512),
 ]
 

@@ -345,8 +345,12 @@ def test_fp8_mfma_accumulation_bound():
 
 
 # ------------------------------------------------ skinny-M decode kernel --
+# The decode kernel serves 2 <= M <= 16 (32 W rows per workgroup; ragged N
+# such as 5000, 6200 and 7184 leave a partial last workgroup), the streaming
+# kernel M = 1 and 17..32.
 DECODE_SHAPES = [(1, 1000, 4096), (7, 2048, 1024), (16, 7168, 4096), (32, 1040, 2048),
-                 (17, 48, 8192), (16, 7184, 12288), (5, 16, 3072)]
+                 (17, 48, 8192), (16, 7184, 12288), (5, 16, 3072), (16, 5000, 2048),
+                 (9, 6200, 1024)]
 
 
 @pytest.mark.parametrize("m,n,k", DECODE_SHAPES)
@@ -372,7 +376,7 @@ def test_fp8_block_decode(m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k", [(1, 1000, 4096), (7, 2048, 1024), (16, 8192, 8192),
-                                   (32, 1040, 2048)])
+                                   (32, 1040, 2048), (16, 5000, 2048), (9, 6200, 1024)])
 def test_mxfp4_decode(m, n, k):
     a = W.randn_bf16((m, k), 321)
     w = W.randn_bf16((n, k), 322, 0.02)
