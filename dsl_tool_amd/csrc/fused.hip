@@ -36,20 +36,6 @@ DSL_DEV float sigmoid_fast(float g) {
   return __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-DSL_DEV void load_w8(const void *w, bool f32, int c, bool ok, float *f) {
-  if (!ok) {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = 0.f;
-  } else if (f32) {
-    const float4 a = reinterpret_cast<const float4 *>(w)[2 * c];
-    const float4 b = reinterpret_cast<const float4 *>(w)[2 * c + 1];
-    f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
-    f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
-  } else {
-    unpack8(reinterpret_cast<const uint4 *>(w)[c], f);
-  }
-}
-
 // Quantize 8 bf16-valued floats of chunk c of a row (team of TL lanes per
 // group: FP8 1x128 -> 16 chunks per group, MXFP4 -> 4) and store codes and,
 // from the team's first lane, the group scale.
@@ -84,7 +70,7 @@ DSL_DEV void store_y(const FusedArgs &p, int row, int c, const float *y) {
 // RMSNorm: one workgroup per row, thread t holding chunks t + 256 j in
 // registers (the sum of squares needs the whole row before any output).
 // A group's 16 (FP8) or 4 (MXFP4) chunks are consecutive threads of one wave.
-template <int QF, int CPL>
+template <int QF, int CPL, bool WF32>
 __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const FusedArgs p) {
   __shared__ float sh[4];
   const int row = blockIdx.x;
@@ -96,6 +82,17 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const FusedArgs p) {
   for (int j = 0; j < CPL; ++j) {
     const int c = tid + 256 * j;
     xa[j] = c < nch ? reinterpret_cast<const uint4 *>(xr)[c] : make_uint4(0, 0, 0, 0);
+  }
+  // the weights are loaded with the row (packed), so their latency hides
+  // behind the row's instead of following the sum-of-squares barrier
+  uint4 wa[CPL][WF32 ? 2 : 1];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = tid + 256 * j;
+#pragma unroll
+    for (int h = 0; h < (WF32 ? 2 : 1); ++h)
+      wa[j][h] = c < nch ? reinterpret_cast<const uint4 *>(p.w)[(WF32 ? 2 : 1) * c + h]
+                         : make_uint4(0, 0, 0, 0);
   }
   float ss = 0.f;
 #pragma unroll
@@ -116,7 +113,15 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const FusedArgs p) {
     const bool ok = c < nch;
     float y[8], w[8];
     unpack8(xa[j], y);
-    load_w8(p.w, p.w_f32, c, ok, w);
+    if constexpr (WF32) {
+      const uint4 a = wa[j][0], b = wa[j][WF32 ? 1 : 0];
+      w[0] = __uint_as_float(a.x); w[1] = __uint_as_float(a.y);
+      w[2] = __uint_as_float(a.z); w[3] = __uint_as_float(a.w);
+      w[4] = __uint_as_float(b.x); w[5] = __uint_as_float(b.y);
+      w[6] = __uint_as_float(b.z); w[7] = __uint_as_float(b.w);
+    } else {
+      unpack8(wa[j][0], w);
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) y[e] = round_bf16((y[e] * rinv) * w[e]);
     if (p.y && ok) store_y(p, row, c, y);
@@ -199,15 +204,21 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const FusedArgs p, ui
   }
 }
 
-template <int QF>
-static void launch_rmsnorm(const FusedArgs &p, hipStream_t st) {
+template <int QF, bool WF32>
+static void launch_rmsnorm_w(const FusedArgs &p, hipStream_t st) {
   const int per = (p.cols / 8 + 255) / 256;
   const unsigned grid = (unsigned)p.rows;
-  if (per <= 1) rmsnorm_quant_kernel<QF, 1><<<grid, 256, 0, st>>>(p);
-  else if (per <= 2) rmsnorm_quant_kernel<QF, 2><<<grid, 256, 0, st>>>(p);
-  else if (per <= 4) rmsnorm_quant_kernel<QF, 4><<<grid, 256, 0, st>>>(p);
-  else if (per <= 8) rmsnorm_quant_kernel<QF, 8><<<grid, 256, 0, st>>>(p);
-  else rmsnorm_quant_kernel<QF, 16><<<grid, 256, 0, st>>>(p);
+  if (per <= 1) rmsnorm_quant_kernel<QF, 1, WF32><<<grid, 256, 0, st>>>(p);
+  else if (per <= 2) rmsnorm_quant_kernel<QF, 2, WF32><<<grid, 256, 0, st>>>(p);
+  else if (per <= 4) rmsnorm_quant_kernel<QF, 4, WF32><<<grid, 256, 0, st>>>(p);
+  else if (per <= 8) rmsnorm_quant_kernel<QF, 8, WF32><<<grid, 256, 0, st>>>(p);
+  else rmsnorm_quant_kernel<QF, 16, WF32><<<grid, 256, 0, st>>>(p);
+}
+
+template <int QF>
+static void launch_rmsnorm(const FusedArgs &p, hipStream_t st) {
+  if (p.w_f32) launch_rmsnorm_w<QF, true>(p, st);
+  else launch_rmsnorm_w<QF, false>(p, st);
 }
 
 template <int QF, int TL, int V>
