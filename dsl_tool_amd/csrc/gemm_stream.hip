@@ -1,6 +1,6 @@
 // Streaming quantized GEMMs for gfx950 at skinny and mid M (M <= 256):
 // C[M,N] = A[M,K] . W[N,K]^T, FP8 per-tensor, FP8 1x128/128x128 block,
-// MXFP4 and bf16, one launch, deterministic.  BASELINE config 1 (M=128,
+// MXFP4, NVFP4 and bf16, one launch, deterministic.  BASELINE config 1 (M=128,
 // N=K=4096) and the decode shapes (M=16) run here.
 //
 // At these shapes the work per W byte is small (M flops per byte) and the
@@ -32,7 +32,12 @@
 // superblock, op_sel j picks the byte).  A and W share the order, so the
 // sum is unchanged.  FP8 block: each 128-byte step is one 128-K group,
 // folded as acc += part * (sa[m][grp] * sb[n/128][grp]), the group-partial
-// form of cuda/gemm/fp8_gemm.cu:84-97.
+// form of cuda/gemm/fp8_gemm.cu:84-97.  NVFP4: its E4M3 scales (one per
+// 16 elements) are not powers of two, so both operands are dequantized
+// exactly to fp16 (E2M1 x E4M3 has at most 6 significant bits) and go to
+// v_mfma_f32_16x16x32_f16; a lane takes one 16-byte chunk per 128-element
+// superblock, whose four words feed four MFMA steps; the fp32 global scales
+// apply in the epilogue.
 // LDS rows are CHUNK bytes; row r's 16-byte chunk c sits in slot c ^ r
 // (r < 16), so the 16 lanes that read one logical chunk of 16 rows hit
 // distinct bank groups.
@@ -50,14 +55,17 @@ struct StreamCfg {
   static constexpr int NW = 4, NT = NW * 64;         // waves split K
   static constexpr bool MX = MODE == MODE_MXFP4;
   static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;
+  static constexpr bool NV = MODE == MODE_NVFP4;
   static constexpr int CHUNK = CHUNK_;               // bytes of one row per item
   static constexpr int STEPS = CHUNK / 128;          // 128-byte MFMA steps (FP8 block: groups)
   static constexpr int SBK = CHUNK / 256;            // MXFP4 512-element superblocks
+  static constexpr int NSB = CHUNK / 64;             // NVFP4 128-element superblocks
   static constexpr int SPR = CHUNK / 16;             // 16-byte slots per row
   static constexpr int RPD = 1024 / CHUNK;           // rows per direct load
   static constexpr int DATA_DMA = 16 / RPD;          // direct loads per 16-row item
-  // scale bytes per row per chunk: E8M0 per 32 elements, fp32 per 128-K group
-  static constexpr int SROW = MX ? CHUNK / 16 : (BLOCK ? 4 * STEPS : 0);
+  // scale bytes per row per chunk: E8M0 per 32 elements, fp32 per 128-K
+  // group, E4M3 per 16 elements
+  static constexpr int SROW = MX ? CHUNK / 16 : (BLOCK ? 4 * STEPS : (NV ? CHUNK / 8 : 0));
   static constexpr bool SC16 = SROW >= 16;           // scales move 16 (else 4) bytes per lane
   static constexpr int AUX = SROW ? (SC16 ? 1024 : 256) : 0;
   static constexpr int DPI = DATA_DMA + (AUX ? 1 : 0);   // direct loads per item
@@ -83,6 +91,8 @@ struct StreamRegs {
   v4i wq[Cfg::TN][Cfg::SBK][4];     // MXFP4 W fragments (16 bytes per step)
   int ws[Cfg::TN][Cfg::SBK];        // MXFP4 W E8M0 words
   float sb[Cfg::STEPS];             // FP8 block: weight scales of the chunk's groups
+  v4i wn[Cfg::TN][Cfg::NSB];        // NVFP4: the lane's 16-byte W chunk of each superblock
+  uint32_t wsn[Cfg::TN][Cfg::NSB];  // NVFP4: that chunk's two E4M3 block scales (low 16 bits)
   v4f acc[Cfg::TN][Cfg::TMA];
 };
 
@@ -137,6 +147,8 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) 
       const uint8_t *sc;
       if constexpr (Cfg::MX) {
         sc = static_cast<const uint8_t *>(isW ? p.sb : p.sa) + row * sld + kb0 / 16;
+      } else if constexpr (Cfg::NV) {   // E4M3 per 16 elements: K/16 bytes per row
+        sc = static_cast<const uint8_t *>(isW ? p.sb : p.sa) + row * (int64_t)(p.K / 16) + kb0 / 8;
       } else {   // fp32 group scales of the chunk: sa[row][.], sb[n0/128][.]
         sc = reinterpret_cast<const uint8_t *>(
             isW ? static_cast<const float *>(p.sb) + (int64_t)(row / 128) * nkg
@@ -169,6 +181,15 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) 
           for (int j = 0; j < 4; ++j) st.wq[KIND][b][j] = chunk16(base, b * 16 + 4 * g + j);
           st.ws[KIND][b] = *reinterpret_cast<const int *>(aux + r16 * SROW + b * 16 + g * 4);
         }
+      } else if constexpr (Cfg::NV) {
+        // superblock b: lane group g takes 16-byte chunk 4b + g and its two
+        // block scales (kept packed; dequantized per activation tile)
+#pragma unroll
+        for (int b = 0; b < Cfg::NSB; ++b) {
+          const int c = 4 * b + g;
+          st.wn[KIND][b] = chunk16(base, c);
+          st.wsn[KIND][b] = *reinterpret_cast<const uint16_t *>(aux + r16 * SROW + 2 * c);
+        }
       } else {
 #pragma unroll
         for (int s = 0; s < Cfg::STEPS; ++s) {
@@ -182,7 +203,31 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) 
       }
     } else {                                    // activation tile x the W tiles
       constexpr int A = KIND - TN;
-      if constexpr (Cfg::MX) {
+      if constexpr (Cfg::NV) {
+        // word s of a lane's chunk holds elements 8s .. 8s+7 of it (block
+        // s / 2); MFMA step s of superblock b sums word s of chunk 4b + g
+        // over the lane groups g: the same permutation of K for A and W
+#pragma unroll
+        for (int b = 0; b < Cfg::NSB; ++b) {
+          const int c = 4 * b + g;
+          const v4i ad = chunk16(base, c);
+          const v2h as2 = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(
+              (uint32_t)*reinterpret_cast<const uint16_t *>(aux + r16 * SROW + 2 * c), 1.0f, false);
+          v2h ws2[TN];
+#pragma unroll
+          for (int t = 0; t < TN; ++t)
+            ws2[t] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(st.wsn[t][b], 1.0f, false);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const v8h ah = fp4x8_to_f16((uint32_t)ad[s], as2[s >> 1]);
+#pragma unroll
+            for (int t = 0; t < TN; ++t) {
+              const v8h wh = fp4x8_to_f16((uint32_t)st.wn[t][b][s], ws2[t][s >> 1]);
+              st.acc[t][A] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, wh, st.acc[t][A], 0, 0, 0);
+            }
+          }
+        }
+      } else if constexpr (Cfg::MX) {
 #pragma unroll
         for (int b = 0; b < Cfg::SBK; ++b) {
           const int asv = *reinterpret_cast<const int *>(aux + r16 * SROW + b * 16 + g * 4);
@@ -288,7 +333,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) 
 
   const int row = m0 + lrow, col0 = n0 + lcol;
   if (row >= p.M) return;
-  if constexpr (Cfg::MODE == MODE_FP8_TENSOR) {
+  if constexpr (Cfg::MODE == MODE_FP8_TENSOR || Cfg::NV) {   // NVFP4: the global scales
     const float s1 = *p.ga, s2 = *p.gb;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) v[c] = (v[c] * s1) * s2;
@@ -343,6 +388,7 @@ StreamPlan plan_for(int mode, int M, int N) {
   const char *e = getenv("DSL_GEMM_STREAM_TN");
   if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && !e[1]) pl.tn = e[0] - '0';
   if (pl.tn == 4 && mode == MODE_FP8_BLOCK && pl.tma == 4) pl.tn = 2;   // register budget
+  if (pl.tn == 4 && mode == MODE_NVFP4 && pl.tma == 4) pl.tn = 2;      // register budget
   return pl;
 }
 
@@ -359,7 +405,12 @@ hipError_t launch_cfg(const GemmArgs &p, hipStream_t st) {
 template <int MODE, int TMA, int CHUNK>
 hipError_t launch_tn(const GemmArgs &p, int tn, hipStream_t st) {
   if (tn == 1) return launch_cfg<MODE, TMA, 1, CHUNK>(p, st);
-  if (tn == 4) return launch_cfg<MODE, TMA, 4, CHUNK>(p, st);
+  // four W tiles beside four activation tiles exceed the registers of the
+  // FP8 block and NVFP4 forms (plan_for never asks for them)
+  constexpr bool four = !(TMA == 4 && (MODE == MODE_FP8_BLOCK || MODE == MODE_NVFP4));
+  if constexpr (four) {
+    if (tn == 4) return launch_cfg<MODE, TMA, 4, CHUNK>(p, st);
+  }
   return launch_cfg<MODE, TMA, 2, CHUNK>(p, st);
 }
 
@@ -379,6 +430,8 @@ bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
   if (mode == MODE_FP8_TENSOR || mode == MODE_BF16) return true;
   // block scales and E8M0 rows move by 16-byte direct loads (K % 512)
   if (mode == MODE_FP8_BLOCK || mode == MODE_MXFP4) return scales16 && K % 512 == 0;
+  // E4M3 rows (K/16 bytes) move by 16-byte direct loads
+  if (mode == MODE_NVFP4) return scales16 && K % 256 == 0;
   return false;
 }
 
@@ -389,6 +442,7 @@ hipError_t launch_gemm_stream(int mode, const GemmArgs &p, hipStream_t st) {
     case MODE_FP8_BLOCK: return launch_mode<MODE_FP8_BLOCK>(p, pl, st);
     case MODE_MXFP4: return launch_mode<MODE_MXFP4>(p, pl, st);
     case MODE_BF16: return launch_mode<MODE_BF16>(p, pl, st);
+    case MODE_NVFP4: return launch_mode<MODE_NVFP4>(p, pl, st);
     default: return hipErrorInvalidValue;
   }
 }

@@ -218,7 +218,8 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   // the decode kernel holds M <= 16 rows of A in registers and was the
   // faster one there (M = 16: 7.8 against 8.1 us); the streaming kernel
   // wins at M = 1 (11.7 against 13.5) and 17..32 (8.7 against 10.9)
-  const bool prefer_stream = skinny_stream || M == 1 || M > 16;
+  // NVFP4: the GEMV for M <= 4, the streaming kernel above that
+  const bool prefer_stream = skinny_stream || (mode == MODE_NVFP4 ? M > 4 : (M == 1 || M > 16));
   if (decode_on && !(prefer_stream && streamable) && decode_supported(mode, M, K, Kb, sc4, sc16)) {
     r.path = PATH_DECODE;
     return r;

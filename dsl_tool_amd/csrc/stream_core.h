@@ -1,5 +1,5 @@
-// Direct-to-LDS streaming helpers shared by the skinny-M and mid-M kernels
-// (gemm_decode.hip, gemm_mid.hip): each wave streams its own items through
+// Direct-to-LDS streaming helpers shared by the skinny-M kernels
+// (gemm_decode.hip, gemm_stream.hip): each wave streams its own items through
 // private LDS regions and waits on its own vector-memory counter.
 #pragma once
 

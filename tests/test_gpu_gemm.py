@@ -387,10 +387,13 @@ def test_mxfp4_decode(m, n, k):
     assert_close(c, ref, what=f"mxfp4 decode {m}x{n}x{k}")
 
 
-# NVFP4 with M <= 4 and M * K/2048 <= 8 runs the GEMV kernel; the other
-# shapes here take the dense paths (same oracle).
+# NVFP4 with M <= 4 and M * K/2048 <= 8 runs the GEMV kernel, 5 <= M <= 256
+# with K % 512 (M <= 32) or % 1024 the streaming kernel; the other shapes
+# here take the dense paths (same oracle).
 @pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (2, 1000, 2048), (3, 530, 4096),
-                                   (4, 64, 4096), (1, 33, 16384), (3, 520, 8192), (4, 100, 8192)])
+                                   (4, 64, 4096), (1, 33, 16384), (3, 520, 8192), (4, 100, 8192),
+                                   (16, 14336, 4096), (8, 1000, 2048), (128, 4096, 4096),
+                                   (100, 520, 1024), (24, 300, 1536)])
 def test_nvfp4_decode(m, n, k):
     a = W.randn_bf16((m, k), 451)
     w = W.randn_bf16((n, k), 452, 0.02)
@@ -569,12 +572,13 @@ def test_mid_m_block_and_mxfp4(m, n, k, mode):
 
 # The streaming kernel on every tile shape: 16-, 32- and 64-row activation
 # blocks with one, two or four 16-row W tiles per workgroup, ragged M and N.
-# DSL_GEMM_SKINNY=stream moves 2 <= M <= 16 onto it as well, and
+# DSL_GEMM_SKINNY=stream moves 2 <= M <= 16 (NVFP4: M <= 4) onto it as well, and
 # DSL_GEMM_STREAM_TN forces the W tiles (both read at every launch).
 STREAM_SHAPES = [("tensor", 16, 7168, 4096), ("block", 16, 7168, 4096), ("mxfp4", 16, 8192, 8192),
                  ("tensor", 1, 1000, 4096), ("block", 32, 1040, 2048), ("mxfp4", 7, 2048, 1024),
                  ("tensor", 96, 7168, 4096), ("block", 200, 1000, 2048), ("mxfp4", 256, 2056, 3072),
-                 ("bf16", 24, 1000, 2048)]
+                 ("bf16", 24, 1000, 2048), ("nvfp4", 16, 7168, 4096), ("nvfp4", 3, 520, 8192),
+                 ("nvfp4", 200, 1000, 3072), ("nvfp4", 40, 2056, 2048)]
 
 
 @pytest.mark.parametrize("tn", ["1", "2", "4"])
@@ -601,6 +605,14 @@ def test_stream_kernel_tile_shapes(mode, m, n, k, tn, monkeypatch):
         qw, ew = Q.quant_mxfp4(w.to(DEV))
         ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
         run = lambda: G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4", out_dtype=torch.float32)
+    elif mode == "nvfp4":
+        a = W.randn_bf16((m, k), 165)
+        qa, sa, ga = Q.quant_nvfp4(a.to(DEV))
+        qw, sw, gw = Q.quant_nvfp4(w.to(DEV))
+        ref = OG.ref_nvfp4(np_u8(qa), np_u8(sa), np_f32(ga)[0], np_u8(qw), np_u8(sw),
+                           np_f32(gw)[0])
+        run = lambda: G.fp4_gemm_packed(qa, sa, qw, sw, fmt="nvfp4", global_a=ga, global_w=gw,
+                                        out_dtype=torch.float32)
     else:
         a = W.randn_bf16((m, k), 164)
         ref = OG.ref_bf16(a.float().numpy(), w.float().numpy()).astype(np.float32)
