@@ -125,9 +125,12 @@ def test_workspace_query_matches_the_planned_path(lib):
     # skinny M with K a multiple of 1024 takes the single-pass decode kernel
     assert lib.dsl_gemm_workspace_bytes(N.OP_FP8, 16, 8192, 8192) == 0
     # FP4 reports the larger of the MXFP4 and NVFP4 plans: NVFP4 with M <= 4
-    # runs the GEMV kernel (no workspace), with M = 8 it plans split-K
+    # runs the GEMV kernel and 5 <= M <= 256 the streaming kernel (no
+    # workspace); a K neither skinny kernel takes (4352: not a multiple of
+    # 512 elements) plans split-K over the register-staged tiles
     assert lib.dsl_gemm_workspace_bytes(N.OP_FP4, 1, 14336, 4096) == 0
-    assert lib.dsl_gemm_workspace_bytes(N.OP_FP4, 8, 14336, 4096) >= 8 * 14336 * 4
+    assert lib.dsl_gemm_workspace_bytes(N.OP_FP4, 8, 14336, 4096) == 0
+    assert lib.dsl_gemm_workspace_bytes(N.OP_FP4, 8, 14336, 4352) >= 8 * 14336 * 4
     # large problems take the pipelined kernels, which need none either
     assert lib.dsl_gemm_workspace_bytes(N.OP_FP8, 8192, 8192, 8192) == 0
     # a skinny problem the decode kernel does not cover plans split-K and
