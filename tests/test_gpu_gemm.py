@@ -470,8 +470,9 @@ def test_nvfp4_pipelined(m, n, k):
 # ------------------------------------ BASELINE config 1 and mid-size M --
 # Config 1 is the shape the reference quotes for its registered fp8_gemm
 # (triton/gemm/gemm_kernels.py:104-122): FP8 per-tensor, A [128, 4096]
-# ~N(0,1), W [4096, 4096] ~N(0, 0.02).  The neighbouring M cover the
-# boundary between the decode kernel (M <= 32) and the larger tiles.
+# ~N(0,1), W [4096, 4096] ~N(0, 0.02); it runs on the streaming kernel.  The
+# neighbouring M cover its 32- and 64-row activation blocks and its upper
+# bound (M = 256).
 MID_SHAPES = [(128, 4096, 4096), (33, 4096, 4096), (64, 4096, 4096), (256, 4096, 4096),
               (96, 1000, 2048), (200, 2056, 1024), (128, 512, 16384)]
 
@@ -544,7 +545,7 @@ def test_misaligned_scales_with_small_workspace():
     assert_close(c, ref, what="mxfp4 misaligned scales")
 
 
-# The mid-M kernel (32 < M <= 256) in its other modes: two W tiles per
+# The streaming kernel at 32 < M <= 256 in its other modes: two W tiles per
 # workgroup (config-1-sized N) and one (small N), ragged M and N edges, and
 # M blocks whose last rows repeat the edge row.
 MID_MODE_SHAPES = [(128, 4096, 4096), (256, 7168, 4096), (40, 512, 2048), (97, 1000, 1024),
