@@ -291,8 +291,8 @@ def build_cases(names, dev):
                                    src.data_ptr(), rws.data_ptr(), nbw, st)
 
         def permute(st):
-            return L.dsl_moe_permute_quant(x.data_ptr(), T, K, K, src.data_ptr(), off.data_ptr(), E,
-                                           rows, qx.data_ptr(), sx.data_ptr(), st)
+            return L.dsl_moe_permute_quant(x.data_ptr(), T, K, K, dest.data_ptr(), k, rows,
+                                           qx.data_ptr(), sx.data_ptr(), st)
 
         def grouped(st):
             return L.dsl_grouped_fp8_gemm(qx.data_ptr(), qw.data_ptr(), y.data_ptr(), off.data_ptr(),
@@ -318,11 +318,12 @@ def build_cases(names, dev):
         nonempty = int((counts > 0).sum())
         flops = 2.0 * rows * Nn * K if stage == "layer" else 0.0
         nbytes = {"route": 4 * rows * 3 + 4 * (E + 1),
-                  "permute": 2 * rows * K + rows * K + 4 * rows,
+                  "permute": 2 * T * K + rows * K + 4 * rows * 2,
                   "combine": 2 * rows * Nn + 4 * rows * 2 + 2 * T * Nn,
                   "layer": 2 * T * K + nonempty * Nn * K + 2 * T * Nn}[stage]
         what = {"route": "MoE route (stable counting sort) of 4096x8 ids over 64 experts",
-                "permute": "MoE permute + per-row E4M3 of 32768 token rows, K=2048 (x re-read per slot)",
+                "permute": "MoE permute + per-row E4M3: 4096 tokens quantized once, K=2048, "
+                           "scattered to their 32768 routed rows",
                 "combine": "MoE weighted combine of 32768 rows, N=1536 -> 4096 tokens",
                 "layer": "MoE projection cfg5: route + permute/quant + grouped FP8 GEMM + combine"}[stage]
         return Case(name, flops, nbytes, PEAK_FP8_TFLOPS, "mfma" if stage == "layer" else "hbm",

@@ -83,7 +83,7 @@ extern "C" {
 
 const char *dsl_last_error(void) { return g_err.c_str(); }
 
-int dsl_abi_version(void) { return 6; }
+int dsl_abi_version(void) { return 7; }
 
 size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
   (void)rows;
@@ -518,23 +518,22 @@ int dsl_moe_route(const int32_t *topk_ids, int64_t tokens, int64_t topk, int64_t
 }
 
 int dsl_moe_permute_quant(const void *x, int64_t tokens, int64_t k, int64_t ldx,
-                          const int32_t *src_token, const int32_t *offsets, int64_t num_experts,
-                          int64_t rows, uint8_t *qx, float *sx, void *stream) {
+                          const int32_t *dest, int64_t topk, int64_t rows, uint8_t *qx, float *sx,
+                          void *stream) {
   const char *fn = "dsl_moe_permute_quant";
-  if (tokens < 0 || rows < 0 || k <= 0 || num_experts <= 0)
-    return fail(DSL_ERR_ARG, "%s: bad sizes", fn);
+  if (tokens < 0 || rows < 0 || k <= 0 || topk <= 0) return fail(DSL_ERR_ARG, "%s: bad sizes", fn);
   if (k % 8 != 0 || k > 32768)
     return fail(DSL_ERR_ARG, "%s: k=%lld must be a multiple of 8 and <= 32768", fn, (long long)k);
   if (ldx < k || ldx % 8 != 0) return fail(DSL_ERR_ARG, "%s: ldx must be >= k, a multiple of 8", fn);
-  if (rows >= ((int64_t)1 << 31)) return fail(DSL_ERR_ARG, "%s: too many rows", fn);
-  if (rows == 0) return ok();
-  if (tokens == 0) return fail(DSL_ERR_ARG, "%s: rows without tokens", fn);
+  if (rows >= ((int64_t)1 << 31) || tokens >= ((int64_t)1 << 31) || tokens * topk >= ((int64_t)1 << 31))
+    return fail(DSL_ERR_ARG, "%s: too many rows", fn);
+  if (rows == 0 || tokens == 0) return ok();
   int rc;
   if ((rc = check_out(fn, x, "x")) || (rc = check_out(fn, qx, "qx"))) return rc;
-  if (!src_token || !offsets || !sx) return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
+  if (!dest || !sx) return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
   return hip_status(dsl::launch_moe_permute_quant(static_cast<const uint16_t *>(x), ldx, (int)k,
-                                                  (int)tokens, src_token, offsets + num_experts,
-                                                  (int)rows, qx, sx, static_cast<hipStream_t>(stream)),
+                                                  (int)tokens, dest, (int)topk, (int)rows, qx, sx,
+                                                  static_cast<hipStream_t>(stream)),
                     fn);
 }
 

@@ -127,10 +127,11 @@ hipError_t launch_fused_quant(int prod, int qf, const FusedArgs &p, hipStream_t 
 size_t moe_route_workspace_bytes(int64_t assignments, int64_t num_experts);
 hipError_t launch_moe_route(const int32_t *ids, int n, int topk, int E, int32_t *offsets,
                             int32_t *dest, int32_t *src_token, int32_t *ws, hipStream_t st);
-// total = &offsets[E]; rows = grid size (every assignment); k_dim <= 32768.
+// One workgroup per token; slots whose row is < 0 or >= rows are skipped;
+// k_dim <= 32768.
 hipError_t launch_moe_permute_quant(const uint16_t *x, int64_t ldx, int k_dim, int tokens,
-                                    const int32_t *src_token, const int32_t *total, int rows,
-                                    uint8_t *qx, float *sx, hipStream_t st);
+                                    const int32_t *dest, int topk, int rows, uint8_t *qx, float *sx,
+                                    hipStream_t st);
 // n <= 32768; slots whose row is < 0 or >= rows_y are skipped.
 hipError_t launch_moe_combine(const uint16_t *y, int rows_y, int64_t ldy, int n, const int32_t *dest,
                               const float *w, int tokens, int topk, void *out, int64_t ldo,

@@ -225,19 +225,16 @@ __global__ __launch_bounds__(1024) void moe_route_one_kernel(const int32_t *__re
   }
 }
 
-// Gather + per-row E4M3: one workgroup per sorted row, thread t holding
-// chunks t + 256 j of the source token's row.  Rows at or past
-// offsets[E] (the routed total; the grid covers every assignment) exit.
+// Per-token E4M3 scattered to every routed slot: one workgroup per token,
+// thread t holding chunks t + 256 j of the row.  The token is read and
+// quantized once and its codes and scale are written to each sorted row
+// dest[t * topk + j] that lies in [0, rows); dropped slots (-1) are skipped.
 template <int CPL>
 __global__ __launch_bounds__(256) void moe_permute_quant_kernel(
-    const uint16_t *__restrict__ x, int64_t ldx, int k_dim, int tokens,
-    const int32_t *__restrict__ src_token, const int32_t *__restrict__ total,
-    uint8_t *__restrict__ qx, float *__restrict__ sx) {
+    const uint16_t *__restrict__ x, int64_t ldx, int k_dim, const int32_t *__restrict__ dest,
+    int topk, int rows, uint8_t *__restrict__ qx, float *__restrict__ sx) {
   __shared__ float sh[4];
-  const int row = blockIdx.x;
-  if (row >= *total) return;                       // whole workgroup
-  int t = src_token[row];
-  t = t < 0 ? 0 : (t >= tokens ? tokens - 1 : t);
+  const int t = blockIdx.x;
   const int nch = k_dim >> 3;
   const uint16_t *xr = x + (int64_t)t * ldx;
   uint4 xa[CPL];
@@ -255,14 +252,22 @@ __global__ __launch_bounds__(256) void moe_permute_quant_kernel(
   }
   const float s = fp8_scale_of(block_max(m, sh));
   const float r = rcp_approx(s);
-  if (threadIdx.x == 0) sx[row] = s;
+  uint2 q[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
-    const int c = threadIdx.x + 256 * j;
-    if (c < nch) {
-      float f[8];
-      unpack8(xa[j], f);
-      *reinterpret_cast<uint2 *>(qx + (int64_t)row * k_dim + (int64_t)c * 8) = e4m3_quot8(f, s, r);
+    float f[8];
+    unpack8(xa[j], f);
+    q[j] = e4m3_quot8(f, s, r);
+  }
+  for (int slot = 0; slot < topk; ++slot) {
+    const int row = dest[(int64_t)t * topk + slot];
+    if (row < 0 || row >= rows) continue;                // uniform across the block
+    if (threadIdx.x == 0) sx[row] = s;
+    uint8_t *qr = qx + (int64_t)row * k_dim;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      if (c < nch) *reinterpret_cast<uint2 *>(qr + (int64_t)c * 8) = q[j];
     }
   }
 }
@@ -350,12 +355,12 @@ static void by_cpl(int cols, F &&f) {
 }
 
 hipError_t launch_moe_permute_quant(const uint16_t *x, int64_t ldx, int k_dim, int tokens,
-                                    const int32_t *src_token, const int32_t *total, int rows,
-                                    uint8_t *qx, float *sx, hipStream_t st) {
-  if (rows == 0) return hipSuccess;
+                                    const int32_t *dest, int topk, int rows, uint8_t *qx, float *sx,
+                                    hipStream_t st) {
+  if (tokens == 0 || rows == 0) return hipSuccess;
   by_cpl(k_dim, [&](auto cpl) {
-    moe_permute_quant_kernel<decltype(cpl)::value><<<rows, 256, 0, st>>>(x, ldx, k_dim, tokens,
-                                                                         src_token, total, qx, sx);
+    moe_permute_quant_kernel<decltype(cpl)::value><<<tokens, 256, 0, st>>>(x, ldx, k_dim, dest, topk,
+                                                                           rows, qx, sx);
   });
   return hipGetLastError();
 }

@@ -61,7 +61,8 @@ def moe_route(topk_ids: torch.Tensor, num_experts: int) -> Route:
 def moe_permute_quant(x: torch.Tensor, route: Route):
     """Token rows of ``x [T, K]`` (bf16) in expert order, E4M3 with one scale
     per row: ``(qx [T*topk, K] uint8, sx [T*topk] float32)``; rows past the
-    routed total are unused."""
+    routed total are unused.  Each token is quantized once and written to
+    its ``topk`` sorted rows ``route.dest``."""
     _gpu(x, "x")
     if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] != route.tokens:
         raise ValueError("x must be bf16 [tokens, K]")
@@ -72,9 +73,8 @@ def moe_permute_quant(x: torch.Tensor, route: Route):
     qx = torch.empty((rows, K), dtype=torch.uint8, device=x.device)
     sx = torch.empty(rows, dtype=torch.float32, device=x.device)
     with torch.cuda.device(x.device):
-        N.call("dsl_moe_permute_quant", N.ptr(x), T, K, x.stride(0), N.ptr(route.src_token),
-               N.ptr(route.offsets), route.num_experts, rows, N.ptr(qx), N.ptr(sx),
-               N.stream_of(x.device))
+        N.call("dsl_moe_permute_quant", N.ptr(x), T, K, x.stride(0), N.ptr(route.dest),
+               route.topk, rows, N.ptr(qx), N.ptr(sx), N.stream_of(x.device))
     return qx, sx
 
 

@@ -236,15 +236,16 @@ int dsl_moe_route(const int32_t *topk_ids, int64_t tokens, int64_t topk, int64_t
                   int32_t *offsets, int32_t *dest, int32_t *src_token,
                   void *workspace, size_t workspace_bytes, void *stream);
 
-/* Sorted row r < offsets[num_experts] of qx [rows][k] E4M3 and sx [rows]
- * float: token src_token[r] of x [tokens][ldx] bf16 quantized per row,
- * scale max(amax/448, 1e-12) (as dsl_quant_fp8_blocks with a 1 x k group).
- * rows = tokens * topk (rows past the routed total are left untouched).
+/* Token t of x [tokens][ldx] bf16 quantized per row to E4M3 with scale
+ * max(amax/448, 1e-12) (as dsl_quant_fp8_blocks with a 1 x k group) and
+ * written to every sorted row d = dest[t*topk+j] with 0 <= d < rows: codes
+ * to qx [rows][k], scale to sx [d].  With dest from dsl_moe_route, row r <
+ * offsets[num_experts] then holds token src_token[r]; rows no slot names
+ * are left untouched.  Each token is read once whatever topk is.
  * k % 8 == 0, k <= 32768. */
 int dsl_moe_permute_quant(const void *x, int64_t tokens, int64_t k, int64_t ldx,
-                          const int32_t *src_token, const int32_t *offsets,
-                          int64_t num_experts, int64_t rows, uint8_t *qx, float *sx,
-                          void *stream);
+                          const int32_t *dest, int64_t topk, int64_t rows,
+                          uint8_t *qx, float *sx, void *stream);
 
 /* out [tokens][ldo] = sum over j of topk_weights[t][j] * y[dest[t*topk+j]]
  * (y [rows][ldy] bf16, the grouped GEMM's output), in fp32 with slot order j

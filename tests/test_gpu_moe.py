@@ -54,12 +54,16 @@ def test_route_config5_routing():
     assert (np.diff(r.offsets.cpu().numpy()) == 0).sum() >= 4        # forced-empty experts
 
 
-@pytest.mark.parametrize("T,k,E,K", [(300, 4, 9, 2048), (64, 2, 3, 136), (5, 3, 4, 7168)])
-def test_permute_quant_matches_oracle(T, k, E, K):
+@pytest.mark.parametrize("T,k,E,K,pad", [(300, 4, 9, 2048, 0), (64, 2, 3, 136, 8), (5, 3, 4, 7168, 0),
+                                         (1000, 8, 64, 2048, 0), (3, 8, 5, 32768, 16), (1, 1, 1, 8, 0)])
+def test_permute_quant_matches_oracle(T, k, E, K, pad):
     ids = _ids(T, k, E, 410 + T, drop=True)
     x = W.randn_bf16((T, K), 411) * 3
     r = M.moe_route(ids.to(DEV), E)
-    qx, sx = M.moe_permute_quant(x.to(DEV), r)
+    xd = x.to(DEV)
+    if pad:      # row stride K + pad: the kernel reads rows at ldx
+        xd = torch.nn.functional.pad(xd, (0, pad))[:, :K]
+    qx, sx = M.moe_permute_quant(xd, r)
     off, dest, src = OM.route(ids.numpy(), E)
     q_ref, s_ref = OM.permute_quant(x.float().numpy(), src)
     n = int(off[-1])

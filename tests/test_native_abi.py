@@ -114,7 +114,7 @@ def test_moe_glue_argument_validation(lib):
     assert need >= 32 * 64 * 4
     rc = lib.dsl_moe_route(fake, 4096, 8, 64, fake, fake, fake, fake, need - 4, None)
     assert rc == N.DSL_ERR_WORKSPACE
-    rc = lib.dsl_moe_permute_quant(fake, 16, 100, 104, fake, fake, 4, 32, fake, fake, None)
+    rc = lib.dsl_moe_permute_quant(fake, 16, 100, 104, fake, 2, 32, fake, fake, None)
     assert rc == N.DSL_ERR_ARG and "multiple of 8" in _err(lib)
     rc = lib.dsl_moe_combine(fake, 32, 64, 32, fake, fake, 16, 2, fake, 64, 0, None)
     assert rc == N.DSL_ERR_ARG and "ldy" in _err(lib)
