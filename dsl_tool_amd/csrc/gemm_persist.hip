@@ -931,7 +931,7 @@ void gemm_persist_kernel(const Args p) {
   pipe::wait_vmcnt<0>();
 }
 
-static int persist_cu_count() {
+int device_cu_count() {
   static int cached[64] = {0};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
@@ -949,7 +949,7 @@ template <int MODE>
 static hipError_t launch_persist_mode(const GemmArgs &p, hipStream_t st) {
   using Cfg = PersCfg<MODE>;
   const int ntiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * ((p.N + Cfg::BN - 1) / Cfg::BN);
-  int grid = persist_cu_count();
+  int grid = device_cu_count();
   if (grid > ntiles) grid = ntiles;
   gemm_persist_kernel<Cfg, GemmArgs><<<grid, Cfg::NT, 0, st>>>(p);
   return hipGetLastError();
@@ -989,7 +989,7 @@ hipError_t launch_grouped_persist(const GroupedArgs &p, hipStream_t st) {
   using Cfg = PersCfg<MODE_FP8_TENSOR, true>;
   const int nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
   const int64_t upper = ((int64_t)(p.rows + Cfg::BM - 1) / Cfg::BM + p.G) * nbn;
-  int64_t grid = persist_cu_count();
+  int64_t grid = device_cu_count();
   if (grid > upper) grid = upper;
   if (grid < 1) grid = 1;
   gemm_persist_kernel<Cfg, GroupedArgs><<<(unsigned)grid, Cfg::NT, 0, st>>>(p);

@@ -211,24 +211,11 @@ void grouped_pipe_kernel(const GroupedArgs p) {
   }
 }
 
-static int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 template <class Cfg>
 static void launch_grouped_cfg(const GroupedArgs &p, hipStream_t st) {
   const int nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
   const int64_t upper = ((int64_t)(p.rows + Cfg::BM - 1) / Cfg::BM + p.G) * nbn;
-  int64_t grid = cu_count();
+  int64_t grid = device_cu_count();
   if (grid > upper) grid = upper;
   if (grid < 1) grid = 1;
   grouped_fp8_kernel<Cfg><<<(unsigned)grid, Cfg::NT, 0, st>>>(p);
@@ -238,7 +225,7 @@ template <class Cfg>
 static void launch_grouped_pipe_cfg(const GroupedArgs &p, hipStream_t st) {
   const int nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
   const int64_t upper = ((int64_t)(p.rows + Cfg::BM - 1) / Cfg::BM + p.G) * nbn;
-  int64_t grid = cu_count();
+  int64_t grid = device_cu_count();
   if (grid > upper) grid = upper;
   if (grid < 1) grid = 1;
   grouped_pipe_kernel<Cfg><<<(unsigned)grid, Cfg::NT, 0, st>>>(p);

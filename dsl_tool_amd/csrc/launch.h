@@ -30,6 +30,10 @@ size_t quant_scratch_bytes();
 // ---------------------------------------------------------------- GEMMs --
 enum GemmMode { MODE_FP8_TENSOR = 0, MODE_FP8_BLOCK = 1, MODE_MXFP4 = 2, MODE_NVFP4 = 3, MODE_BF16 = 4 };
 
+// Compute units of the current device (cached per device; 256 if the query
+// fails).
+int device_cu_count();
+
 struct GemmArgs {
   const uint8_t *a;      // [M][Kb] packed, K-major
   const uint8_t *b;      // [N][Kb] packed, K-major
