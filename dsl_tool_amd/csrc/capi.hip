@@ -386,19 +386,31 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct LoraPlan {
   int64_t ld2;                 // padded columns of hi | lo and of B^T | B^T
+  bool tt;                     // T^T = A^T X^T on the streaming kernel, split in its epilogue
+  bool one_pass;               // adapter term as a second K segment of the persistent kernel
+  int rep;                     // ... reading B^T twice: its pairs per row (else 0: B^T | B^T copied)
   size_t t32, ws, t2, b2, total;
 };
 
 LoraPlan lora_plan(int64_t m, int64_t n, int64_t k, int64_t lr) {
   LoraPlan p;
   p.ld2 = (2 * lr + 63) / 64 * 64;
+  // T^T = A^T X^T on the streaming kernel when the adapter columns are few
+  // enough to be its skinny M; its epilogue writes hi | lo itself.
+  p.tt = lr <= 256 && dsl::stream_supported(dsl::MODE_BF16, (int)lr, (int)m, (int)k, (int)(2 * k), true);
+  p.one_pass = dsl::persist_supported(dsl::MODE_BF16, (int)m, (int)n, (int)k, (int)(2 * (k + p.ld2)), true) &&
+               (2 * k) % 128 == 0;
+  // hi | lo against B^T | B^T without the copy (one pass only): B^T's rows
+  // must be whole pairs (64 bf16), a power of two of them, filling ld2 / 2
+  const int64_t pr = lr / 64;
+  p.rep = (p.one_pass && lr % 64 == 0 && (pr & (pr - 1)) == 0 && p.ld2 == 2 * lr) ? (int)pr : 0;
   const size_t ws1 = dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, lr, k);
   const size_t ws3 = dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, n, k);
   const size_t ws4 = dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, n, p.ld2, true);
-  p.t32 = align256((size_t)(m * lr) * 4);
+  p.t32 = p.tt ? 0 : align256((size_t)(m * lr) * 4);
   p.ws = align256(std::max(ws1, std::max(ws3, ws4)));
   p.t2 = align256((size_t)(m * p.ld2) * 2);
-  p.b2 = align256((size_t)(n * p.ld2) * 2);
+  p.b2 = p.rep ? 0 : align256((size_t)(n * p.ld2) * 2);
   p.total = p.t32 + p.ws + p.t2 + p.b2;
   return p;
 }
@@ -463,25 +475,37 @@ int dsl_lora_gemm(const void *x, const void *w, const void *a_t, const void *b_t
   hipStream_t st = static_cast<hipStream_t>(stream);
   // T = X A^T.  With at most 256 adapter columns it is computed as
   // T^T = A^T X^T: the adapter rows are then the skinny M of the streaming
-  // (or decode) kernel, which reads X once in one launch; otherwise (and
-  // when K does not suit those kernels) T comes from the register-staged
-  // tiles over the workspace.
-  const bool tt = lr <= 256 && dsl::stream_supported(dsl::MODE_BF16, (int)lr, (int)m, (int)k,
-                                                     (int)(2 * k), true);
-  hipError_t e = tt ? dsl::launch_gemm(dsl::MODE_BF16, bf16_args(a_t, x, t32, lr, m, k, m, false, nullptr, 0), st)
-                    : dsl::launch_gemm(dsl::MODE_BF16, bf16_args(x, a_t, t32, m, lr, k, lr, false, gws, pl.ws), st);
-  if (e == hipSuccess)
-    e = dsl::launch_lora_split(t32, (int)m, (int)lr, (int)pl.ld2, (int)rank, tt, scales, t2, st);
-  if (e == hipSuccess) e = dsl::launch_lora_dup(static_cast<const uint16_t *>(b_t), (int)n, (int)lr,
-                                                (int)pl.ld2, b2, st);
+  // kernel, which reads X once in one launch and whose epilogue writes
+  // hi | lo of T*s (transposed back) straight into t2; otherwise (and when
+  // K does not suit that kernel) T comes from the register-staged tiles over
+  // the workspace and a separate split pass.
+  hipError_t e;
+  if (pl.tt) {
+    dsl::GemmArgs tg = bf16_args(a_t, x, t2, lr, m, k, pl.ld2, false, nullptr, 0);
+    tg.out_f32 = 0;
+    tg.lora_scales = scales;
+    tg.lora_rank = (int)rank;
+    e = dsl::launch_gemm(dsl::MODE_BF16, tg, st);
+  } else {
+    e = dsl::launch_gemm(dsl::MODE_BF16, bf16_args(x, a_t, t32, m, lr, k, lr, false, gws, pl.ws), st);
+    if (e == hipSuccess)
+      e = dsl::launch_lora_split(t32, (int)m, (int)lr, (int)pl.ld2, (int)rank, scales, t2, st);
+  }
+  if (e == hipSuccess && !pl.rep)
+    e = dsl::launch_lora_dup(static_cast<const uint16_t *>(b_t), (int)n, (int)lr, (int)pl.ld2, b2, st);
   if (e != hipSuccess) return hip_status(e, fn);
   dsl::GemmArgs g = bf16_args(x, w, y, m, n, k, ldy, false, gws, pl.ws);
-  if (dsl::persist_supported(dsl::MODE_BF16, (int)m, (int)n, (int)k, (int)(2 * (k + pl.ld2)), true) &&
-      (2 * k) % 128 == 0) {
+  if (pl.one_pass) {
     // one pass: the adapter columns are a second K segment of every row
     g.a2 = reinterpret_cast<const uint8_t *>(t2);
-    g.b2 = reinterpret_cast<const uint8_t *>(b2);
     g.Kb2 = (int)(2 * pl.ld2);
+    if (pl.rep) {            // B^T | B^T read from B^T itself
+      g.b2 = static_cast<const uint8_t *>(b_t);
+      g.ldb2 = (int)(2 * lr);
+      g.rep2 = pl.rep;
+    } else {
+      g.b2 = reinterpret_cast<const uint8_t *>(b2);
+    }
     e = dsl::launch_gemm(dsl::MODE_BF16, g, st);
   } else {
     e = dsl::launch_gemm(dsl::MODE_BF16, g, st);

@@ -175,18 +175,21 @@ struct Ring {
   int lim;                       // last valid tile row of the operand (uniform)
   int kb;
   int kb2, nk1;                  // second segment: row stride, first pair
+  int rmask;                     // second segment: pair index mask (W2 repeating), else all ones
   uint32_t vsub;                 // lane's row within one DMA
   uint32_t vchunk;               // lane's chunk byte offset for even DMAs
   uint32_t soff;                 // lane's scale offset
   int wave;
   bool full;
 
-  DSL_DEV void target(const TileRef &tr, int kb_, int wave_, int lane, int kb2_ = 0) {
+  DSL_DEV void target(const TileRef &tr, int kb_, int wave_, int lane, int kb2_ = 0,
+                      int ldb2_ = 0, int rep2_ = 0) {
     wave = wave_;
-    kb2 = kb2_;
     nk1 = kb_ / Cfg::PKB;
     full = Cfg::DS > 0 && wave < Cfg::SC_DMA;
     const bool isA = wave * Cfg::DD < Cfg::A_DMA;
+    kb2 = isA || ldb2_ == 0 ? kb2_ : ldb2_;
+    rmask = isA || rep2_ == 0 ? 0x7fffffff : rep2_ - 1;
     lim = (isA ? tr.arows : tr.brows) - 1;
     kb = kb_;
     wrow = (isA ? wave * Cfg::DD : wave * Cfg::DD - Cfg::A_DMA) * Cfg::RPI;
@@ -238,7 +241,8 @@ struct Ring {
     if constexpr (Cfg::BF16) {
       // pairs from nk1 on come from the second segment (selects, no branch)
       const bool s2 = q >= nk1;
-      const uint8_t *base = s2 ? dbase2 + (int64_t)(q - nk1) * Cfg::PKB : dbase + (int64_t)q * Cfg::PKB;
+      const uint8_t *base =
+          s2 ? dbase2 + (int64_t)((q - nk1) & rmask) * Cfg::PKB : dbase + (int64_t)q * Cfg::PKB;
       dma16(base, __umul24((uint32_t)r, (uint32_t)(s2 ? kb2 : kb)) + ch,
             slot + (uint32_t)((wave * Cfg::DD + j) * 1024));
     } else {
@@ -532,8 +536,12 @@ void gemm_persist_kernel(const Args p) {
     }
   }
   if (my_tiles <= 0) return;                      // before any copy is issued
-  int kb2 = 0;
-  if constexpr (Cfg::BF16) kb2 = p.Kb2;
+  int kb2 = 0, ldb2 = 0, rep2 = 0;
+  if constexpr (Cfg::BF16) {
+    kb2 = p.Kb2;
+    ldb2 = p.ldb2;
+    rep2 = p.rep2;
+  }
   const int nkp = (kb + kb2) / Cfg::PKB;          // pairs per tile, >= 1
 
   auto tile_ref = [&](int t) __attribute__((always_inline)) {
@@ -548,7 +556,7 @@ void gemm_persist_kernel(const Args p) {
       tr.a2 = tr.b2 = nullptr;
       if constexpr (Cfg::BF16) {
         tr.a2 = p.a2 + (int64_t)tr.m0 * kb2;
-        tr.b2 = p.b2 + (int64_t)tr.n0 * kb2;
+        tr.b2 = p.b2 + (int64_t)tr.n0 * (ldb2 ? ldb2 : kb2);
       }
       tr.arows = p.M - tr.m0;
       tr.mend = p.M;
@@ -589,7 +597,7 @@ void gemm_persist_kernel(const Args p) {
   int it = 0, iq = 0, ig = 0, iqc = -1, ies = 0;
   TileRef itr = tile_ref(0);
   auto retarget = [&]() __attribute__((always_inline)) {
-    ring.target(itr, kb, wave, lane, kb2);
+    ring.target(itr, kb, wave, lane, kb2, ldb2, rep2);
     if constexpr (Cfg::SCALED) ring.target_scales(p, itr.m0, itr.n0, lane);
   };
   retarget();

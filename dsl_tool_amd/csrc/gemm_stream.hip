@@ -326,6 +326,29 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) 
   __syncthreads();
 
   constexpr int CPT = Cfg::CPT, GPR = Cfg::BN / CPT;
+  if constexpr (Cfg::MODE == MODE_BF16) {
+    if (p.lora_scales) {
+      // LoRA: C^T, scaled per adapter column, as a bf16 hi + lo pair.
+      // Thread -> tile column n (a row of the output) and CPT consecutive
+      // tile rows, so that the NT / BN threads of one n cover its BM rows.
+      constexpr int TPN = Cfg::NT / Cfg::BN, RPT = Cfg::BM / TPN;
+      static_assert(TPN * RPT == Cfg::BM, "transposed epilogue mapping");
+      const int tn = threadIdx.x / TPN, tm = (threadIdx.x % TPN) * RPT;
+      const int ncol = n0 + tn;
+      if (ncol >= p.N) return;
+      uint16_t *orow = static_cast<uint16_t *>(p.c) + (int64_t)ncol * p.ldc;
+      for (int i = 0; i < RPT && m0 + tm + i < p.M; ++i) {
+        const int m = m0 + tm + i;
+        const float v = T[(tm + i) * Cfg::TLD + tn] * p.lora_scales[m / p.lora_rank];
+        const uint16_t h = f32_to_bf16(v);
+        orow[m] = h;
+        orow[p.M + m] = f32_to_bf16(v - bf16_to_f32(h));
+      }
+      if (m0 == 0 && tm == 0)
+        for (int64_t c = 2 * (int64_t)p.M; c < p.ldc; ++c) orow[c] = 0;
+      return;
+    }
+  }
   const int lrow = threadIdx.x / GPR, lcol = (threadIdx.x % GPR) * CPT;
   float v[CPT];
 #pragma unroll
@@ -436,6 +459,8 @@ bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
 }
 
 hipError_t launch_gemm_stream(int mode, const GemmArgs &p, hipStream_t st) {
+  if (p.lora_scales && (mode != MODE_BF16 || p.lora_rank < 1 || p.ldc < 2 * (int64_t)p.M))
+    return hipErrorInvalidValue;
   const StreamPlan pl = plan_for(mode, p.M, p.N);
   switch (mode) {
     case MODE_FP8_TENSOR: return launch_mode<MODE_FP8_TENSOR>(p, pl, st);

@@ -264,12 +264,23 @@ size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K, bool accu
 hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
   const uintptr_t sc = reinterpret_cast<uintptr_t>(p.sa) | reinterpret_cast<uintptr_t>(p.sb);
   if (p.Kb2 > 0) {   // a second K segment: the persistent BF16 kernel only
-    if (mode != MODE_BF16 || p.accumulate || p.Kb % 128 != 0 || p.Kb2 % 128 != 0 ||
-        !persist_supported(mode, p.M, p.N, p.K, p.Kb + p.Kb2, true))
+    if (mode != MODE_BF16 || p.accumulate || p.lora_scales || p.Kb % 128 != 0 ||
+        p.Kb2 % 128 != 0 || !persist_supported(mode, p.M, p.N, p.K, p.Kb + p.Kb2, true))
+      return hipErrorInvalidValue;
+    // W2 read from a narrower B whose pairs repeat: whole pairs, a power of
+    // two of them per row
+    if (p.rep2 != 0 && ((p.rep2 & (p.rep2 - 1)) != 0 || p.ldb2 % 16 != 0 ||
+                        p.ldb2 < p.rep2 * 128 || p.Kb2 % (p.rep2 * 128) != 0))
       return hipErrorInvalidValue;
     return launch_gemm_persist(mode, p, st);
   }
+  if (p.rep2 != 0 || p.ldb2 != 0) return hipErrorInvalidValue;
   Route r = route_for(mode, p.M, p.N, p.K, p.Kb, (sc & 3) == 0, (sc & 15) == 0);
+  if (p.lora_scales) {   // the LoRA epilogue: the streaming kernel only
+    if (mode != MODE_BF16 || !stream_supported(mode, p.M, p.N, p.K, p.Kb, true) || p.accumulate)
+      return hipErrorInvalidValue;
+    return launch_gemm_stream(mode, p, st);
+  }
   if (p.accumulate) r.path = PATH_TILED;   // only the register-staged kernels add into C
   p.ksplit = 1;
   if (r.path == PATH_DECODE) return launch_gemm_decode(mode, p, st);

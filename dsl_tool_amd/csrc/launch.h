@@ -54,6 +54,16 @@ struct GemmArgs {
   // A2 W2^T with A2 [M][Kb2], W2 [N][Kb2] (Kb2 % 128 == 0; 0: none)
   const uint8_t *a2, *b2;
   int Kb2;
+  // ... and W2's own row stride in bytes (0: Kb2) and the period in 128-byte
+  // pairs after which W2's columns repeat (0: none; else a power of two): W2
+  // = [B | B] is then read from B itself
+  int ldb2 = 0, rep2 = 0;
+  // Streaming kernel only, BF16 (the LoRA adapter product T^T = A^T X^T):
+  // v = C[m][n] * lora_scales[m / lora_rank] is stored transposed, as bf16
+  // hi at c[n * ldc + m] and lo = bf16(v - hi) at c[n * ldc + M + m], and
+  // columns [2M, ldc) of those rows are zeroed (no other output)
+  const float *lora_scales = nullptr;
+  int lora_rank = 1;
 };
 
 // LDS-DMA pipelined kernel (FP8_TENSOR / MXFP4, Kb % 64 == 0, no split-K);
@@ -145,7 +155,8 @@ hipError_t launch_moe_combine(const uint16_t *y, int rows_y, int64_t ldy, int n,
 // t32 [M][LR] fp32 (tt: its transpose [LR][M]) -> t2 [M][ld2] bf16:
 // cols [0, LR) hi = bf16(t * s), [LR, 2 LR) lo = bf16(t * s - hi), the rest
 // 0; s = scales[col / rank].
-hipError_t launch_lora_split(const float *t32, int M, int LR, int ld2, int rank, bool tt,
+// t32 [M][LR] -> t2 [M][ld2]: hi | lo of T*s, zero padded.
+hipError_t launch_lora_split(const float *t32, int M, int LR, int ld2, int rank,
                              const float *scales, uint16_t *t2, hipStream_t st);
 // bt [N][LR] -> b2 [N][ld2] = bt | bt | 0.
 hipError_t launch_lora_dup(const uint16_t *bt, int N, int LR, int ld2, uint16_t *b2,

@@ -18,12 +18,17 @@ DEV = "cuda"
 LORA_TOL = 2e-5
 
 
-# T = X A^T is computed transposed on the skinny-M kernels when L*R <= 256
-# and K suits them (L*R = 32, 64, 64, and 16 in the test below); K = 264 and
-# L*R = 320 take the register-staged tiles.
+# T = X A^T is computed transposed on the streaming kernel when L*R <= 256
+# and K suits it (its epilogue writes the scaled hi | lo pair, transposed
+# back); K = 264 and L*R = 320 take the register-staged tiles and a separate
+# split pass.  With L*R = 64, 128 or 256 the base GEMM reads B^T twice
+# instead of a copied B^T | B^T (1, 2 and 4 pairs per row); L*R = 24, 32, 48
+# take the copy (24 and 48 also pad hi | lo to 64 columns).
 @pytest.mark.parametrize("m,n,k,r,l", [(512, 768, 1024, 16, 2), (300, 520, 264, 8, 3),
                                        (4096, 4352, 512, 16, 4), (16, 256, 2048, 64, 1),
-                                       (256, 512, 1024, 64, 5)])
+                                       (256, 512, 1024, 64, 5), (1024, 1024, 4096, 16, 4),
+                                       (512, 640, 4096, 32, 4), (256, 1000, 2048, 64, 4),
+                                       (300, 520, 3072, 24, 2), (700, 260, 2048, 8, 3)])
 def test_lora_fused_gemm(m, n, k, r, l):
     x = W.randn_bf16((m, k), 500)
     w = W.randn_bf16((n, k), 501, 0.05)
