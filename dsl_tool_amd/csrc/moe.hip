@@ -272,6 +272,59 @@ __global__ __launch_bounds__(256) void moe_permute_quant_kernel(
   }
 }
 
+// The same with 16 elements per thread (k % 16 == 0): 128 threads, each
+// chunk read as two 16-byte loads and written as one 16-byte store of codes
+// per routed row.  Per element it is the same arithmetic, so the codes and
+// scales are identical.
+template <int CPL>
+__global__ __launch_bounds__(128) void moe_permute_quant16_kernel(
+    const uint16_t *__restrict__ x, int64_t ldx, int k_dim, const int32_t *__restrict__ dest,
+    int topk, int rows, uint8_t *__restrict__ qx, float *__restrict__ sx) {
+  __shared__ float sh[2];
+  const int t = blockIdx.x;
+  const int nch = k_dim >> 4;
+  const uint4 *xr = reinterpret_cast<const uint4 *>(x + (int64_t)t * ldx);
+  uint4 xa[CPL][2];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = threadIdx.x + 128 * j;
+    xa[j][0] = c < nch ? xr[2 * c] : make_uint4(0, 0, 0, 0);
+    xa[j][1] = c < nch ? xr[2 * c + 1] : make_uint4(0, 0, 0, 0);
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      float f[8];
+      unpack8(xa[j][h], f);
+      m = fmaxf(m, amax8(f));
+    }
+  const float s = fp8_scale_of(block_max(m, sh));
+  const float r = rcp_approx(s);
+  uint4 q[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    float f[8];
+    unpack8(xa[j][0], f);
+    const uint2 lo = e4m3_quot8(f, s, r);
+    unpack8(xa[j][1], f);
+    const uint2 hi = e4m3_quot8(f, s, r);
+    q[j] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+  }
+  for (int slot = 0; slot < topk; ++slot) {
+    const int row = dest[(int64_t)t * topk + slot];
+    if (row < 0 || row >= rows) continue;                // uniform across the block
+    if (threadIdx.x == 0) sx[row] = s;
+    uint4 *qr = reinterpret_cast<uint4 *>(qx + (int64_t)row * k_dim);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = threadIdx.x + 128 * j;
+      if (c < nch) qr[c] = q[j];
+    }
+  }
+}
+
 // out[t] = sum_j w[t, j] * y[dest[t, j]] (dropped slots skipped), fp32 in
 // slot order with separate multiply and add, then bf16 or fp32.
 template <int CPL>
@@ -358,10 +411,19 @@ hipError_t launch_moe_permute_quant(const uint16_t *x, int64_t ldx, int k_dim, i
                                     const int32_t *dest, int topk, int rows, uint8_t *qx, float *sx,
                                     hipStream_t st) {
   if (tokens == 0 || rows == 0) return hipSuccess;
-  by_cpl(k_dim, [&](auto cpl) {
-    moe_permute_quant_kernel<decltype(cpl)::value><<<tokens, 256, 0, st>>>(x, ldx, k_dim, dest, topk,
-                                                                           rows, qx, sx);
-  });
+  if (k_dim % 16 == 0 && ldx % 8 == 0) {
+    // 16-element chunks over 128 threads: the chunk count per thread is
+    // that of 8-element chunks over 256
+    by_cpl(k_dim, [&](auto cpl) {
+      moe_permute_quant16_kernel<decltype(cpl)::value><<<tokens, 128, 0, st>>>(x, ldx, k_dim, dest,
+                                                                               topk, rows, qx, sx);
+    });
+  } else {
+    by_cpl(k_dim, [&](auto cpl) {
+      moe_permute_quant_kernel<decltype(cpl)::value><<<tokens, 256, 0, st>>>(x, ldx, k_dim, dest,
+                                                                             topk, rows, qx, sx);
+    });
+  }
   return hipGetLastError();
 }
 
