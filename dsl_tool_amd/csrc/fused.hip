@@ -25,7 +25,16 @@ DSL_DEV float wave_sum(float v) {
   return v;
 }
 
-DSL_DEV float round_bf16(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+// y[e] rounded to bf16 (nearest even) and widened back, two at a time by
+// the hardware pack (pack_bf16x2: the same bits as f32_to_bf16).
+DSL_DEV void round_bf16x8(float *y) {
+#pragma unroll
+  for (int e = 0; e < 8; e += 2) {
+    const uint32_t pk = pack_bf16x2(y[e], y[e + 1]);
+    y[e] = u2f(pk << 16);
+    y[e + 1] = u2f(pk & 0xffff0000u);
+  }
+}
 
 // 1 / (1 + e^-g) from the hardware 2^x and reciprocal (each within about an
 // ulp): a few ulp of fp32 from the IEEE form, far below the bf16 rounding of
@@ -123,7 +132,8 @@ __global__ __launch_bounds__(256) void rmsnorm_quant_kernel(const FusedArgs p) {
       unpack8(wa[j][0], w);
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) y[e] = round_bf16((y[e] * rinv) * w[e]);
+    for (int e = 0; e < 8; ++e) y[e] = (y[e] * rinv) * w[e];
+    round_bf16x8(y);
     if (p.y && ok) store_y(p, row, c, y);
     if constexpr (QF == QF_FP8_G128) emit_chunk<QF, 16>(p, row, c, ok, (tid & 15) == 0, y);
     else emit_chunk<QF, 4>(p, row, c, ok, (tid & 3) == 0, y);
@@ -173,8 +183,9 @@ __global__ __launch_bounds__(256) void swiglu_quant_kernel(const FusedArgs p, ui
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float g = y[j][e];
-          y[j][e] = round_bf16((g * sigmoid_fast(g)) * u[e]);
+          y[j][e] = (g * sigmoid_fast(g)) * u[e];
         }
+        round_bf16x8(y[j]);
         m = fmaxf(m, amax8(y[j]));
       }
       m = team_max<TL>(m);
