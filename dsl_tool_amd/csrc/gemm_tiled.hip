@@ -207,6 +207,7 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   static const bool stream_on = !env_off("DSL_GEMM_STREAM");
   const char *skinny = getenv("DSL_GEMM_SKINNY");      // read per launch (tests switch it)
   const bool skinny_stream = skinny && strcmp(skinny, "stream") == 0;
+  const bool skinny_decode = skinny && strcmp(skinny, "decode") == 0;
   static const bool persist_on = !env_off("DSL_GEMM_PERSIST");
   static const int pipe_forced = [] {
     if (env_off("DSL_GEMM_PIPE")) return -2;
@@ -215,11 +216,28 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   }();
   Route r{PATH_TILED, -1, plan_for(M, N, Kb)};
   const bool streamable = stream_on && stream_supported(mode, M, N, K, Kb, sc16);
-  // the decode kernel holds M <= 16 rows of A in registers and was the
-  // faster one there (M = 16: 7.8 against 8.1 us); the streaming kernel
-  // wins at M = 1 (11.7 against 13.5) and 17..32 (8.7 against 10.9)
-  // NVFP4: the GEMV for M <= 4, the streaming kernel above that
-  const bool prefer_stream = skinny_stream || (mode == MODE_NVFP4 ? M > 4 : (M == 1 || M > 16));
+  // Skinny M (measured, graph timing over rotating weights): the streaming
+  // kernel is the faster one for M <= 8 (FP8, MXFP4: 4-25%), for bf16 at
+  // every M <= 16 (5-26%), and at M = 9..16 wherever the decode kernel's
+  // 32-row grid leaves CUs idle or needs a second round (N = 4096: 5.3
+  // against 6.1 us, N = 14336: 11.4 against 13.1).  The decode kernel keeps
+  // 9 <= M <= 16 when that grid fills 7/8 of the CUs or more in one round
+  // (N = 7168: 7.1 against 7.4 us, N = 8192).  NVFP4: the GEMV for M <= 4,
+  // the streaming kernel above that.  DSL_GEMM_SKINNY=stream|decode forces
+  // one of them (tests).
+  bool prefer_stream;
+  if (skinny_stream) {
+    prefer_stream = true;
+  } else if (skinny_decode) {
+    prefer_stream = false;
+  } else if (mode == MODE_NVFP4) {
+    prefer_stream = M > 4;
+  } else if (M <= 8 || M > 16 || mode == MODE_BF16) {
+    prefer_stream = true;
+  } else {
+    const int64_t g = (N + 31) / 32, cus = device_cu_count();
+    prefer_stream = !(8 * g >= 7 * cus && g <= cus);
+  }
   if (decode_on && !(prefer_stream && streamable) && decode_supported(mode, M, K, Kb, sc4, sc16)) {
     r.path = PATH_DECODE;
     return r;

@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import formats as OF
 from oracle import gemm as OG
 from oracle import quant as OQ
 from dsl_tool_amd import gemm as G
@@ -345,9 +346,11 @@ def test_fp8_mfma_accumulation_bound():
 
 
 # ------------------------------------------------ skinny-M decode kernel --
-# The decode kernel serves 2 <= M <= 16 (32 W rows per workgroup; ragged N
-# such as 5000, 6200 and 7184 leave a partial last workgroup), the streaming
-# kernel M = 1 and 17..32.
+# Skinny M runs on the streaming kernel, except 9 <= M <= 16 (not bf16)
+# where the decode kernel's 32-row grid fills most CUs in one round (here
+# N = 7168 and 7184); test_decode_kernel_forced below runs every shape on the
+# decode kernel (32 W rows per workgroup; ragged N such as 5000, 6200 and
+# 7184 leave a partial last workgroup).
 DECODE_SHAPES = [(1, 1000, 4096), (7, 2048, 1024), (16, 7168, 4096), (32, 1040, 2048),
                  (17, 48, 8192), (16, 7184, 12288), (5, 16, 3072), (16, 5000, 2048),
                  (9, 6200, 1024)]
@@ -385,6 +388,36 @@ def test_mxfp4_decode(m, n, k):
     c = G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4")
     ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
     assert_close(c, ref, what=f"mxfp4 decode {m}x{n}x{k}")
+
+
+# The decode kernel on shapes the default routing gives to the streaming
+# kernel (DSL_GEMM_SKINNY=decode, read at every launch).
+@pytest.mark.parametrize("m,n,k", [(2, 4096, 4096), (7, 2048, 1024), (8, 1000, 2048), (16, 5000, 2048),
+                                   (9, 6200, 1024), (5, 16, 3072), (32, 1040, 2048), (16, 14336, 1024)])
+@pytest.mark.parametrize("mode", ["tensor", "block", "mxfp4", "bf16"])
+def test_decode_kernel_forced(mode, m, n, k, monkeypatch):
+    monkeypatch.setenv("DSL_GEMM_SKINNY", "decode")
+    a = W.randn_bf16((m, k), 631)
+    w = W.randn_bf16((n, k), 632, 0.02)
+    if mode == "tensor":
+        qa, sa = Q.quant_fp8_tensor(a.to(DEV))
+        qw, sw = Q.quant_fp8_tensor(w.to(DEV))
+        c = G.fp8_gemm_packed(qa, qw, sa, sw)
+        ref = OG.ref_fp8_per_tensor(np_u8(qa), np_f32(sa)[0], np_u8(qw), np_f32(sw)[0])
+    elif mode == "block":
+        qa, sa = Q.quant_fp8_blocks(a.to(DEV), 1, 128)
+        qw, sw = Q.quant_fp8_blocks(w.to(DEV), 128, 128)
+        c = G.fp8_gemm_packed(qa, qw, sa, sw, block=True)
+        ref = OG.ref_fp8_groupwise(np_u8(qa), np_f32(sa), np_u8(qw), np_f32(sw))
+    elif mode == "mxfp4":
+        qa, ea = Q.quant_mxfp4(a.to(DEV))
+        qw, ew = Q.quant_mxfp4(w.to(DEV))
+        c = G.fp4_gemm_packed(qa, ea, qw, ew, fmt="mxfp4")
+        ref = OG.ref_mxfp4(np_u8(qa), np_u8(ea), np_u8(qw), np_u8(ew))
+    else:
+        c = G.bf16_gemm(a.to(DEV), w.to(DEV).t(), out_dtype=torch.bfloat16)
+        ref = OF.round_to_bf16(OG.ref_bf16(a.float().numpy(), w.float().numpy()))
+    assert_close(c, ref, what=f"{mode} forced decode {m}x{n}x{k}")
 
 
 # NVFP4 with M <= 4 and M * K/2048 <= 8 runs the GEMV kernel, 5 <= M <= 256
@@ -573,7 +606,7 @@ def test_mid_m_block_and_mxfp4(m, n, k, mode):
 
 # The streaming kernel on every tile shape: 16-, 32- and 64-row activation
 # blocks with one, two or four 16-row W tiles per workgroup, ragged M and N.
-# DSL_GEMM_SKINNY=stream moves 2 <= M <= 16 (NVFP4: M <= 4) onto it as well, and
+# DSL_GEMM_SKINNY=stream moves all of 2 <= M <= 16 (NVFP4: M <= 4) onto it, and
 # DSL_GEMM_STREAM_TN forces the W tiles (both read at every launch).
 STREAM_SHAPES = [("tensor", 16, 7168, 4096), ("block", 16, 7168, 4096), ("mxfp4", 16, 8192, 8192),
                  ("tensor", 1, 1000, 4096), ("block", 32, 1040, 2048), ("mxfp4", 7, 2048, 1024),
