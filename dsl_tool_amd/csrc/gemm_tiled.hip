@@ -248,7 +248,13 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   }
   if (mode == MODE_BF16) {   // persistent kernel or the register-staged tiles
     const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-    if (persist_on && t256 >= 240 && persist_supported(mode, M, N, K, Kb, sc16))
+    // one partial round of the persistent kernel beats the register-staged
+    // tiles from about a sixth of the CUs' worth of 256x256 tiles (M=768
+    // N=4096 K=4096: 77 against 102 us; M=2048 N=7168: 104 against 220) and
+    // about 2.4M outputs (M=288 N=7168, 56 tiles of which 28 hold 32 rows:
+    // 77 against 70 us; M=384: 78 against 89)
+    if (persist_on && 6 * t256 >= device_cu_count() && (int64_t)M * N >= 2400000 &&
+        persist_supported(mode, M, N, K, Kb, sc16))
       r.path = PATH_PERSIST;
     return r;
   }
@@ -256,12 +262,23 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   if (pipe_ok) {
     const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
     const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
-    if (t256 >= 240) {
+    // Rounds of tiles per CU: a round of 256x256 persistent tiles costs
+    // about as much as 1.6 rounds of the 128x128 pipelined tiles (1.5-2 with
+    // block scales), so the persistent kernel takes over once the 128x128
+    // grid needs twice its rounds (three times with block scales); below
+    // that the 128x128 tiles, down to 40 of them: one round of those beats
+    // the register-staged split-K tiles by 1.3-4.6x (M=300 N=5000 K=4096:
+    // 24 against 67 us; block 31 against 149).  Measured at N = 512..14336,
+    // K = 4096 and 8192, M = 288..3072.
+    const int64_t cus = device_cu_count();
+    const int64_t r128 = (t128 + cus - 1) / cus, r256 = (t256 + cus - 1) / cus;
+    const bool persist_wins = t256 >= 240 || r128 >= (mode == MODE_FP8_BLOCK ? 3 : 2) * r256;
+    if (persist_wins) {
       r.path = PATH_PIPE;
-      r.variant = pipe_forced >= 0 ? pipe_forced : 0;
+      r.variant = pipe_forced >= 0 ? pipe_forced : (t256 >= 240 ? 0 : 1);
       if (persist_on && pipe_forced < 0 && persist_supported(mode, M, N, K, Kb, sc16))
         r.path = PATH_PERSIST;
-    } else if (M > 64 && N > 64 && t128 >= 200) {
+    } else if (M > 64 && N > 64 && t128 >= 40) {
       r.path = PATH_PIPE;
       r.variant = 1;
     }
