@@ -215,7 +215,20 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
     return (e && e[0] >= '1' && e[0] <= '9' && !e[1]) ? e[0] - '0' : -1;
   }();
   Route r{PATH_TILED, -1, plan_for(M, N, Kb)};
-  const bool streamable = stream_on && stream_supported(mode, M, N, K, Kb, sc16);
+  bool streamable = stream_on && stream_supported(mode, M, N, K, Kb, sc16);
+  // The streaming kernel's time grows with the number of 64-row activation
+  // blocks times N (each block streams all of W, and each W slice re-reads
+  // its activation rows), while the 128x128 / persistent tiles stay at about
+  // one round up to a few thousand rows.  Measured at K = 4096, N = 4096,
+  // 14336, 28672, M = 48..256 (the crossover does not move with K: both
+  // sides scale with it): past ceil(M/64) * N = 9 x 4096 (FP8 per-tensor,
+  // MXFP4), 7 x 4096 (FP8 block) or 18 x 4096 (bf16) the tiles are faster
+  // (FP8 block M=256 N=14336: 31.8 against 58.1 us).
+  if (streamable && !skinny_stream && M > 32 && mode != MODE_NVFP4) {
+    const int64_t span = (int64_t)((M + 63) / 64) * N;
+    const int64_t thr = mode == MODE_FP8_BLOCK ? 7 : (mode == MODE_BF16 ? 18 : 9);
+    if (span >= thr * 4096) streamable = false;
+  }
   // Skinny M (measured, graph timing over rotating weights): the streaming
   // kernel is the faster one for M <= 8 (FP8, MXFP4: 4-25%), for bf16 at
   // every M <= 16 (5-26%), and at M = 9..16 wherever the decode kernel's
