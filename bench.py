@@ -173,8 +173,10 @@ def build_cases(names, dev):
         return Case(name, 2.0 * m * n * k, nbytes, PEAK_BF16_TFLOPS, bound, launch, rot,
                     f"bf16 M={m} N={n} K={k}, fp32 out (bf16 MFMA peak)")
 
-    def grouped_case(name):
-        x, w, offsets, counts = W.moe_problem()
+    def grouped_case(name, tokens=4096):
+        """Config 5's grouped GEMM; with few tokens (MoE decode) it streams the
+        non-empty experts' weights and is HBM-bound."""
+        x, w, offsets, counts = W.moe_problem(tokens=tokens)
         T, K = x.shape
         E, Nn, _ = w.shape
         qx, sx = Q.quant_fp8_blocks(x.to(dev), 1, K)
@@ -193,9 +195,10 @@ def build_cases(names, dev):
         nonempty = int((counts > 0).sum())
         flops = 2.0 * T * Nn * K
         nbytes = T * K + nonempty * Nn * K + 4 * T + 4 * nonempty * Nn + 2 * T * Nn
-        return Case(name, flops, nbytes, PEAK_FP8_TFLOPS, "mfma", launch, rot,
-                    f"grouped fp8 MoE E={E} T={T} N={Nn} K={K} ({E - nonempty} empty), "
-                    f"{rot} weight copies rotated")
+        return Case(name, flops, nbytes, PEAK_FP8_TFLOPS, "mfma" if tokens >= 1024 else "hbm", launch,
+                    rot, f"grouped fp8 MoE E={E} T={T}"
+                    + (f" ({tokens} tokens x top-8, decode)" if tokens < 1024 else "")
+                    + f" N={Nn} K={K} ({E - nonempty} empty), {rot} weight copies rotated")
 
     def quant_case(name, kind, r, k):
         """One quantize/pack pass over a bf16 [r, k] operand resident in HBM."""
@@ -373,6 +376,7 @@ def build_cases(names, dev):
         "nvfp4_m1": lambda: fp4_case("nvfp4_m1", 1, 14336, 4096, "nvfp4"),
         "nvfp4_m2048": lambda: fp4_case("nvfp4_m2048", 2048, 14336, 4096, "nvfp4"),
         "grouped_moe": lambda: grouped_case("grouped_moe"),
+        "grouped_moe_decode": lambda: grouped_case("grouped_moe_decode", tokens=32),
         "bf16_8192": lambda: bf16_case("bf16_8192", 8192, 8192, 8192),
         "bf16_m4096": lambda: bf16_case("bf16_m4096", 4096, 7168, 4096),
         "bf16_m16": lambda: bf16_case("bf16_m16", 16, 7168, 4096),
@@ -401,7 +405,7 @@ def build_cases(names, dev):
 
 ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor_cfg1",
              "fp8_tensor_8192",
-             "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe",
+             "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe", "grouped_moe_decode",
              "bf16_8192", "bf16_m4096", "bf16_m16",
              "rmsnorm_quant_fp8", "rmsnorm_then_quant_fp8", "swiglu_quant_fp8", "swiglu_then_quant_fp8",
              "moe_route", "moe_permute_quant", "moe_combine", "moe_layer_cfg5", "lora_m4096", "bf16_4096",

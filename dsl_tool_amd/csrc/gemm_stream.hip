@@ -96,21 +96,18 @@ struct StreamRegs {
   v4f acc[Cfg::TN][Cfg::TMA];
 };
 
+// One workgroup's tile: C rows [m0, m0 + BM) x columns [n0, n0 + BN) of the
+// problem p over all of K.  gsx / gsw (grouped FP8): the output is (acc *
+// gsx[row]) * gsw[col] instead of the per-tensor scaling.
 template <class Cfg>
-__global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) {
+DSL_DEV void stream_tile(const GemmArgs &p, const int m0, const int n0, const float *gsx,
+                         const float *gsw) {
   constexpr int TMA = Cfg::TMA, TN = Cfg::TN, NW = Cfg::NW, P = Cfg::P, DPI = Cfg::DPI;
   constexpr int NR = Cfg::NR, CHUNK = Cfg::CHUNK, SROW = Cfg::SROW;
   __shared__ __align__(16) uint8_t lds[Cfg::LDS];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r16 = lane & 15, g = lane >> 4;
-  // workgroup -> (M block, N block); the M blocks of one W slice are 8 apart
-  const int nmb = (p.M + Cfg::BM - 1) / Cfg::BM;
-  const int nnb = (p.N + Cfg::BN - 1) / Cfg::BN;
-  const int local = blockIdx.x >> 3;
-  const int mblk = local % nmb, nblk = (local / nmb) * 8 + (blockIdx.x & 7);
-  if (nblk >= nnb) return;                   // whole workgroup: no barrier reached
-  const int m0 = mblk * Cfg::BM, n0 = nblk * Cfg::BN;
   const int nchunks = p.Kb / CHUNK;
   const int c_begin = nchunks * wave / NW, c_end = nchunks * (wave + 1) / NW;
   const int nitems = (c_end - c_begin) * P;
@@ -356,7 +353,11 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) 
 
   const int row = m0 + lrow, col0 = n0 + lcol;
   if (row >= p.M) return;
-  if constexpr (Cfg::MODE == MODE_FP8_TENSOR || Cfg::NV) {   // NVFP4: the global scales
+  if (gsx) {                                 // grouped: (acc * sx[row]) * sw[col]
+    const float sxr = gsx[row];
+#pragma unroll
+    for (int c = 0; c < CPT; ++c) v[c] = (v[c] * sxr) * gsw[col0 + c < p.N ? col0 + c : p.N - 1];
+  } else if constexpr (Cfg::MODE == MODE_FP8_TENSOR || Cfg::NV) {   // NVFP4: the global scales
     const float s1 = *p.ga, s2 = *p.gb;
 #pragma unroll
     for (int c = 0; c < CPT; ++c) v[c] = (v[c] * s1) * s2;
@@ -384,6 +385,92 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) 
       for (int c = 0; c < CPT && col0 + c < p.N; ++c) dst[c] = f32_to_bf16(v[c]);
     }
   }
+}
+
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) {
+  // workgroup -> (M block, N block); the M blocks of one W slice are 8 apart
+  const int nmb = (p.M + Cfg::BM - 1) / Cfg::BM;
+  const int nnb = (p.N + Cfg::BN - 1) / Cfg::BN;
+  const int local = blockIdx.x >> 3;
+  const int mblk = local % nmb, nblk = (local / nmb) * 8 + (blockIdx.x & 7);
+  if (nblk >= nnb) return;                   // whole workgroup: no barrier reached
+  stream_tile<Cfg>(p, mblk * Cfg::BM, nblk * Cfg::BN, nullptr, nullptr);
+}
+
+// Grouped FP8 (MoE) on the streaming tiles: workgroup -> (BM-row block of one
+// group's rows, BN-row slice of that group's W).  Each workgroup builds the
+// groups' block prefix from the device offset table (clamped to [0, rows]
+// and made non-decreasing, as the persistent grouped kernel does); blocks
+// past the total exit before any load.  A group's W slice is streamed once
+// per row block, so at decode sizes (a few rows per group) W is read once.
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT) void gemm_stream_grouped_kernel(const GroupedArgs gp) {
+  __shared__ int s_pre[kMaxGroups + 1];      // row blocks before group e
+  __shared__ int s_sum[Cfg::NW];
+  const int tid = threadIdx.x;
+  const int per = (gp.G + Cfg::NT - 1) / Cfg::NT;
+  auto off_of = [&](int e) {                 // offsets clamped to [0, rows], non-decreasing use below
+    int o = gp.offsets[e];
+    return o < 0 ? 0 : (o > gp.rows ? gp.rows : o);
+  };
+  int mine = 0;
+  for (int i = 0; i < per; ++i) {
+    const int e = tid * per + i;
+    if (e < gp.G) {
+      const int lo = off_of(e), hi0 = off_of(e + 1), hi = hi0 < lo ? lo : hi0;
+      mine += (hi - lo + Cfg::BM - 1) / Cfg::BM;
+    }
+  }
+  // exclusive prefix of the threads' sums: a shuffle scan within each wave,
+  // then the earlier waves' totals
+  const int lane = tid & 63, wv = tid >> 6;
+  int incl = mine;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int t = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += t;
+  }
+  if (lane == 63) s_sum[wv] = incl;
+  __syncthreads();
+  int base = 0;
+  for (int w = 0; w < wv; ++w) base += s_sum[w];
+  if (tid == Cfg::NT - 1) s_pre[gp.G] = base + incl;
+  {
+    int run = base + incl - mine;
+    for (int i = 0; i < per; ++i) {
+      const int e = tid * per + i;
+      if (e < gp.G) {
+        s_pre[e] = run;
+        const int lo = off_of(e), hi0 = off_of(e + 1), hi = hi0 < lo ? lo : hi0;
+        run += (hi - lo + Cfg::BM - 1) / Cfg::BM;
+      }
+    }
+  }
+  __syncthreads();
+  const int nnb = (gp.N + Cfg::BN - 1) / Cfg::BN;
+  const int id = blockIdx.x / nnb, nblk = blockIdx.x - id * nnb;
+  if (id >= s_pre[gp.G]) return;             // whole workgroup, before any load
+  int l = 0, u = gp.G - 1;                   // largest group e with s_pre[e] <= id
+  while (l < u) {
+    const int mid = (l + u + 1) >> 1;
+    if (s_pre[mid] <= id) l = mid;
+    else u = mid - 1;
+  }
+  const int e = __builtin_amdgcn_readfirstlane(l);
+  const int lo = off_of(e), hi0 = off_of(e + 1), hi = hi0 < lo ? lo : hi0;
+  GemmArgs q{};
+  q.a = gp.x + (int64_t)lo * gp.K;
+  q.b = gp.w + (int64_t)e * gp.N * gp.K;
+  q.c = static_cast<uint8_t *>(gp.y) + (int64_t)lo * gp.ldy * (gp.out_f32 ? 4 : 2);
+  q.M = hi - lo;
+  q.N = gp.N;
+  q.K = gp.K;
+  q.Kb = gp.K;
+  q.ldc = gp.ldy;
+  q.out_f32 = gp.out_f32;
+  stream_tile<Cfg>(q, (id - s_pre[e]) * Cfg::BM, nblk * Cfg::BN, gp.sx + lo,
+                   gp.sw + (int64_t)e * gp.N);
 }
 
 // ---------------------------------------------------------------- plans --
@@ -444,7 +531,30 @@ hipError_t launch_mode(const GemmArgs &p, const StreamPlan &pl, hipStream_t st) 
   return launch_tn<MODE, 4, 512>(p, pl.tn, st);
 }
 
+template <int TMA, int TN, int CHUNK>
+hipError_t launch_grouped_cfg(const GroupedArgs &gp, hipStream_t st) {
+  using Cfg = StreamCfg<MODE_FP8_TENSOR, TMA, TN, CHUNK, 4>;
+  const int64_t nnb = (gp.N + Cfg::BN - 1) / Cfg::BN;
+  const int64_t blocks = (gp.rows + Cfg::BM - 1) / Cfg::BM + gp.G;   // >= sum of per-group blocks
+  const int64_t grid = blocks * nnb;
+  if (grid >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
+  gemm_stream_grouped_kernel<Cfg><<<(unsigned)grid, Cfg::NT, 0, st>>>(gp);
+  return hipGetLastError();
+}
+
 }  // namespace
+
+bool grouped_stream_supported(const GroupedArgs &gp) {
+  return gp.G >= 1 && gp.G <= kMaxGroups && gp.K % 256 == 0 && gp.K >= 256 && gp.N >= 1;
+}
+
+// Row blocks of 16 or 32 rows by the groups' average size (the router sends
+// averages below 48 here); two 16-row W tiles per workgroup.
+hipError_t launch_grouped_stream(const GroupedArgs &gp, hipStream_t st) {
+  if (!grouped_stream_supported(gp)) return hipErrorInvalidValue;
+  if (gp.rows / gp.G <= 16) return launch_grouped_cfg<1, 2, 256>(gp, st);
+  return launch_grouped_cfg<2, 2, 256>(gp, st);
+}
 
 bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
   if (M < 1 || M > 256 || N < 1) return false;

@@ -114,6 +114,9 @@ hipError_t launch_grouped_fp8(GroupedArgs args, hipStream_t st);
 // Grouped FP8 on the persistent kernel (K % 128 == 0, K < 2^24).
 bool grouped_persist_supported(const GroupedArgs &args);
 hipError_t launch_grouped_persist(const GroupedArgs &args, hipStream_t st);
+// Grouped FP8 on the streaming tiles (few rows per group; K % 256 == 0).
+bool grouped_stream_supported(const GroupedArgs &args);
+hipError_t launch_grouped_stream(const GroupedArgs &args, hipStream_t st);
 
 // -------------------------------------------- fused quantize producers --
 enum { PROD_RMSNORM = 0, PROD_SWIGLU = 1 };

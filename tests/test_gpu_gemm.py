@@ -173,6 +173,39 @@ def test_grouped_variable(counts, n, k):
     assert_close(y, ref, what=f"grouped {counts}")
 
 
+# Few rows per group (MoE decode, fewer than 48 on average): the grouped
+# streaming kernel, 16- or 32-row blocks by the average group size, K % 256
+# == 0.  Zipf-routed counts
+# from 1 to 56 tokens x top-8 over 64 experts (empty experts; the largest
+# groups span several row blocks), ragged N, and hand-made tables with a
+# group far above the average.
+DECODE_MOE = [("zipf", 1, 1536, 2048), ("zipf", 4, 1536, 2048), ("zipf", 32, 1000, 2048),
+              ("zipf", 56, 1536, 1024), ("zipf", 300, 1536, 768), ([0, 3, 0, 0, 200, 1, 0, 9], 384, 512),
+              ([16, 17, 15, 0, 33, 64, 65, 2], 256, 1536)]
+
+
+@pytest.mark.parametrize("case", DECODE_MOE, ids=lambda c: str(c[:2]))
+def test_grouped_stream_decode_sizes(case):
+    if case[0] == "zipf":
+        _, tokens, n, k = case
+        counts = W.moe_counts(tokens=tokens).tolist()
+    else:
+        counts, n, k = case
+    x, w, offsets = _grouped_case(counts, n, k, 711 + len(counts))
+    G_ = len(counts)
+    assert int(offsets[-1]) // G_ < 48              # the streaming kernel's range
+    qx, sx = Q.quant_fp8_blocks(x.to(DEV), 1, k)
+    qw, sw = Q.quant_fp8_blocks(w.reshape(G_ * n, k).to(DEV), 1, k)
+    off_d = torch.from_numpy(offsets).to(DEV)
+    y = G.grouped_fp8_gemm_packed(qx, sx, qw.reshape(G_, n, k), sw.reshape(G_, n), off_d)
+    ref = OG.ref_grouped_fp8(np_u8(qx), np_f32(sx)[:, 0], np_u8(qw).reshape(G_, n, k),
+                             np_f32(sw).reshape(G_, n), offsets)
+    assert_close(y, ref, what=f"grouped stream {case[:2]}")
+    y32 = G.grouped_fp8_gemm_packed(qx, sx, qw.reshape(G_, n, k), sw.reshape(G_, n), off_d,
+                                    out_dtype=torch.float32)
+    assert_close(y32, ref, what=f"grouped stream fp32 {case[:2]}")
+
+
 def test_grouped_registered_variable_and_fixed():
     counts = [7, 0, 60, 33]
     x, w, offsets = _grouped_case(counts, 128, 256, 601)
