@@ -244,10 +244,14 @@ hipError_t launch_grouped_fp8(GroupedArgs p, hipStream_t st) {
   }();
   // Few rows per group (MoE decode): the streaming tiles read each group's W
   // once with its rows (64 experts, N=1536 K=2048, 32 tokens x top-8: 37.4
-  // against 53.3 us); from 64 rows per group the pipelined tiles win again
-  // (512 tokens: 75.3 against 117.9 us).
+  // against 53.3 us); from 64 rows per group the tiles win again (512
+  // tokens: 63.8 us persistent, 117.9 streaming).
   if (avg < 48 && grouped_stream_supported(p)) return launch_grouped_stream(p, st);
-  if (persist_on && avg >= 256 && grouped_persist_supported(p)) return launch_grouped_persist(p, st);
+  // From there on the persistent 256x256 walk, also for groups well below
+  // 256 rows: 64 experts, N=1536 K=2048, 1024 tokens x top-8 (128 rows per
+  // expert): 67.6 against 110.2 us on the 128x256 pipelined tiles; 384
+  // tokens: 63.8 against 71.9.
+  if (persist_on && grouped_persist_supported(p)) return launch_grouped_persist(p, st);
   if (p.K % 64 == 0) {
     // DSL_GROUPED_TILE=256 / 128 forces the 256x256 / 128x256 tile (tuning)
     static const int forced = [] {

@@ -471,9 +471,10 @@ def test_nvfp4_decode(m, n, k):
 
 
 def test_grouped_moe_skewed_counts_pipelined():
-    # Zipf-skewed expert counts (two empty experts), K % 64 == 0 -> pipelined kernel
+    # Zipf-skewed expert counts (two empty experts), K % 64 == 0 but not % 128
+    # -> the pipelined kernel (the persistent one needs whole 128-byte pairs)
     counts = W.moe_counts(num_experts=16, tokens=512, top_k=4, n_empty=2, seed=777).tolist()
-    n, k = 512, 2048
+    n, k = 512, 2112
     x, w, offsets = _grouped_case(counts, n, k, 701)
     G_ = len(counts)
     qx, sx = Q.quant_fp8_blocks(x.to(DEV), 1, k)
@@ -485,17 +486,20 @@ def test_grouped_moe_skewed_counts_pipelined():
     assert_close(y, ref, what=f"grouped MoE {counts}")
 
 
-# Grouped GEMM on the persistent kernel (K % 128 == 0, >= 256 rows per group
+# Grouped GEMM on the persistent kernel (K % 128 == 0, >= 48 rows per group
 # on average): Zipf-skewed experts with empty ones and more tiles than CUs
 # (the tile walk crosses groups inside a workgroup; epilogue scales ride in
 # with each tile's first pair), and a small problem whose grid is not a
 # multiple of 8 (plain tile order) with workgroups that get no tile.
-@pytest.mark.parametrize("case", ["moe", "small"])
+@pytest.mark.parametrize("case", ["moe", "small", "mid"])
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
 def test_grouped_persistent(case, out_dtype):
     if case == "moe":
         counts = W.moe_counts(num_experts=32, tokens=4096, top_k=4, n_empty=3, seed=778).tolist()
         n, k = 1536, 512
+    elif case == "mid":                          # ~100 rows per group: mostly partial tiles
+        counts = W.moe_counts(num_experts=64, tokens=800, top_k=8, seed=779).tolist()
+        n, k = 1536, 1024
     else:
         counts, n, k = [600, 300], 512, 256
     x, w, offsets = _grouped_case(counts, n, k, 721)
