@@ -266,11 +266,13 @@ def build_cases(names, dev):
         return Case(name, flops, nbytes, PEAK_BF16_TFLOPS, "mfma", launch, 1,
                     f"LoRA fused GEMM M={m} N={n} K={k}, {l} adapters of rank {r}, fp32 out")
 
-    def moe_case(name, stage):
+    def moe_case(name, stage, tokens=4096):
         """BASELINE config 5 routing (4096 tokens, top-8 of 64 experts,
         K=2048, N=1536) through the MoE glue: one stage, or the whole
-        projection route -> permute + quantize -> grouped GEMM -> combine."""
-        ids, wts = W.moe_routing()
+        projection route -> permute + quantize -> grouped GEMM -> combine.
+        With few tokens (decode) the experts' weights rotate over copies past
+        the Infinity Cache and the step is timed as a captured graph."""
+        ids, wts = W.moe_routing(tokens=tokens)
         T, k = ids.shape
         E, Nn, K = 64, 1536, 2048
         ids, wts = ids.to(dev), wts.to(dev)
@@ -278,6 +280,9 @@ def build_cases(names, dev):
         w = rnd((E * Nn, K), 10, 0.02)
         qw, sw = Q.quant_fp8_blocks(w, 1, K)
         del w
+        decode = tokens < 1024
+        rot = _rotations(qw.numel()) if decode else 1
+        qws = [qw] + [qw.clone() for _ in range(rot - 1)]
         rows = T * k
         off = torch.empty(E + 1, dtype=torch.int32, device=dev)
         dest = torch.empty(rows, dtype=torch.int32, device=dev)
@@ -297,9 +302,12 @@ def build_cases(names, dev):
             return L.dsl_moe_permute_quant(x.data_ptr(), T, K, K, dest.data_ptr(), k, rows,
                                            qx.data_ptr(), sx.data_ptr(), st)
 
+        it = [0]
+
         def grouped(st):
-            return L.dsl_grouped_fp8_gemm(qx.data_ptr(), qw.data_ptr(), y.data_ptr(), off.data_ptr(),
-                                          E, rows, Nn, K, Nn, N.OUT_BF16, sx.data_ptr(),
+            it[0] += 1
+            return L.dsl_grouped_fp8_gemm(qx.data_ptr(), qws[it[0] % rot].data_ptr(), y.data_ptr(),
+                                          off.data_ptr(), E, rows, Nn, K, Nn, N.OUT_BF16, sx.data_ptr(),
                                           sw.data_ptr(), st)
 
         def combine(st):
@@ -317,7 +325,7 @@ def build_cases(names, dev):
                 if rc:
                     return rc
             return 0
-        counts = W.moe_counts()
+        counts = W.moe_counts(tokens=tokens)
         nonempty = int((counts > 0).sum())
         flops = 2.0 * rows * Nn * K if stage == "layer" else 0.0
         nbytes = {"route": 4 * rows * 3 + 4 * (E + 1),
@@ -329,8 +337,13 @@ def build_cases(names, dev):
                            "scattered to their 32768 routed rows",
                 "combine": "MoE weighted combine of 32768 rows, N=1536 -> 4096 tokens",
                 "layer": "MoE projection cfg5: route + permute/quant + grouped FP8 GEMM + combine"}[stage]
-        return Case(name, flops, nbytes, PEAK_FP8_TFLOPS, "mfma" if stage == "layer" else "hbm",
-                    launch, 1, what)
+        if decode:
+            what = (f"MoE projection at decode size ({tokens} tokens x top-8 over 64 experts, N=1536 "
+                    f"K=2048): route + permute/quant + grouped FP8 GEMM + combine, {rot} weight copies "
+                    f"rotated") if stage == "layer" else what.replace("4096", str(tokens)).replace(
+                        "32768", str(rows))
+        return Case(name, flops, nbytes, PEAK_FP8_TFLOPS,
+                    "mfma" if stage == "layer" and not decode else "hbm", launch, rot, what)
 
     def producer_case(name, kind, r, c, fused=True):
         """RMSNorm / SwiGLU with the output quantized to FP8 1x128 groups:
@@ -390,6 +403,7 @@ def build_cases(names, dev):
         "bf16_4096": lambda: bf16_case("bf16_4096", 4096, 4096, 4096),
         "moe_route": lambda: moe_case("moe_route", "route"),
         "moe_permute_quant": lambda: moe_case("moe_permute_quant", "permute"),
+        "moe_layer_decode": lambda: moe_case("moe_layer_decode", "layer", tokens=32),
         "moe_combine": lambda: moe_case("moe_combine", "combine"),
         "moe_layer_cfg5": lambda: moe_case("moe_layer_cfg5", "layer"),
         "quant_fp8_block128_w": lambda: quant_case("quant_fp8_block128_w", "fp8_block128", 7168, 4096),
@@ -408,7 +422,7 @@ ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor
              "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe", "grouped_moe_decode",
              "bf16_8192", "bf16_m4096", "bf16_m16",
              "rmsnorm_quant_fp8", "rmsnorm_then_quant_fp8", "swiglu_quant_fp8", "swiglu_then_quant_fp8",
-             "moe_route", "moe_permute_quant", "moe_combine", "moe_layer_cfg5", "lora_m4096", "bf16_4096",
+             "moe_route", "moe_permute_quant", "moe_combine", "moe_layer_cfg5", "moe_layer_decode", "lora_m4096", "bf16_4096",
              "quant_fp8_block128_w", "quant_fp8_row128_a", "quant_fp8_tensor_w", "quant_mxfp4_w",
              "quant_nvfp4_w"]
 

@@ -202,15 +202,24 @@ __global__ __launch_bounds__(1024) void moe_route_one_kernel(const int32_t *__re
     tot[e] = s;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {                // exclusive scan over experts (E <= 2048)
-    int s = 0;
-    for (int e = 0; e < E; ++e) {
-      const int c = tot[e];
-      tot[e] = s;
-      offsets[e] = s;
-      s += c;
+  if (w == 0) {                          // exclusive scan over experts, 64 at a time
+    int carry = 0;
+    for (int e0 = 0; e0 < E; e0 += 64) {
+      const int e = e0 + lane;
+      const int c = e < E ? tot[e] : 0;
+      int incl = c;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int t = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += t;
+      }
+      if (e < E) {
+        tot[e] = carry + incl - c;
+        offsets[e] = carry + incl - c;
+      }
+      carry += __shfl(incl, 63, 64);
     }
-    offsets[E] = s;
+    if (lane == 0) offsets[E] = carry;
   }
   __syncthreads();
 #pragma unroll
