@@ -398,8 +398,13 @@ LoraPlan lora_plan(int64_t m, int64_t n, int64_t k, int64_t lr) {
   // T^T = A^T X^T on the streaming kernel when the adapter columns are few
   // enough to be its skinny M; its epilogue writes hi | lo itself.
   p.tt = lr <= 256 && dsl::stream_supported(dsl::MODE_BF16, (int)lr, (int)m, (int)k, (int)(2 * k), true);
+  // One pass (the adapter term as a second K segment of the persistent
+  // kernel) above 256 rows; at skinny and mid M the base GEMM takes its own
+  // (streaming) kernel and the adapter term is added by a second streaming
+  // pass into the fp32 output (M=16 N=K=4096, 4 x rank 16: 79.9 us in one
+  // pass, the base GEMM alone 7.3).
   p.one_pass = dsl::persist_supported(dsl::MODE_BF16, (int)m, (int)n, (int)k, (int)(2 * (k + p.ld2)), true) &&
-               (2 * k) % 128 == 0;
+               (2 * k) % 128 == 0 && m > 256;
   // hi | lo against B^T | B^T without the copy (one pass only): B^T's rows
   // must be whole pairs (64 bf16), a power of two of them, filling ld2 / 2
   const int64_t pr = lr / 64;

@@ -366,10 +366,13 @@ DSL_DEV void stream_tile(const GemmArgs &p, const int m0, const int n0, const fl
     float *dst = static_cast<float *>(p.c) + (int64_t)row * p.ldc + col0;
     if (CPT % 4 == 0 && col0 + CPT <= p.N && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
 #pragma unroll
-      for (int c = 0; c + 3 < CPT; c += 4)
-        *reinterpret_cast<v4f *>(dst + c) = (v4f){v[c], v[c + 1], v[c + 2], v[c + 3]};
+      for (int c = 0; c + 3 < CPT; c += 4) {
+        v4f o = (v4f){v[c], v[c + 1], v[c + 2], v[c + 3]};
+        if (p.accumulate) o = *reinterpret_cast<const v4f *>(dst + c) + o;   // C += result
+        *reinterpret_cast<v4f *>(dst + c) = o;
+      }
     } else {
-      for (int c = 0; c < CPT && col0 + c < p.N; ++c) dst[c] = v[c];
+      for (int c = 0; c < CPT && col0 + c < p.N; ++c) dst[c] = p.accumulate ? dst[c] + v[c] : v[c];
     }
   } else {
     uint16_t *dst = static_cast<uint16_t *>(p.c) + (int64_t)row * p.ldc + col0;
@@ -481,13 +484,14 @@ struct StreamPlan {
 };
 
 // Activation tiles by M (16, 32 or 64 rows per workgroup; 256-byte chunks
-// for the skinny ones, 512-byte chunks otherwise), and the most W tiles
+// for the skinny ones, 512-byte chunks otherwise; rows of an odd number of
+// 256-byte chunks take the 32-row tiles), and the most W tiles
 // per workgroup (4, 2, 1) that still leave >= 192 workgroups: fewer but
 // larger workgroups read A and W fewer times (measured at M = 96..256), as
 // long as they cover most CUs.  DSL_GEMM_STREAM_TN overrides it (tuning).
-StreamPlan plan_for(int mode, int M, int N) {
+StreamPlan plan_for(int mode, int M, int N, int Kb) {
   StreamPlan pl;
-  pl.tma = M <= 16 ? 1 : (M <= 32 ? 2 : 4);
+  pl.tma = M <= 16 ? 1 : ((M <= 32 || Kb % 512 != 0) ? 2 : 4);
   const int64_t nmb = (M + 16 * pl.tma - 1) / (16 * pl.tma);
   pl.tn = 1;
   for (int tn = 4; tn >= 2; tn /= 2)
@@ -558,8 +562,7 @@ hipError_t launch_grouped_stream(const GroupedArgs &gp, hipStream_t st) {
 
 bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
   if (M < 1 || M > 256 || N < 1) return false;
-  const int chunk = M <= 32 ? 256 : 512;
-  if (Kb % chunk != 0) return false;
+  if (Kb % 256 != 0) return false;   // 512-byte chunks where they fit, else 256
   if (mode == MODE_FP8_TENSOR || mode == MODE_BF16) return true;
   // block scales and E8M0 rows move by 16-byte direct loads (K % 512)
   if (mode == MODE_FP8_BLOCK || mode == MODE_MXFP4) return scales16 && K % 512 == 0;
@@ -571,7 +574,8 @@ bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
 hipError_t launch_gemm_stream(int mode, const GemmArgs &p, hipStream_t st) {
   if (p.lora_scales && (mode != MODE_BF16 || p.lora_rank < 1 || p.ldc < 2 * (int64_t)p.M))
     return hipErrorInvalidValue;
-  const StreamPlan pl = plan_for(mode, p.M, p.N);
+  if (p.accumulate && (!p.out_f32 || p.lora_scales)) return hipErrorInvalidValue;
+  const StreamPlan pl = plan_for(mode, p.M, p.N, p.Kb);
   switch (mode) {
     case MODE_FP8_TENSOR: return launch_mode<MODE_FP8_TENSOR>(p, pl, st);
     case MODE_FP8_BLOCK: return launch_mode<MODE_FP8_BLOCK>(p, pl, st);

@@ -202,9 +202,14 @@ struct Route {
   Plan tiled;     // PATH_TILED plan
 };
 
+static bool stream_enabled() {
+  static const bool on = !env_off("DSL_GEMM_STREAM");
+  return on;
+}
+
 static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc16) {
   static const bool decode_on = !env_off("DSL_GEMM_DECODE");
-  static const bool stream_on = !env_off("DSL_GEMM_STREAM");
+  const bool stream_on = stream_enabled();
   const char *skinny = getenv("DSL_GEMM_SKINNY");      // read per launch (tests switch it)
   const bool skinny_stream = skinny && strcmp(skinny, "stream") == 0;
   const bool skinny_decode = skinny && strcmp(skinny, "decode") == 0;
@@ -223,9 +228,11 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   // 14336, 28672, M = 48..256 (the crossover does not move with K: both
   // sides scale with it): past ceil(M/64) * N = 9 x 4096 (FP8 per-tensor,
   // MXFP4), 7 x 4096 (FP8 block) or 18 x 4096 (bf16) the tiles are faster
-  // (FP8 block M=256 N=14336: 31.8 against 58.1 us).
+  // (FP8 block M=256 N=14336: 31.8 against 58.1 us).  Rows of an odd
+  // number of 256-byte chunks stream in 32-row blocks: twice the blocks.
   if (streamable && !skinny_stream && M > 32 && mode != MODE_NVFP4) {
-    const int64_t span = (int64_t)((M + 63) / 64) * N;
+    const int bm = Kb % 512 == 0 ? 64 : 32;
+    const int64_t span = (int64_t)((M + bm - 1) / bm) * N;
     const int64_t thr = mode == MODE_FP8_BLOCK ? 7 : (mode == MODE_BF16 ? 18 : 9);
     if (span >= thr * 4096) streamable = false;
   }
@@ -329,7 +336,14 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
       return hipErrorInvalidValue;
     return launch_gemm_stream(mode, p, st);
   }
-  if (p.accumulate) r.path = PATH_TILED;   // only the register-staged kernels add into C
+  // C += result: the streaming kernel where the router picks a skinny
+  // kernel (fp32 out, one writer per element), else the register-staged
+  // kernels
+  if (p.accumulate)
+    r.path = ((r.path == PATH_STREAM || r.path == PATH_DECODE) && p.out_f32 &&
+              stream_supported(mode, p.M, p.N, p.K, p.Kb, (sc & 15) == 0))
+                 ? PATH_STREAM
+                 : PATH_TILED;
   p.ksplit = 1;
   if (r.path == PATH_DECODE) return launch_gemm_decode(mode, p, st);
   if (r.path == PATH_STREAM) return launch_gemm_stream(mode, p, st);
