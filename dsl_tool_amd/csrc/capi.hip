@@ -389,8 +389,20 @@ struct LoraPlan {
   bool tt;                     // T^T = A^T X^T on the streaming kernel, split in its epilogue
   bool one_pass;               // adapter term as a second K segment of the persistent kernel
   int rep;                     // ... reading B^T twice: its pairs per row (else 0: B^T | B^T copied)
+  bool valu;                   // few tokens: fp32 T and the add on the vector ALUs
+  bool vt;                     // T (as hi | lo) on the vector ALUs, the add on MFMA
   size_t t32, ws, t2, b2, total;
 };
+
+// Most tokens for the vector-ALU add (DSL_LORA_VALU_MAX_M overrides it, for
+// tuning).
+int64_t lora_valu_max_m() {
+  static const int64_t v = [] {
+    const char *e = getenv("DSL_LORA_VALU_MAX_M");
+    return e ? (int64_t)atoll(e) : (int64_t)2;
+  }();
+  return v;
+}
 
 LoraPlan lora_plan(int64_t m, int64_t n, int64_t k, int64_t lr) {
   LoraPlan p;
@@ -407,12 +419,28 @@ LoraPlan lora_plan(int64_t m, int64_t n, int64_t k, int64_t lr) {
                (2 * k) % 128 == 0 && m > 256;
   // hi | lo against B^T | B^T without the copy (one pass only): B^T's rows
   // must be whole pairs (64 bf16), a power of two of them, filling ld2 / 2
+  // Up to 256 tokens T comes from the vector-ALU kernel, which splits A^T's
+  // rows over workgroups (the streaming kernel's T^T runs the 64 adapter rows
+  // as one row block: one workgroup streams all of A^T); for the fewest
+  // tokens the add is on the vector ALUs too, in fp32.
+  p.vt = !p.one_pass && m <= 256 && dsl::lora_valu_supported(m, k, lr);
+  p.valu = p.vt && m <= lora_valu_max_m();
+  if (p.vt) p.tt = false;
+  if (p.valu) {
+    p.tt = p.one_pass = false;
+    p.rep = 0;
+    p.t32 = align256((size_t)(m * lr) * 4);
+    p.ws = align256(dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, n, k));
+    p.t2 = p.b2 = 0;
+    p.total = p.t32 + p.ws;
+    return p;
+  }
   const int64_t pr = lr / 64;
   p.rep = (p.one_pass && lr % 64 == 0 && (pr & (pr - 1)) == 0 && p.ld2 == 2 * lr) ? (int)pr : 0;
   const size_t ws1 = dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, lr, k);
   const size_t ws3 = dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, n, k);
   const size_t ws4 = dsl::gemm_workspace_bytes(dsl::MODE_BF16, m, n, p.ld2, true);
-  p.t32 = p.tt ? 0 : align256((size_t)(m * lr) * 4);
+  p.t32 = (p.tt || p.vt) ? 0 : align256((size_t)(m * lr) * 4);
   p.ws = align256(std::max(ws1, std::max(ws3, ws4)));
   p.t2 = align256((size_t)(m * p.ld2) * 2);
   p.b2 = p.rep ? 0 : align256((size_t)(n * p.ld2) * 2);
@@ -478,14 +506,26 @@ int dsl_lora_gemm(const void *x, const void *w, const void *a_t, const void *b_t
   uint16_t *t2 = reinterpret_cast<uint16_t *>(base + pl.t32 + pl.ws);
   uint16_t *b2 = reinterpret_cast<uint16_t *>(base + pl.t32 + pl.ws + pl.t2);
   hipStream_t st = static_cast<hipStream_t>(stream);
+  hipError_t e;
+  if (pl.valu) {   // few tokens: fp32 T*s, the base GEMM, then Y += T*s B^T
+    e = dsl::launch_lora_t(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(a_t),
+                           (int)m, (int)k, (int)lr, (int)rank, scales, t32, nullptr, 0, st);
+    if (e == hipSuccess) e = dsl::launch_gemm(dsl::MODE_BF16, bf16_args(x, w, y, m, n, k, ldy, false, gws, pl.ws), st);
+    if (e == hipSuccess)
+      e = dsl::launch_lora_apply(t32, static_cast<const uint16_t *>(b_t), y, (int)m, (int)n, (int)lr,
+                                 ldy, st);
+    return hip_status(e, fn);
+  }
   // T = X A^T.  With at most 256 adapter columns it is computed as
   // T^T = A^T X^T: the adapter rows are then the skinny M of the streaming
   // kernel, which reads X once in one launch and whose epilogue writes
   // hi | lo of T*s (transposed back) straight into t2; otherwise (and when
   // K does not suit that kernel) T comes from the register-staged tiles over
   // the workspace and a separate split pass.
-  hipError_t e;
-  if (pl.tt) {
+  if (pl.vt) {
+    e = dsl::launch_lora_t(static_cast<const uint16_t *>(x), static_cast<const uint16_t *>(a_t),
+                           (int)m, (int)k, (int)lr, (int)rank, scales, nullptr, t2, (int)pl.ld2, st);
+  } else if (pl.tt) {
     dsl::GemmArgs tg = bf16_args(a_t, x, t2, lr, m, k, pl.ld2, false, nullptr, 0);
     tg.out_f32 = 0;
     tg.lora_scales = scales;

@@ -159,6 +159,14 @@ hipError_t launch_moe_combine(const uint16_t *y, int rows_y, int64_t ldy, int n,
 // cols [0, LR) hi = bf16(t * s), [LR, 2 LR) lo = bf16(t * s - hi), the rest
 // 0; s = scales[col / rank].
 // t32 [M][LR] -> t2 [M][ld2]: hi | lo of T*s, zero padded.
+// LoRA with few tokens: T = s * X A^T and Y += T B^T on the vector ALUs in
+// fp32 (lora.hip); L*R up to kLoraValuMaxLR.
+constexpr int kLoraValuMaxLR = 512;
+bool lora_valu_supported(int64_t M, int64_t K, int64_t LR);
+hipError_t launch_lora_t(const uint16_t *x, const uint16_t *a_t, int M, int K, int LR, int rank,
+                         const float *scales, float *t, uint16_t *t2, int ld2, hipStream_t st);
+hipError_t launch_lora_apply(const float *t, const uint16_t *b_t, float *y, int M, int N, int LR,
+                             int64_t ldy, hipStream_t st);
 hipError_t launch_lora_split(const float *t32, int M, int LR, int ld2, int rank,
                              const float *scales, uint16_t *t2, hipStream_t st);
 // bt [N][LR] -> b2 [N][ld2] = bt | bt | 0.

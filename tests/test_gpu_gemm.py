@@ -642,14 +642,18 @@ def test_mid_m_block_and_mxfp4(m, n, k, mode):
 
 
 # The streaming kernel on every tile shape: 16-, 32- and 64-row activation
-# blocks with one, two or four 16-row W tiles per workgroup, ragged M and N.
+# blocks with one, two or four 16-row W tiles per workgroup, ragged M and N,
+# 256- and 512-byte chunks.
 # DSL_GEMM_SKINNY=stream moves all of 2 <= M <= 16 (NVFP4: M <= 4) onto it, and
 # DSL_GEMM_STREAM_TN forces the W tiles (both read at every launch).
 STREAM_SHAPES = [("tensor", 16, 7168, 4096), ("block", 16, 7168, 4096), ("mxfp4", 16, 8192, 8192),
                  ("tensor", 1, 1000, 4096), ("block", 32, 1040, 2048), ("mxfp4", 7, 2048, 1024),
                  ("tensor", 96, 7168, 4096), ("block", 200, 1000, 2048), ("mxfp4", 256, 2056, 3072),
                  ("bf16", 24, 1000, 2048), ("nvfp4", 16, 7168, 4096), ("nvfp4", 3, 520, 8192),
-                 ("nvfp4", 200, 1000, 3072), ("nvfp4", 40, 2056, 2048)]
+                 ("nvfp4", 200, 1000, 3072), ("nvfp4", 40, 2056, 2048),
+                 # rows of an odd number of 256-byte chunks: 32-row blocks at any M
+                 ("tensor", 100, 1000, 768), ("mxfp4", 130, 2056, 1536), ("bf16", 200, 700, 1408),
+                 ("nvfp4", 72, 1000, 1536), ("bf16", 256, 520, 128)]
 
 
 @pytest.mark.parametrize("tn", ["1", "2", "4"])

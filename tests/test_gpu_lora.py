@@ -24,15 +24,19 @@ LORA_TOL = 2e-5
 # split pass.  With L*R = 64, 128 or 256 the base GEMM reads B^T twice
 # instead of a copied B^T | B^T (1, 2 and 4 pairs per row); L*R = 24, 32, 48
 # take the copy (24 and 48 also pad hi | lo to 64 columns).  Up to 256 rows
-# the base GEMM runs on its own kernel and the adapter term is added by a
-# second streaming pass into the fp32 result (M = 1, 16, 64, 256; N = 2056
-# leaves a ragged column edge for that pass's scalar epilogue).
+# the base GEMM runs on its own kernel, T*s comes from the vector-ALU kernel
+# (as hi | lo, padded: L*R = 24 at M = 40) and the adapter term is added by a
+# second streaming pass into the fp32 result (M = 8..256; N = 2056 leaves a
+# ragged column edge for that pass's scalar epilogue); M = 1, 2 add it on
+# the vector ALUs in fp32; L*R = 640 at M = 8 takes the register-staged T.
 @pytest.mark.parametrize("m,n,k,r,l", [(512, 768, 1024, 16, 2), (300, 520, 264, 8, 3),
                                        (4096, 4352, 512, 16, 4), (16, 256, 2048, 64, 1),
                                        (256, 512, 1024, 64, 5), (1024, 1024, 4096, 16, 4),
                                        (512, 640, 4096, 32, 4), (256, 1000, 2048, 64, 4),
                                        (300, 520, 3072, 24, 2), (700, 260, 2048, 8, 3),
-                                       (1, 4096, 4096, 16, 4), (64, 2056, 1024, 32, 2)])
+                                       (1, 4096, 4096, 16, 4), (64, 2056, 1024, 32, 2),
+                                       (40, 520, 1024, 8, 3), (2, 1000, 512, 8, 2),
+                                       (8, 512, 1024, 64, 10)])
 def test_lora_fused_gemm(m, n, k, r, l):
     x = W.randn_bf16((m, k), 500)
     w = W.randn_bf16((n, k), 501, 0.05)
