@@ -488,10 +488,14 @@ struct StreamPlan {
 // 256-byte chunks take the 32-row tiles), and the most W tiles
 // per workgroup (4, 2, 1) that still leave >= 192 workgroups: fewer but
 // larger workgroups read A and W fewer times (measured at M = 96..256), as
-// long as they cover most CUs.  DSL_GEMM_STREAM_TN overrides it (tuning).
+// long as they cover most CUs.  DSL_GEMM_STREAM_TMA / DSL_GEMM_STREAM_TN
+// override them (tuning).
 StreamPlan plan_for(int mode, int M, int N, int Kb) {
   StreamPlan pl;
   pl.tma = M <= 16 ? 1 : ((M <= 32 || Kb % 512 != 0) ? 2 : 4);
+  const char *et = getenv("DSL_GEMM_STREAM_TMA");
+  const bool force_tma = et && (et[0] == '1' || et[0] == '2' || (et[0] == '4' && Kb % 512 == 0)) && !et[1];
+  if (force_tma) pl.tma = et[0] - '0';
   const int64_t nmb = (M + 16 * pl.tma - 1) / (16 * pl.tma);
   pl.tn = 1;
   for (int tn = 4; tn >= 2; tn /= 2)
@@ -499,6 +503,16 @@ StreamPlan plan_for(int mode, int M, int N, int Kb) {
       pl.tn = tn;
       break;
     }
+  // 33..64 rows (FP8 per-tensor, bf16): two 32-row blocks of two W tiles
+  // read (32 + 32) K-rows per workgroup against (64 + 16) for one 64-row
+  // block, when that grid is one round of 192 or more workgroups (M=64
+  // N=4096 K=4096: 7.4 against 8.1 us per-tensor, 11.3 against 12.2 bf16;
+  // past one round, and in the block / MXFP4 forms, it measured slower)
+  if (!force_tma && (mode == MODE_FP8_TENSOR || mode == MODE_BF16) && M > 32 && M <= 64 &&
+      pl.tma == 4) {
+    const int64_t g = (int64_t)((M + 31) / 32) * ((N + 31) / 32);
+    if (g >= 192 && g <= device_cu_count()) pl.tma = pl.tn = 2;
+  }
   const char *e = getenv("DSL_GEMM_STREAM_TN");
   if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && !e[1]) pl.tn = e[0] - '0';
   if (pl.tn == 4 && mode == MODE_FP8_BLOCK && pl.tma == 4) pl.tn = 2;   // register budget

@@ -35,6 +35,7 @@ SHAPES = [
     (1, 256, 64),
     (128, 4096, 2048),
     (72, 1000, 512),
+    (48, 4000, 1024),     # 33..64 rows in one round: two 32-row blocks of two W tiles
 ]
 
 
