@@ -83,6 +83,7 @@ def build_cases(names, dev):
     import torch
 
     from dsl_tool_amd import _native as N
+    from dsl_tool_amd import moe as MOE
     from dsl_tool_amd import quant as Q
     from dsl_tool_amd import workloads as W
 
@@ -281,7 +282,7 @@ def build_cases(names, dev):
         qw, sw = Q.quant_fp8_blocks(w, 1, K)
         del w
         decode = tokens < 1024
-        rot = _rotations(qw.numel()) if decode else 1
+        rot = _rotations(qw.numel()) if decode or stage.startswith("grouped") else 1
         qws = [qw] + [qw.clone() for _ in range(rot - 1)]
         rows = T * k
         off = torch.empty(E + 1, dtype=torch.int32, device=dev)
@@ -289,7 +290,11 @@ def build_cases(names, dev):
         src = torch.empty(rows, dtype=torch.int32, device=dev)
         nbw = L.dsl_moe_route_workspace_bytes(T, k, E)
         rws = torch.empty(max(nbw, 4) // 4, dtype=torch.int32, device=dev)
+        # the permuted copy, or (gather form) token-major codes read through
+        # the row map
+        gather = MOE.gather_applies(T, k, E, K)
         qx = torch.empty((rows, K), dtype=torch.uint8, device=dev)
+        qt = torch.empty((T, K), dtype=torch.uint8, device=dev)
         sx = torch.empty(rows, dtype=torch.float32, device=dev)
         y = torch.empty((rows, Nn), dtype=torch.bfloat16, device=dev)
         out = torch.empty((T, Nn), dtype=torch.bfloat16, device=dev)
@@ -302,6 +307,10 @@ def build_cases(names, dev):
             return L.dsl_moe_permute_quant(x.data_ptr(), T, K, K, dest.data_ptr(), k, rows,
                                            qx.data_ptr(), sx.data_ptr(), st)
 
+        def quant_tokens(st):
+            return L.dsl_moe_quant_tokens(x.data_ptr(), T, K, K, dest.data_ptr(), k, rows,
+                                          qt.data_ptr(), sx.data_ptr(), st)
+
         it = [0]
 
         def grouped(st):
@@ -310,14 +319,23 @@ def build_cases(names, dev):
                                           off.data_ptr(), E, rows, Nn, K, Nn, N.OUT_BF16, sx.data_ptr(),
                                           sw.data_ptr(), st)
 
+        def grouped_gather(st):
+            it[0] += 1
+            return L.dsl_moe_grouped_fp8_gemm(qt.data_ptr(), T, src.data_ptr(), qws[it[0] % rot].data_ptr(),
+                                              y.data_ptr(), off.data_ptr(), E, rows, Nn, K, Nn,
+                                              N.OUT_BF16, sx.data_ptr(), sw.data_ptr(), st)
+
         def combine(st):
             return L.dsl_moe_combine(y.data_ptr(), rows, Nn, Nn, dest.data_ptr(), wts.data_ptr(), T, k,
                                      out.data_ptr(), Nn, N.OUT_BF16, st)
         s0 = torch.cuda.current_stream().cuda_stream
-        for f in (route, permute, grouped, combine):     # tables and buffers valid before timing
+        # tables and buffers valid before timing
+        for f in (route, permute, grouped, quant_tokens) + ((grouped_gather,) if gather else ()) + (combine,):
             assert f(s0) == 0
-        stages = {"route": [route], "permute": [permute], "combine": [combine],
-                  "layer": [route, permute, grouped, combine]}[stage]
+        stages = {"route": [route], "permute": [permute], "quant_tokens": [quant_tokens],
+                  "combine": [combine], "grouped": [grouped], "grouped_gather": [grouped_gather],
+                  "layer": [route, quant_tokens, grouped_gather, combine] if gather
+                  else [route, permute, grouped, combine]}[stage]
 
         def launch(i, stream):
             for f in stages:
@@ -327,23 +345,34 @@ def build_cases(names, dev):
             return 0
         counts = W.moe_counts(tokens=tokens)
         nonempty = int((counts > 0).sum())
-        flops = 2.0 * rows * Nn * K if stage == "layer" else 0.0
+        flops = 2.0 * rows * Nn * K if stage in ("layer", "grouped", "grouped_gather") else 0.0
         nbytes = {"route": 4 * rows * 3 + 4 * (E + 1),
                   "permute": 2 * T * K + rows * K + 4 * rows * 2,
+                  "quant_tokens": 2 * T * K + T * K + 4 * rows * 2,
+                  "grouped": rows * K + nonempty * Nn * K + 4 * rows + 4 * nonempty * Nn + 2 * rows * Nn,
+                  "grouped_gather": T * K + 4 * rows + nonempty * Nn * K + 4 * rows
+                                    + 4 * nonempty * Nn + 2 * rows * Nn,
                   "combine": 2 * rows * Nn + 4 * rows * 2 + 2 * T * Nn,
                   "layer": 2 * T * K + nonempty * Nn * K + 2 * T * Nn}[stage]
         what = {"route": "MoE route (stable counting sort) of 4096x8 ids over 64 experts",
                 "permute": "MoE permute + per-row E4M3: 4096 tokens quantized once, K=2048, "
                            "scattered to their 32768 routed rows",
+                "quant_tokens": "MoE per-row E4M3 of 4096 tokens in token order, K=2048, scales "
+                                "to their 32768 routed rows",
                 "combine": "MoE weighted combine of 32768 rows, N=1536 -> 4096 tokens",
-                "layer": "MoE projection cfg5: route + permute/quant + grouped FP8 GEMM + combine"}[stage]
+                "layer": "MoE projection cfg5: route + per-token E4M3 + grouped FP8 GEMM reading A "
+                         "through the row map + combine",
+                "grouped": f"grouped FP8 GEMM of the routed rows (permuted copy), {rot} weight copies "
+                           "rotated",
+                "grouped_gather": f"grouped FP8 GEMM of the routed rows, A read through the row map "
+                                  f"from 4096 token-major rows, {rot} weight copies rotated"}[stage]
         if decode:
             what = (f"MoE projection at decode size ({tokens} tokens x top-8 over 64 experts, N=1536 "
                     f"K=2048): route + permute/quant + grouped FP8 GEMM + combine, {rot} weight copies "
                     f"rotated") if stage == "layer" else what.replace("4096", str(tokens)).replace(
                         "32768", str(rows))
         return Case(name, flops, nbytes, PEAK_FP8_TFLOPS,
-                    "mfma" if stage == "layer" and not decode else "hbm", launch, rot, what)
+                    "mfma" if flops and not decode else "hbm", launch, rot, what)
 
     def producer_case(name, kind, r, c, fused=True):
         """RMSNorm / SwiGLU with the output quantized to FP8 1x128 groups:
@@ -403,6 +432,9 @@ def build_cases(names, dev):
         "bf16_4096": lambda: bf16_case("bf16_4096", 4096, 4096, 4096),
         "moe_route": lambda: moe_case("moe_route", "route"),
         "moe_permute_quant": lambda: moe_case("moe_permute_quant", "permute"),
+        "moe_quant_tokens": lambda: moe_case("moe_quant_tokens", "quant_tokens"),
+        "moe_grouped_permuted": lambda: moe_case("moe_grouped_permuted", "grouped"),
+        "moe_grouped_gather": lambda: moe_case("moe_grouped_gather", "grouped_gather"),
         "moe_layer_decode": lambda: moe_case("moe_layer_decode", "layer", tokens=32),
         "moe_combine": lambda: moe_case("moe_combine", "combine"),
         "moe_layer_cfg5": lambda: moe_case("moe_layer_cfg5", "layer"),
@@ -422,7 +454,8 @@ ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor
              "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe", "grouped_moe_decode",
              "bf16_8192", "bf16_m4096", "bf16_m16",
              "rmsnorm_quant_fp8", "rmsnorm_then_quant_fp8", "swiglu_quant_fp8", "swiglu_then_quant_fp8",
-             "moe_route", "moe_permute_quant", "moe_combine", "moe_layer_cfg5", "moe_layer_decode", "lora_m4096", "bf16_4096",
+             "moe_route", "moe_permute_quant", "moe_quant_tokens", "moe_combine", "moe_grouped_permuted",
+             "moe_grouped_gather", "moe_layer_cfg5", "moe_layer_decode", "lora_m4096", "bf16_4096",
              "quant_fp8_block128_w", "quant_fp8_row128_a", "quant_fp8_tensor_w", "quant_mxfp4_w",
              "quant_nvfp4_w"]
 

@@ -83,7 +83,7 @@ extern "C" {
 
 const char *dsl_last_error(void) { return g_err.c_str(); }
 
-int dsl_abi_version(void) { return 7; }
+int dsl_abi_version(void) { return 8; }
 
 size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
   (void)rows;
@@ -586,24 +586,74 @@ int dsl_moe_route(const int32_t *topk_ids, int64_t tokens, int64_t topk, int64_t
                     fn);
 }
 
-int dsl_moe_permute_quant(const void *x, int64_t tokens, int64_t k, int64_t ldx,
-                          const int32_t *dest, int64_t topk, int64_t rows, uint8_t *qx, float *sx,
-                          void *stream) {
-  const char *fn = "dsl_moe_permute_quant";
+static int run_moe_quant(const char *fn, const void *x, int64_t tokens, int64_t k, int64_t ldx,
+                         const int32_t *dest, int64_t topk, int64_t rows, uint8_t *qx, float *sx,
+                         bool tok_major, void *stream) {
   if (tokens < 0 || rows < 0 || k <= 0 || topk <= 0) return fail(DSL_ERR_ARG, "%s: bad sizes", fn);
   if (k % 8 != 0 || k > 32768)
     return fail(DSL_ERR_ARG, "%s: k=%lld must be a multiple of 8 and <= 32768", fn, (long long)k);
   if (ldx < k || ldx % 8 != 0) return fail(DSL_ERR_ARG, "%s: ldx must be >= k, a multiple of 8", fn);
   if (rows >= ((int64_t)1 << 31) || tokens >= ((int64_t)1 << 31) || tokens * topk >= ((int64_t)1 << 31))
     return fail(DSL_ERR_ARG, "%s: too many rows", fn);
-  if (rows == 0 || tokens == 0) return ok();
+  if (tokens == 0 || (rows == 0 && !tok_major)) return ok();
   int rc;
   if ((rc = check_out(fn, x, "x")) || (rc = check_out(fn, qx, "qx"))) return rc;
-  if (!dest || !sx) return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
+  if (!dest || (rows > 0 && !sx)) return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
   return hip_status(dsl::launch_moe_permute_quant(static_cast<const uint16_t *>(x), ldx, (int)k,
                                                   (int)tokens, dest, (int)topk, (int)rows, qx, sx,
-                                                  static_cast<hipStream_t>(stream)),
+                                                  tok_major, static_cast<hipStream_t>(stream)),
                     fn);
+}
+
+int dsl_moe_permute_quant(const void *x, int64_t tokens, int64_t k, int64_t ldx,
+                          const int32_t *dest, int64_t topk, int64_t rows, uint8_t *qx, float *sx,
+                          void *stream) {
+  return run_moe_quant("dsl_moe_permute_quant", x, tokens, k, ldx, dest, topk, rows, qx, sx, false,
+                       stream);
+}
+
+int dsl_moe_quant_tokens(const void *x, int64_t tokens, int64_t k, int64_t ldx,
+                         const int32_t *dest, int64_t topk, int64_t rows, uint8_t *qx, float *sx,
+                         void *stream) {
+  return run_moe_quant("dsl_moe_quant_tokens", x, tokens, k, ldx, dest, topk, rows, qx, sx, true,
+                       stream);
+}
+
+int dsl_moe_grouped_fp8_gemm(const uint8_t *x, int64_t tokens, const int32_t *src_token,
+                             const uint8_t *w, void *y, const int32_t *offsets, int64_t num_groups,
+                             int64_t total_rows, int64_t n, int64_t k, int64_t ldy, int out_dtype,
+                             const float *sx, const float *sw, void *stream) {
+  const char *fn = "dsl_moe_grouped_fp8_gemm";
+  if (num_groups <= 0 || num_groups > 2048)
+    return fail(DSL_ERR_ARG, "%s: num_groups=%lld must be in [1, 2048]", fn,
+                (long long)num_groups);
+  int rc = check_gemm_dims(fn, total_rows, n, k, ldy, 16, out_dtype);
+  if (rc) return rc;
+  if (tokens < 0 || tokens >= ((int64_t)1 << 24))
+    return fail(DSL_ERR_ARG, "%s: tokens=%lld must be in [0, 2^24)", fn, (long long)tokens);
+  if (total_rows == 0 || n == 0) return ok();
+  if (tokens == 0) return fail(DSL_ERR_ARG, "%s: rows to compute but no tokens", fn);
+  if ((rc = check_out(fn, x, "x")) || (rc = check_out(fn, w, "w"))) return rc;
+  if (!y || !offsets || !sx || !sw || !src_token)
+    return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
+  if (k % 128 != 0 || tokens * k >= ((int64_t)1 << 32))
+    return fail(DSL_ERR_UNSUPPORTED, "%s: needs k %% 128 == 0 and tokens * k < 2^32", fn);
+  dsl::GroupedArgs p;
+  p.x = x;
+  p.w = w;
+  p.y = y;
+  p.offsets = offsets;
+  p.G = (int)num_groups;
+  p.rows = (int)total_rows;
+  p.N = (int)n;
+  p.K = (int)k;
+  p.ldy = ldy;
+  p.sx = sx;
+  p.sw = sw;
+  p.out_f32 = out_dtype == DSL_OUT_F32;
+  p.arow = src_token;
+  p.xrows = (int)tokens;
+  return hip_status(dsl::launch_grouped_persist(p, static_cast<hipStream_t>(stream)), fn);
 }
 
 int dsl_moe_combine(const void *y, int64_t rows, int64_t n, int64_t ldy, const int32_t *dest,

@@ -63,10 +63,11 @@
 
 namespace dsl {
 
-template <int MODE_, bool GROUPED_ = false>
+template <int MODE_, bool GROUPED_ = false, bool GATHER_ = false>
 struct PersCfg {
   static constexpr int MODE = MODE_;
   static constexpr bool GROUPED = GROUPED_;    // FP8 grouped (MoE) tile walk
+  static constexpr bool GATHER = GATHER_;      // grouped: A rows through a row table
   static constexpr int BM = 256, BN = 256, WGM = 2, WGN = 4;
   static constexpr int NW = WGM * WGN, NT = NW * 64, OCC = 2;
   static constexpr int WM = BM / WGM, WN = BN / WGN, TM = WM / 32, TN = WN / 32;
@@ -88,7 +89,10 @@ struct PersCfg {
   // of three slots (the slot of tile t is refilled with tile t+3's first
   // pair, after tile t's epilogue even when a tile is a single pair)
   static constexpr int ES = GROUPED ? 2 * 256 * 4 : 0, NES = 3;
-  static constexpr int LDS = 2 * PAIR + 2 * SQ + NES * ES;
+  // gather: the A-row tables (256 int32) of two tiles
+  static constexpr int TAB = GATHER ? 256 * 4 : 0;
+  static constexpr int TAB_OFF = 2 * PAIR + 2 * SQ + NES * ES;
+  static constexpr int LDS = TAB_OFF + 2 * TAB;
   static constexpr int A_DMA = A_BYTES / 1024, B_DMA = B_BYTES / 1024;
   static constexpr int SA_DMA = SQA / 1024, SB_DMA = SQB / 1024;
   static constexpr int DATA_DMA = A_DMA + B_DMA, SC_DMA = SA_DMA + SB_DMA;
@@ -99,6 +103,7 @@ struct PersCfg {
   static_assert(!BLOCK || (WN <= 128 && 128 % WN == 0), "one weight-scale block per wave");
   static_assert(!GROUPED || MODE == MODE_FP8_TENSOR, "grouped: FP8 with row x channel scales");
   static_assert(!GROUPED || NW == 8, "grouped: one epilogue-scale DMA per wave");
+  static_assert(!GATHER || (GROUPED && A_DMA == 4 * DD), "gather: A copied by waves 0-3");
 };
 
 // One output tile as the kernel sees it: where its A and W rows start, how
@@ -181,13 +186,15 @@ struct Ring {
   uint32_t soff;                 // lane's scale offset
   int wave;
   bool full;
+  bool isA;                      // this wave copies A
+  uint32_t grw[Cfg::GATHER ? Cfg::DD : 1];   // gather, A waves: x row of the lane's DMA j
 
   DSL_DEV void target(const TileRef &tr, int kb_, int wave_, int lane, int kb2_ = 0,
                       int ldb2_ = 0, int rep2_ = 0) {
     wave = wave_;
     nk1 = kb_ / Cfg::PKB;
     full = Cfg::DS > 0 && wave < Cfg::SC_DMA;
-    const bool isA = wave * Cfg::DD < Cfg::A_DMA;
+    isA = wave * Cfg::DD < Cfg::A_DMA;
     kb2 = isA || ldb2_ == 0 ? kb2_ : ldb2_;
     rmask = isA || rep2_ == 0 ? 0x7fffffff : rep2_ - 1;
     lim = (isA ? tr.arows : tr.brows) - 1;
@@ -245,9 +252,38 @@ struct Ring {
           s2 ? dbase2 + (int64_t)((q - nk1) & rmask) * Cfg::PKB : dbase + (int64_t)q * Cfg::PKB;
       dma16(base, __umul24((uint32_t)r, (uint32_t)(s2 ? kb2 : kb)) + ch,
             slot + (uint32_t)((wave * Cfg::DD + j) * 1024));
+    } else if constexpr (Cfg::GATHER) {
+      // A: the row table's x row (dbase is x itself); W: the tile's rows
+      const uint32_t rr = isA ? grw[j] : (uint32_t)r;
+      dma16(dbase + (int64_t)q * Cfg::PKB, __umul24(rr, (uint32_t)kb) + ch,
+            slot + (uint32_t)((wave * Cfg::DD + j) * 1024));
     } else {
       dma16(dbase + (int64_t)q * Cfg::PKB, __umul24((uint32_t)r, (uint32_t)kb) + ch,
             slot + (uint32_t)((wave * Cfg::DD + j) * 1024));
+    }
+  }
+  // gather, A waves, first tile: the x rows straight from the row table in
+  // memory (before any copy is in flight)
+  DSL_DEV void gather_rows_global(const int32_t *arow, int m0, int last, int xrows) {
+    if constexpr (Cfg::GATHER) {
+#pragma unroll
+      for (int j = 0; j < Cfg::DD; ++j) {
+        int r = wrow + j * Cfg::RPI + (int)vsub;
+        r = r < last ? r : last;
+        const uint32_t v = (uint32_t)arow[m0 + r];
+        grw[j] = v < (uint32_t)xrows ? v : (uint32_t)(xrows - 1);
+      }
+    }
+  }
+  // gather, A waves: the x rows of the lane's DMAs from a tile's row table
+  // (clamped to the group's rows when it was copied; x rows to xrows - 1)
+  DSL_DEV void gather_rows(const int32_t *tab, int xrows) {
+    if constexpr (Cfg::GATHER) {
+#pragma unroll
+      for (int j = 0; j < Cfg::DD; ++j) {
+        const uint32_t v = (uint32_t)tab[wrow + j * Cfg::RPI + (int)vsub];
+        grw[j] = v < (uint32_t)xrows ? v : (uint32_t)(xrows - 1);
+      }
     }
   }
   // the wave's scale DMA of tile-local quad c into the quad slot at
@@ -577,7 +613,7 @@ void gemm_persist_kernel(const Args p) {
       tr.m0 = __builtin_amdgcn_readfirstlane(lo + mt * Cfg::BM);
       tr.n0 = nt * Cfg::BN;
       tr.mend = __builtin_amdgcn_readfirstlane(hi);
-      tr.a = p.x + (int64_t)tr.m0 * kb;
+      tr.a = Cfg::GATHER ? p.x : p.x + (int64_t)tr.m0 * kb;   // gather: rows from the table
       tr.b = p.w + ((int64_t)e * p.N + tr.n0) * kb;
       tr.a2 = tr.b2 = nullptr;
       tr.arows = tr.mend - tr.m0;
@@ -600,7 +636,30 @@ void gemm_persist_kernel(const Args p) {
     ring.target(itr, kb, wave, lane, kb2, ldb2, rep2);
     if constexpr (Cfg::SCALED) ring.target_scales(p, itr.m0, itr.n0, lane);
   };
+  // gather: waves 0-3 copy tile t's row table (256 x rows, clamped to its
+  // group's rows) into table slot t % 2, a tile ahead of its use
+  auto copy_table = [&](int t) __attribute__((always_inline)) {
+    if constexpr (Cfg::GATHER) {
+      const TileRef nt = tile_ref(t);
+      const int last = nt.mend - nt.m0 - 1;
+      int k = wave * 64 + pers::lane_id();
+      k = k < last ? k : last;
+      pers::dma4_if(__builtin_amdgcn_readfirstlane((int)(wave < 4)),
+                    reinterpret_cast<const uint8_t *>(p.arow + nt.m0), (uint32_t)k * 4u,
+                    lds0 + (uint32_t)(Cfg::TAB_OFF + (t & 1) * Cfg::TAB + wave * 256));
+    }
+  };
   retarget();
+  if constexpr (Cfg::GATHER) {
+    if (ring.isA) ring.gather_rows_global(p.arow, itr.m0, itr.mend - itr.m0 - 1, p.xrows);
+    if (my_tiles > 1) {
+      copy_table(1);
+      if (nkp == 1) {            // tile 1's first pair is copied in the prologue
+        pipe::wait_vmcnt<0>();
+        __syncthreads();
+      }
+    }
+  }
   auto issue_pair_prep = [&]() __attribute__((always_inline)) {
     if (iq == nkp && it + 1 < my_tiles) {
       iq = 0;
@@ -608,6 +667,14 @@ void gemm_persist_kernel(const Args p) {
       ies = ies == Cfg::NES - 1 ? 0 : ies + 1;
       itr = tile_ref(it);
       retarget();
+      if constexpr (Cfg::GATHER) {
+        // the table copied a tile ago (waited for and published by the
+        // barrier before this point); then the next tile's
+        if (ring.isA)
+          ring.gather_rows(reinterpret_cast<const int32_t *>(smem + Cfg::TAB_OFF + (it & 1) * Cfg::TAB),
+                           p.xrows);
+        if (it + 1 < my_tiles) copy_table(it + 1);
+      }
     }
   };
   auto slot_of = [&](int gp) __attribute__((always_inline)) { return lds0 + (uint32_t)((gp & 1) * Cfg::PAIR); };
@@ -993,8 +1060,8 @@ bool grouped_persist_supported(const GroupedArgs &p) {
 // The device-side tile count is not known here: the grid is one workgroup
 // per CU (at most the tile-count upper bound); workgroups without a tile
 // return before issuing anything.
-hipError_t launch_grouped_persist(const GroupedArgs &p, hipStream_t st) {
-  using Cfg = PersCfg<MODE_FP8_TENSOR, true>;
+template <class Cfg>
+static hipError_t launch_grouped_persist_cfg(const GroupedArgs &p, hipStream_t st) {
   const int nbn = (p.N + Cfg::BN - 1) / Cfg::BN;
   const int64_t upper = ((int64_t)(p.rows + Cfg::BM - 1) / Cfg::BM + p.G) * nbn;
   int64_t grid = device_cu_count();
@@ -1002,6 +1069,16 @@ hipError_t launch_grouped_persist(const GroupedArgs &p, hipStream_t st) {
   if (grid < 1) grid = 1;
   gemm_persist_kernel<Cfg, GroupedArgs><<<(unsigned)grid, Cfg::NT, 0, st>>>(p);
   return hipGetLastError();
+}
+
+hipError_t launch_grouped_persist(const GroupedArgs &p, hipStream_t st) {
+  if (p.arow) {
+    // x rows are addressed by 32-bit offsets row * K
+    if (p.xrows < 1 || (int64_t)p.xrows * p.K >= ((int64_t)1 << 32) || p.xrows >= (1 << 24))
+      return hipErrorInvalidValue;
+    return launch_grouped_persist_cfg<PersCfg<MODE_FP8_TENSOR, true, true>>(p, st);
+  }
+  return launch_grouped_persist_cfg<PersCfg<MODE_FP8_TENSOR, true>>(p, st);
 }
 
 }  // namespace dsl

@@ -109,6 +109,10 @@ struct GroupedArgs {
   const float *sx;       // [rows]
   const float *sw;       // [G][N]
   int out_f32;
+  // gather form: x is [xrows][K] and sorted row r reads x row arow[r]
+  // (persistent kernel only)
+  const int32_t *arow = nullptr;
+  int xrows = 0;
 };
 hipError_t launch_grouped_fp8(GroupedArgs args, hipStream_t st);
 // Grouped FP8 on the persistent kernel (K % 128 == 0, K < 2^24).
@@ -145,10 +149,11 @@ size_t moe_route_workspace_bytes(int64_t assignments, int64_t num_experts);
 hipError_t launch_moe_route(const int32_t *ids, int n, int topk, int E, int32_t *offsets,
                             int32_t *dest, int32_t *src_token, int32_t *ws, hipStream_t st);
 // One workgroup per token; slots whose row is < 0 or >= rows are skipped;
-// k_dim <= 32768.
+// k_dim <= 32768.  tok_major: the codes go once to the token's row of qx
+// ([tokens][k_dim]) and only the scales to the sorted rows.
 hipError_t launch_moe_permute_quant(const uint16_t *x, int64_t ldx, int k_dim, int tokens,
                                     const int32_t *dest, int topk, int rows, uint8_t *qx, float *sx,
-                                    hipStream_t st);
+                                    bool tok_major, hipStream_t st);
 // n <= 32768; slots whose row is < 0 or >= rows_y are skipped.
 hipError_t launch_moe_combine(const uint16_t *y, int rows_y, int64_t ldy, int n, const int32_t *dest,
                               const float *w, int tokens, int topk, void *out, int64_t ldo,

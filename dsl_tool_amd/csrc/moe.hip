@@ -241,7 +241,7 @@ __global__ __launch_bounds__(1024) void moe_route_one_kernel(const int32_t *__re
 template <int CPL>
 __global__ __launch_bounds__(256) void moe_permute_quant_kernel(
     const uint16_t *__restrict__ x, int64_t ldx, int k_dim, const int32_t *__restrict__ dest,
-    int topk, int rows, uint8_t *__restrict__ qx, float *__restrict__ sx) {
+    int topk, int rows, uint8_t *__restrict__ qx, float *__restrict__ sx, int tok_major) {
   __shared__ float sh[4];
   const int t = blockIdx.x;
   const int nch = k_dim >> 3;
@@ -272,7 +272,16 @@ __global__ __launch_bounds__(256) void moe_permute_quant_kernel(
     const int row = dest[(int64_t)t * topk + slot];
     if (row < 0 || row >= rows) continue;                // uniform across the block
     if (threadIdx.x == 0) sx[row] = s;
+    if (tok_major) continue;
     uint8_t *qr = qx + (int64_t)row * k_dim;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = threadIdx.x + 256 * j;
+      if (c < nch) *reinterpret_cast<uint2 *>(qr + (int64_t)c * 8) = q[j];
+    }
+  }
+  if (tok_major) {                                       // codes once, at the token's row
+    uint8_t *qr = qx + (int64_t)t * k_dim;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = threadIdx.x + 256 * j;
@@ -288,7 +297,7 @@ __global__ __launch_bounds__(256) void moe_permute_quant_kernel(
 template <int CPL>
 __global__ __launch_bounds__(128) void moe_permute_quant16_kernel(
     const uint16_t *__restrict__ x, int64_t ldx, int k_dim, const int32_t *__restrict__ dest,
-    int topk, int rows, uint8_t *__restrict__ qx, float *__restrict__ sx) {
+    int topk, int rows, uint8_t *__restrict__ qx, float *__restrict__ sx, int tok_major) {
   __shared__ float sh[2];
   const int t = blockIdx.x;
   const int nch = k_dim >> 4;
@@ -325,7 +334,16 @@ __global__ __launch_bounds__(128) void moe_permute_quant16_kernel(
     const int row = dest[(int64_t)t * topk + slot];
     if (row < 0 || row >= rows) continue;                // uniform across the block
     if (threadIdx.x == 0) sx[row] = s;
+    if (tok_major) continue;
     uint4 *qr = reinterpret_cast<uint4 *>(qx + (int64_t)row * k_dim);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int c = threadIdx.x + 128 * j;
+      if (c < nch) qr[c] = q[j];
+    }
+  }
+  if (tok_major) {                                       // codes once, at the token's row
+    uint4 *qr = reinterpret_cast<uint4 *>(qx + (int64_t)t * k_dim);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
       const int c = threadIdx.x + 128 * j;
@@ -418,19 +436,21 @@ static void by_cpl(int cols, F &&f) {
 
 hipError_t launch_moe_permute_quant(const uint16_t *x, int64_t ldx, int k_dim, int tokens,
                                     const int32_t *dest, int topk, int rows, uint8_t *qx, float *sx,
-                                    hipStream_t st) {
-  if (tokens == 0 || rows == 0) return hipSuccess;
+                                    bool tok_major, hipStream_t st) {
+  if (tokens == 0 || (rows == 0 && !tok_major)) return hipSuccess;
   if (k_dim % 16 == 0 && ldx % 8 == 0) {
     // 16-element chunks over 128 threads: the chunk count per thread is
     // that of 8-element chunks over 256
     by_cpl(k_dim, [&](auto cpl) {
       moe_permute_quant16_kernel<decltype(cpl)::value><<<tokens, 128, 0, st>>>(x, ldx, k_dim, dest,
-                                                                               topk, rows, qx, sx);
+                                                                               topk, rows, qx, sx,
+                                                                               tok_major ? 1 : 0);
     });
   } else {
     by_cpl(k_dim, [&](auto cpl) {
       moe_permute_quant_kernel<decltype(cpl)::value><<<tokens, 256, 0, st>>>(x, ldx, k_dim, dest,
-                                                                             topk, rows, qx, sx);
+                                                                             topk, rows, qx, sx,
+                                                                             tok_major ? 1 : 0);
     });
   }
   return hipGetLastError();

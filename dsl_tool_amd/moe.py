@@ -8,7 +8,12 @@ An MoE FFN projection, on the device end to end:
     out = moe_combine(y, route, topk_weights)       # weighted sum over each token's experts
 
 ``routed_grouped_gemm`` runs the four steps (registered as
-``moe.routed_grouped_gemm``).  The reference has no MoE glue; its grouped
+``moe.routed_grouped_gemm``).  Where the persistent grouped kernel takes the
+GEMM (groups averaging 48 rows or more, K % 128 == 0) the middle two are
+``moe_quant_tokens`` (codes in token order, scales per sorted row) and
+``moe_grouped_fp8_gemm``, which reads each sorted row's A through
+``route.src_token``: the codes are written once per token instead of topk
+times, with the same result bit for bit.  The reference has no MoE glue; its grouped
 GEMM takes rows already sorted by group (cuda/gemm/grouped_gemm.cu:26-32,
 :77-104, triton/gemm/gemm_kernels.py:164-182).  Everything runs in
 ``libdsl_gemm.so``; the sorted order is a stable counting sort, so results
@@ -78,6 +83,62 @@ def moe_permute_quant(x: torch.Tensor, route: Route):
     return qx, sx
 
 
+def moe_quant_tokens(x: torch.Tensor, route: Route):
+    """``x [T, K]`` (bf16) to E4M3 in token order, one scale per row:
+    ``(qx [T, K] uint8, sx [T*topk] float32)`` where ``sx`` holds each
+    token's scale at its sorted rows ``route.dest`` (the input of
+    :func:`moe_grouped_fp8_gemm`; the codes are those of
+    :func:`moe_permute_quant`, not copied per routed row)."""
+    _gpu(x, "x")
+    if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] != route.tokens:
+        raise ValueError("x must be bf16 [tokens, K]")
+    if x.stride(1) != 1:
+        x = x.contiguous()
+    T, K = x.shape
+    rows = T * route.topk
+    qx = torch.empty((T, K), dtype=torch.uint8, device=x.device)
+    sx = torch.empty(rows, dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        N.call("dsl_moe_quant_tokens", N.ptr(x), T, K, x.stride(0), N.ptr(route.dest),
+               route.topk, rows, N.ptr(qx), N.ptr(sx), N.stream_of(x.device))
+    return qx, sx
+
+
+def moe_grouped_fp8_gemm(qx: torch.Tensor, sx: torch.Tensor, route: Route, qw: torch.Tensor,
+                         sw: torch.Tensor, *, out_dtype=torch.bfloat16) -> torch.Tensor:
+    """The grouped GEMM over the routed rows with A read through the row
+    map: sorted row r multiplies token ``route.src_token[r]`` of the
+    token-major codes ``qx [T, K]`` (from :func:`moe_quant_tokens`) with its
+    expert's ``qw [E, N, K]``; ``y [T*topk, N]`` in sorted order, as
+    ``grouped_fp8_gemm_packed`` over the permuted copy gives."""
+    dev = G._require_gpu(qx, qw, sx, sw)
+    qx, qw = G._u8(qx).contiguous(), G._u8(qw).contiguous()
+    T, K = qx.shape
+    E, Nn, K2 = qw.shape
+    if K != K2 or T != route.tokens or E != route.num_experts:
+        raise ValueError("qx [tokens, K] / qw [E, N, K] do not match the route")
+    rows = T * route.topk
+    sx = sx.reshape(-1).float().contiguous()
+    sw = sw.reshape(E, Nn).float().contiguous()
+    if sx.numel() != rows:
+        raise ValueError("sx must have one entry per routed row")
+    y = torch.empty((rows, Nn), dtype=G._as_dtype(out_dtype), device=dev)
+    with torch.cuda.device(dev):
+        N.call("dsl_moe_grouped_fp8_gemm", N.ptr(qx), T, N.ptr(route.src_token), N.ptr(qw),
+               N.ptr(y), N.ptr(route.offsets), E, rows, Nn, K, y.stride(0), G._out_code(y.dtype),
+               N.ptr(sx), N.ptr(sw), N.stream_of(dev))
+    return y
+
+
+def gather_applies(tokens: int, topk: int, num_experts: int, k: int) -> bool:
+    """Whether the routed GEMM reads A through the row map: the persistent
+    grouped kernel (groups averaging 48 rows or more; fewer take the
+    streaming tiles over the permuted copy), k % 128 == 0, tokens < 2^24 and
+    tokens * k < 2^32."""
+    return (k % 128 == 0 and (tokens * topk) // max(num_experts, 1) >= 48
+            and tokens < (1 << 24) and tokens * k < (1 << 32))
+
+
 def moe_combine(y: torch.Tensor, route: Route, topk_weights: torch.Tensor, *,
                 out_dtype=torch.bfloat16) -> torch.Tensor:
     """``out[t] = sum_j topk_weights[t, j] * y[dest[t*topk + j]]`` (fp32 sum)."""
@@ -116,6 +177,11 @@ def routed_grouped_gemm(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: t
         qw, sw = Q.quant_fp8_blocks(wt, 1, K)
         qw, sw = qw.reshape(E, Nn, K), sw.reshape(E, Nn)
     route = moe_route(topk_ids, E)
-    qx, sx = moe_permute_quant(x, route)
-    y = G.grouped_fp8_gemm_packed(qx, sx, qw, sw, route.offsets, out_dtype=torch.bfloat16)
+    if gather_applies(route.tokens, route.topk, E, qw.shape[2]):
+        # token-major codes, A rows through the row map: no permuted copy
+        qx, sx = moe_quant_tokens(x, route)
+        y = moe_grouped_fp8_gemm(qx, sx, route, qw, sw, out_dtype=torch.bfloat16)
+    else:
+        qx, sx = moe_permute_quant(x, route)
+        y = G.grouped_fp8_gemm_packed(qx, sx, qw, sw, route.offsets, out_dtype=torch.bfloat16)
     return moe_combine(y, route, topk_weights, out_dtype=out_dtype)

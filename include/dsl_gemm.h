@@ -247,6 +247,27 @@ int dsl_moe_permute_quant(const void *x, int64_t tokens, int64_t k, int64_t ldx,
                           const int32_t *dest, int64_t topk, int64_t rows,
                           uint8_t *qx, float *sx, void *stream);
 
+/* dsl_moe_permute_quant without the row copies: the codes of token t go
+ * once to row t of qx [tokens][k], and only the scales to the sorted rows
+ * (sx [d] for every d = dest[t*topk+j] with 0 <= d < rows).  The input of
+ * dsl_moe_grouped_fp8_gemm. */
+int dsl_moe_quant_tokens(const void *x, int64_t tokens, int64_t k, int64_t ldx,
+                         const int32_t *dest, int64_t topk, int64_t rows,
+                         uint8_t *qx, float *sx, void *stream);
+
+/* dsl_grouped_fp8_gemm whose sorted row r reads x row src_token[r]: x is
+ * the token-major [tokens][k] E4M3 of dsl_moe_quant_tokens (8x fewer bytes
+ * than the permuted copy at topk = 8), sx the per-sorted-row scales it
+ * wrote, src_token from dsl_moe_route (entries outside [0, tokens) are
+ * clamped).  Same result as dsl_moe_permute_quant + dsl_grouped_fp8_gemm.
+ * k % 128 == 0, tokens < 2^24, tokens * k < 2^32 (else
+ * DSL_ERR_UNSUPPORTED). */
+int dsl_moe_grouped_fp8_gemm(const uint8_t *x, int64_t tokens, const int32_t *src_token,
+                             const uint8_t *w, void *y, const int32_t *offsets,
+                             int64_t num_groups, int64_t total_rows, int64_t n, int64_t k,
+                             int64_t ldy, int out_dtype, const float *sx, const float *sw,
+                             void *stream);
+
 /* out [tokens][ldo] = sum over j of topk_weights[t][j] * y[dest[t*topk+j]]
  * (y [rows][ldy] bf16, the grouped GEMM's output), in fp32 with slot order j
  * and a separate multiply and add per term, then bf16 or fp32.  Slots with

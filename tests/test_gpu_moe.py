@@ -104,3 +104,78 @@ def test_routed_grouped_gemm_end_to_end():
     # term (a rounding flip from the GEMM's own fp32 order) lands whole on a
     # sum that cancels, so only the global north-star bound is meaningful.
     assert_close(out, ref, what="routed grouped gemm", elem_tol=float("inf"))
+
+
+@pytest.mark.parametrize("T,k,E,K,pad", [(300, 4, 9, 2048, 0), (64, 2, 3, 136, 8), (1000, 8, 64, 2048, 0),
+                                         (3, 8, 5, 32768, 16), (1, 1, 1, 8, 0)])
+def test_quant_tokens_matches_oracle(T, k, E, K, pad):
+    # token-major codes; the scales at every sorted row of the token
+    ids = _ids(T, k, E, 440 + T, drop=True)
+    x = W.randn_bf16((T, K), 441) * 3
+    r = M.moe_route(ids.to(DEV), E)
+    xd = x.to(DEV)
+    if pad:
+        xd = torch.nn.functional.pad(xd, (0, pad))[:, :K]
+    qt, sx = M.moe_quant_tokens(xd, r)
+    off, dest, src = OM.route(ids.numpy(), E)
+    q_ref, s_ref = OM.permute_quant(x.float().numpy(), src)
+    n = int(off[-1])
+    assert np.array_equal(np_u8(qt)[src], q_ref)
+    assert np.array_equal(np_f32(sx)[:n], s_ref)
+
+
+def _expert_weights(E, Nn, K, seed):
+    from dsl_tool_amd import quant as Q
+    w = W.randn_bf16((E * Nn, K), seed, 0.02).to(DEV)
+    qw, sw = Q.quant_fp8_blocks(w, 1, K)
+    return qw.reshape(E, Nn, K), sw.reshape(E, Nn)
+
+
+# The gather kernel against the persistent kernel over the permuted copy:
+# the same codes, scales and MFMA order, so the same bits.  K = 128 is one
+# pair per tile (the next tile's row table is waited for before the first
+# copies); ragged N; one expert; config 5's routing and sizes.
+GATHER_CASES = [(512, 4, 16, 1024, 768), (300, 3, 2, 128, 520), (1000, 2, 5, 256, 256),
+                (2000, 1, 1, 384, 300), (4096, 8, 64, 2048, 1536)]
+
+
+@pytest.mark.parametrize("T,k,E,K,Nn", GATHER_CASES)
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_gather_gemm_equals_permuted(T, k, E, K, Nn, out_dtype):
+    from dsl_tool_amd import gemm as G
+    if (T, E) == (4096, 64):
+        ids = W.moe_routing()[0]
+    else:
+        ids = _ids(T, k, E, 450 + T, drop=True)
+    assert M.gather_applies(T, k, E, K)
+    x = (W.randn_bf16((T, K), 451) * 2).to(DEV)
+    qw, sw = _expert_weights(E, Nn, K, 452)
+    r = M.moe_route(ids.to(DEV), E)
+    qt, st = M.moe_quant_tokens(x, r)
+    qp, sp = M.moe_permute_quant(x, r)
+    yg = M.moe_grouped_fp8_gemm(qt, st, r, qw, sw, out_dtype=out_dtype)
+    yp = G.grouped_fp8_gemm_packed(qp, sp, qw, sw, r.offsets, out_dtype=out_dtype)
+    torch.cuda.synchronize()
+    n = int(r.offsets[-1].item())
+    assert torch.equal(yg[:n].view(torch.int16 if out_dtype == torch.bfloat16 else torch.int32),
+                       yp[:n].view(torch.int16 if out_dtype == torch.bfloat16 else torch.int32))
+
+
+def test_gather_gemm_clamps_bad_row_map():
+    # row-map entries outside [0, tokens) read the last token's row
+    from dsl_tool_amd import gemm as G
+    T, k, E, K, Nn = 700, 2, 3, 256, 384
+    ids = _ids(T, k, E, 460)
+    x = W.randn_bf16((T, K), 461).to(DEV)
+    qw, sw = _expert_weights(E, Nn, K, 462)
+    r = M.moe_route(ids.to(DEV), E)
+    qt, st = M.moe_quant_tokens(x, r)
+    bad = r.src_token.clone()
+    bad[5], bad[300], bad[1000] = -7, T, 1 << 30          # first tile, later tiles
+    rb = r._replace(src_token=bad)
+    yg = M.moe_grouped_fp8_gemm(qt, st, rb, qw, sw)
+    qp = qt[bad.clamp(0, T - 1).long()]                    # -7 -> 2^32 - 7 -> last token too
+    qp[5] = qt[T - 1]
+    yp = G.grouped_fp8_gemm_packed(qp, st, qw, sw, r.offsets)
+    torch.cuda.synchronize()
+    assert torch.equal(yg.view(torch.int16), yp.view(torch.int16))
