@@ -561,7 +561,8 @@ int dsl_lora_gemm(const void *x, const void *w, const void *a_t, const void *b_t
 }
 
 size_t dsl_moe_route_workspace_bytes(int64_t tokens, int64_t topk, int64_t num_experts) {
-  if (tokens <= 0 || topk <= 0 || num_experts <= 0) return 0;
+  // tokens == 0 still needs one block's histogram (the offsets are written)
+  if (tokens < 0 || topk <= 0 || num_experts <= 0) return 0;
   return dsl::moe_route_workspace_bytes(tokens * topk, num_experts);
 }
 

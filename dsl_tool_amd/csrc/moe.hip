@@ -15,7 +15,8 @@
 
 namespace dsl {
 
-constexpr int kRouteChunk = 256;      // assignments per block in the count/scatter passes
+constexpr int kRouteChunk = 256;      // assignments per block in the count and scatter passes
+constexpr int kFusedScan = 16384;     // histogram ints each scatter block may read itself
 
 // Pass 1: per-block expert histograms, counts[b][e].
 __global__ __launch_bounds__(256) void moe_count_kernel(const int32_t *__restrict__ ids, int n,
@@ -32,7 +33,7 @@ __global__ __launch_bounds__(256) void moe_count_kernel(const int32_t *__restric
   for (int e = threadIdx.x; e < E; e += 256) counts[(int64_t)blockIdx.x * E + e] = hist[e];
 }
 
-// Pass 2 (one block of 16 x 64 threads): offsets[e] = rows of experts < e;
+// Scan for many blocks (one block of 16 x 64 threads): offsets[e] = rows of experts < e;
 // counts[b][e] is replaced by the first sorted row of block b's expert-e
 // assignments.  Experts go in runs of 64; thread (part, l) owns expert
 // e0 + l over a contiguous range of blocks, so the column sums, the prefix
@@ -86,25 +87,88 @@ __global__ __launch_bounds__(1024) void moe_scan_kernel(int32_t *__restrict__ co
   if (threadIdx.x == 0) offsets[E] = carry;
 }
 
-// Pass 3: stable scatter, one wave per chunk.  The wave walks its chunk 64
-// assignments at a time; the lanes holding the same expert are found with
-// one ballot per expert-id bit, so a lane's rank among the step's earlier
-// same-expert lanes is a popcount, and the step's last such lane advances
-// the expert's next row in LDS (a single wave: LDS operations stay in
-// program order).
-__global__ __launch_bounds__(64) void moe_scatter_kernel(const int32_t *__restrict__ ids, int n,
+// Pass 2: bases and stable scatter, one block of four waves per chunk.
+// With a small histogram (nb x E <= kFusedScan ints) the four waves first
+// form, for each expert e (in runs of 64, thread (q, l) owning expert e0 + l
+// over a quarter of the blocks), the rows of experts < e (offsets[e],
+// written by block 0 for the grouped GEMM) plus the rows of expert e in
+// blocks before this one: the chunk's first sorted row per expert.  Every
+// block reads the whole histogram (L2-resident) instead of waiting for a
+// separate scan launch.  Larger histograms take moe_scan_kernel first
+// (scanned = 1: counts then holds each block's first rows).  Then wave 0 walks the
+// chunk 64 assignments at a time; the lanes holding the same expert are
+// found with one ballot per expert-id bit, so a lane's rank among the
+// step's earlier same-expert lanes is a popcount, and the step's last such
+// lane advances the expert's next row in LDS (a single wave: LDS operations
+// stay in program order).
+__global__ __launch_bounds__(256) void moe_scatter_kernel(const int32_t *__restrict__ ids, int n,
                                                          int E, int topk,
-                                                         const int32_t *__restrict__ base,
+                                                         const int32_t *__restrict__ counts, int nb,
+                                                         int scanned, int32_t *__restrict__ offsets,
                                                          int32_t *__restrict__ dest,
                                                          int32_t *__restrict__ src_token) {
   extern __shared__ int run[];          // [E] next sorted row per expert
-  const int lane = threadIdx.x;
-  for (int e = lane; e < E; e += 64) run[e] = base[(int64_t)blockIdx.x * E + e];
-  __syncthreads();
+  __shared__ int qbefore[4][64], qtot[4][64];
+  const int l = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int blk = blockIdx.x;
+  if (scanned) {                        // the bases are in counts already
+    if (q != 0) return;
+    for (int e = l; e < E; e += 64) run[e] = counts[(int64_t)blk * E + e];
+  } else {
+  const int bpq = (nb + 3) / 4, qb0 = q * bpq, qb1 = min(nb, qb0 + bpq);
+  int carry = 0;                        // wave 0: rows of the experts of earlier runs
+  for (int e0 = 0; e0 < E; e0 += 64) {
+    const int e = e0 + l;
+    int before = 0, tot = 0;
+    if (e < E) {
+      // eight loads in flight per thread (the sums are integers: any order)
+      int b = qb0;
+      for (; b + 8 <= qb1; b += 8) {
+        int c[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) c[u] = counts[(int64_t)(b + u) * E + e];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          tot += c[u];
+          before += b + u < blk ? c[u] : 0;
+        }
+      }
+      for (; b < qb1; ++b) {
+        const int c = counts[(int64_t)b * E + e];
+        tot += c;
+        before += b < blk ? c : 0;
+      }
+    }
+    qbefore[q][l] = before;
+    qtot[q][l] = tot;
+    __syncthreads();
+    if (q == 0) {
+      const int bef = qbefore[0][l] + qbefore[1][l] + qbefore[2][l] + qbefore[3][l];
+      const int tt = qtot[0][l] + qtot[1][l] + qtot[2][l] + qtot[3][l];
+      int incl = tt;                    // inclusive scan over the run's 64 experts
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int v = __shfl_up(incl, d, 64);
+        incl += l >= d ? v : 0;
+      }
+      const int off = carry + incl - tt;
+      if (e < E) {
+        run[e] = off + bef;
+        if (blk == 0) offsets[e] = off;
+      }
+      carry += __shfl(incl, 63, 64);
+    }
+    __syncthreads();                    // qbefore / qtot are rewritten by the next run
+  }
+  if (q != 0) return;
+  if (blk == 0 && l == 0) offsets[E] = carry;
+  }
+  __builtin_amdgcn_wave_barrier();      // wave 0 alone from here: run[] is its own
+  const int lane = l;
   int bits = 0;
   while ((1 << bits) < E + 1) ++bits;   // ids -1 map to E: bits cover 0..E
   const uint64_t below = (1ull << lane) - 1ull;
-  const int a0 = blockIdx.x * kRouteChunk;
+  const int a0 = blk * kRouteChunk;
   constexpr int STEPS = kRouteChunk / 64;
   int idv[STEPS];                       // the chunk's ids, all loads in flight at once
 #pragma unroll
@@ -408,19 +472,23 @@ size_t moe_route_workspace_bytes(int64_t assignments, int64_t num_experts) {
 
 hipError_t launch_moe_route(const int32_t *ids, int n, int topk, int E, int32_t *offsets,
                             int32_t *dest, int32_t *src_token, int32_t *ws, hipStream_t st) {
-  // one launch for small batches (decode-time routing); the three-pass form
-  // spreads the scattered row writes over many CUs and wins beyond that
-  // (32768 assignments: 20 us against 38 us in one workgroup)
+  // one launch for small batches (decode-time routing); the two-pass form
+  // (histograms, then bases + scatter per chunk) spreads the scattered row
+  // writes over many CUs and wins beyond that (32768 assignments: 20 us for
+  // the earlier three passes against 38 us in one workgroup)
   if (n <= 4096 && E <= 2047 && 16 * E * (int)sizeof(int) <= 64 * 1024) {
     moe_route_one_kernel<<<1, 1024, (size_t)16 * E * sizeof(int), st>>>(ids, n, E, topk, offsets,
                                                                         dest, src_token);
     return hipGetLastError();
   }
-  const int nb = n > 0 ? (n + kRouteChunk - 1) / kRouteChunk : 0;
+  // at least one block: with no assignments it still writes the zero offsets
+  const int nb = n > 0 ? (n + kRouteChunk - 1) / kRouteChunk : 1;
   const size_t lds = (size_t)E * sizeof(int);
-  if (nb > 0) moe_count_kernel<<<nb, 256, lds, st>>>(ids, n, E, ws);
-  moe_scan_kernel<<<1, 1024, 0, st>>>(ws, nb, E, offsets);
-  if (nb > 0) moe_scatter_kernel<<<nb, 64, lds, st>>>(ids, n, E, topk, ws, dest, src_token);
+  moe_count_kernel<<<nb, 256, lds, st>>>(ids, n, E, ws);
+  const int scanned = (int64_t)nb * E > kFusedScan;
+  if (scanned) moe_scan_kernel<<<1, 1024, 0, st>>>(ws, nb, E, offsets);
+  moe_scatter_kernel<<<nb, 256, lds, st>>>(ids, n, E, topk, ws, nb, scanned, offsets, dest,
+                                           src_token);
   return hipGetLastError();
 }
 

@@ -25,14 +25,17 @@ def _ids(T, k, E, seed, drop=False):
     return ids
 
 
-# Route paths: one workgroup (<= 4096 assignments), and count + scan +
-# scatter for the rest: 4096 x 8 over 64 experts, 3000 x 6 over 2048, 2100 x 3
-# over 100 (two 64-expert runs of the scan, ragged last chunk), 5000 x 2 over
-# 3, and 40000 x 8 over 256 (more blocks than the scan's 16 ranges cover
-# evenly).
+# Route paths: one workgroup (<= 4096 assignments, <= 1024 experts), and
+# count + scatter for the rest, the scatter blocks forming their own bases
+# from a small histogram (4096 x 8 over 64 experts, 2100 x 3 over 100: two
+# 64-expert runs, ragged last chunk; 5000 x 2 over 3; 200 x 8 over 1100) or
+# after a separate scan of a large one (3000 x 6 over 2048; 40000 x 8 over
+# 256: more blocks than the scan's 16 ranges cover evenly); no assignments
+# over 1500 experts still writes the zero offsets.
 ROUTE_CASES = [(4096, 8, 64, False), (37, 3, 5, True), (1, 1, 1, False), (3000, 6, 2048, True),
                (513, 4, 7, False), (512, 8, 64, True), (1024, 4, 1000, False),
-               (2100, 3, 100, True), (5000, 2, 3, False), (40000, 8, 256, True)]
+               (2100, 3, 100, True), (5000, 2, 3, False), (40000, 8, 256, True),
+               (0, 4, 1500, False), (200, 8, 1100, True)]
 
 
 @pytest.mark.parametrize("T,k,E,drop", ROUTE_CASES)
