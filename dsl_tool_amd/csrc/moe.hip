@@ -430,19 +430,35 @@ __global__ __launch_bounds__(256) void moe_combine_kernel(
   for (int j = 0; j < CPL; ++j)
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-  for (int s = 0; s < topk; ++s) {
-    const int row = dest[(int64_t)t * topk + s];
-    if (row < 0 || row >= rows_y) continue;             // uniform across the block
-    const float ws = w[(int64_t)t * topk + s];
-    const uint16_t *yr = y + (int64_t)row * ldy;
+  // slots in groups of up to 8: every row load of a group in flight before
+  // its adds, which stay in slot order
+  constexpr int G = CPL <= 2 ? 8 : (CPL <= 4 ? 4 : 1);
+  for (int s0 = 0; s0 < topk; s0 += G) {
+    uint4 yv[G][CPL];
+    float wsv[G];
+    bool ok[G];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-      const int c = threadIdx.x + 256 * j;
-      if (c < nch) {
+    for (int g = 0; g < G; ++g) {
+      const int s = s0 + g;
+      const int row = s < topk ? dest[(int64_t)t * topk + s] : -1;
+      ok[g] = row >= 0 && row < rows_y;                 // uniform across the block
+      wsv[g] = ok[g] ? w[(int64_t)t * topk + s] : 0.f;
+      const uint4 *yr = reinterpret_cast<const uint4 *>(y + (int64_t)(ok[g] ? row : 0) * ldy);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        const int c = threadIdx.x + 256 * j;
+        yv[g][j] = (ok[g] && c < nch) ? yr[c] : make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (!ok[g]) continue;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
         float f[8];
-        unpack8(reinterpret_cast<const uint4 *>(yr)[c], f);
+        unpack8(yv[g][j], f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] = acc[j][e] + ws * f[e];
+        for (int e = 0; e < 8; ++e) acc[j][e] = acc[j][e] + wsv[g] * f[e];
       }
     }
   }
