@@ -203,6 +203,88 @@ __global__ __launch_bounds__(256) void moe_scatter_kernel(const int32_t *__restr
   }
 }
 
+// Whole route in one wave (decode-size batches, up to 64 * kWaveSteps
+// assignments): the ballot ranking of moe_scatter_kernel over the
+// assignments step by step with per-expert counts in LDS, the exclusive
+// scan over the experts (64 at a time, wave shuffles), then each lane writes
+// the rows of the assignments it holds in registers.  One wave keeps its LDS
+// operations in program order, so there is no barrier.
+constexpr int kWaveSteps = 16;         // steps of 64: up to 1024 assignments
+
+__global__ __launch_bounds__(64) void moe_route_wave_kernel(const int32_t *__restrict__ ids, int n,
+                                                           int E, int topk,
+                                                           int32_t *__restrict__ offsets,
+                                                           int32_t *__restrict__ dest,
+                                                           int32_t *__restrict__ src_token) {
+  extern __shared__ int cnt[];           // [E] counts, then first rows
+  const int lane = threadIdx.x;
+  for (int e = lane; e < E; e += 64) cnt[e] = 0;
+  int bits = 0;
+  while ((1 << bits) < E + 1) ++bits;
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int steps = (n + 63) / 64;
+  int kr[kWaveSteps];                    // key (12 bits, E for dropped) | rank << 12
+#pragma unroll
+  for (int st = 0; st < kWaveSteps; ++st) {
+    kr[st] = E;
+    if (st < steps) {                    // uniform
+      const int a = st * 64 + lane;
+      const int e = a < n ? ids[a] : -1;
+      kr[st] = (e >= 0 && e < E) ? e : E;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0): the zeroed counts are in LDS
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int st = 0; st < kWaveSteps; ++st) {
+    if (st < steps) {                    // uniform
+      const int k = kr[st];
+      uint64_t same = ~0ull;
+      for (int b = 0; b < bits; ++b) {
+        const uint64_t m = __ballot((k >> b) & 1);
+        same &= ((k >> b) & 1) ? m : ~m;
+      }
+      int r = 0;
+      if (k < E) r = cnt[k] + __popcll(same & below);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // every lane's read of cnt is back
+      __builtin_amdgcn_wave_barrier();
+      if (k < E && (same >> lane) == 1ull) cnt[k] = r + 1;
+      kr[st] = k | (r << 12);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  int carry = 0;
+  for (int e0 = 0; e0 < E; e0 += 64) {   // exclusive scan over the experts
+    const int e = e0 + lane;
+    const int c = e < E ? cnt[e] : 0;
+    int incl = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int t = __shfl_up(incl, d, 64);
+      if (lane >= d) incl += t;
+    }
+    if (e < E) {
+      cnt[e] = carry + incl - c;
+      offsets[e] = carry + incl - c;
+    }
+    carry += __shfl(incl, 63, 64);
+  }
+  if (lane == 0) offsets[E] = carry;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int st = 0; st < kWaveSteps; ++st) {
+    const int a = st * 64 + lane;
+    if (st < steps && a < n) {
+      const int k = kr[st] & 0xfff, r = kr[st] >> 12;
+      const int row = k < E ? cnt[k] + r : -1;
+      dest[a] = row;
+      if (row >= 0) src_token[row] = a / topk;
+    }
+  }
+}
+
 // Whole route in one workgroup of 16 waves (small n; up to 16 * kOneSteps * 64):
 // wave w ranks its contiguous range of assignments step by step with the
 // ballot scheme of moe_scatter_kernel, keeping per-expert counts in LDS;
@@ -492,6 +574,11 @@ hipError_t launch_moe_route(const int32_t *ids, int n, int topk, int E, int32_t 
   // (histograms, then bases + scatter per chunk) spreads the scattered row
   // writes over many CUs and wins beyond that (32768 assignments: 20 us for
   // the earlier three passes against 38 us in one workgroup)
+  if (n <= 64 * kWaveSteps && E <= 2047) {
+    moe_route_wave_kernel<<<1, 64, (size_t)E * sizeof(int), st>>>(ids, n, E, topk, offsets, dest,
+                                                                  src_token);
+    return hipGetLastError();
+  }
   if (n <= 4096 && E <= 2047 && 16 * E * (int)sizeof(int) <= 64 * 1024) {
     moe_route_one_kernel<<<1, 1024, (size_t)16 * E * sizeof(int), st>>>(ids, n, E, topk, offsets,
                                                                         dest, src_token);

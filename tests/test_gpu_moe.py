@@ -25,7 +25,9 @@ def _ids(T, k, E, seed, drop=False):
     return ids
 
 
-# Route paths: one workgroup (<= 4096 assignments, <= 1024 experts), and
+# Route paths: one wave (<= 1024 assignments: 1 x 1, 37 x 3 over 5, 128 x 8
+# and 32 x 8 over 64, 100 x 6 over 300 (five 64-expert runs of the scan),
+# 256 x 4 over 2000), one workgroup (<= 4096 assignments, <= 1024 experts), and
 # count + scatter for the rest, the scatter blocks forming their own bases
 # from a small histogram (4096 x 8 over 64 experts, 2100 x 3 over 100: two
 # 64-expert runs, ragged last chunk; 5000 x 2 over 3; 200 x 8 over 1100) or
@@ -35,7 +37,8 @@ def _ids(T, k, E, seed, drop=False):
 ROUTE_CASES = [(4096, 8, 64, False), (37, 3, 5, True), (1, 1, 1, False), (3000, 6, 2048, True),
                (513, 4, 7, False), (512, 8, 64, True), (1024, 4, 1000, False),
                (2100, 3, 100, True), (5000, 2, 3, False), (40000, 8, 256, True),
-               (0, 4, 1500, False), (200, 8, 1100, True)]
+               (0, 4, 1500, False), (200, 8, 1100, True), (128, 8, 64, True), (100, 6, 300, True),
+               (32, 8, 64, False), (256, 4, 2000, True)]
 
 
 @pytest.mark.parametrize("T,k,E,drop", ROUTE_CASES)
