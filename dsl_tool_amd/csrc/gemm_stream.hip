@@ -567,11 +567,18 @@ bool grouped_stream_supported(const GroupedArgs &gp) {
 }
 
 // Row blocks of 16 or 32 rows by the groups' average size (the router sends
-// averages below 48 here); two 16-row W tiles per workgroup.
+// averages below 48 here); four 16-row W tiles per workgroup.  Measured
+// (64 experts, N=1536 K=2048, 3 weight copies rotated): 16-row blocks up to
+// 4 rows per group on average, 32-row blocks above (32 tokens x top-8:
+// 31.5 against 33.7 us; 64 tokens: 34.9 against 37.6); two W tiles per
+// workgroup were 12-22% slower (32 tokens 37.6 us, 128 tokens 56.2 against
+// 41.6), one W tile or 512-byte chunks slower still, and 64-row blocks
+// 30-90% slower.  Against the persistent kernel the crossover stays at 48
+// rows per group (384 tokens: 62.2 against 62.7 us).
 hipError_t launch_grouped_stream(const GroupedArgs &gp, hipStream_t st) {
   if (!grouped_stream_supported(gp)) return hipErrorInvalidValue;
-  if (gp.rows / gp.G <= 16) return launch_grouped_cfg<1, 2, 256>(gp, st);
-  return launch_grouped_cfg<2, 2, 256>(gp, st);
+  if (gp.rows / gp.G <= 4) return launch_grouped_cfg<1, 4, 256>(gp, st);
+  return launch_grouped_cfg<2, 4, 256>(gp, st);
 }
 
 bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
