@@ -242,16 +242,17 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   // 32-row grid leaves CUs idle or needs a second round (N = 4096: 5.3
   // against 6.1 us, N = 14336: 11.4 against 13.1).  The decode kernel keeps
   // 9 <= M <= 16 when that grid fills 7/8 of the CUs or more in one round
-  // (N = 7168: 7.1 against 7.4 us, N = 8192).  NVFP4: the GEMV for M <= 4,
-  // the streaming kernel above that.  DSL_GEMM_SKINNY=stream|decode forces
-  // one of them (tests).
+  // (N = 7168: 7.1 against 7.4 us, N = 8192).  NVFP4: the GEMV for M = 1,
+  // the streaming kernel above that (N=14336 K=4096: M=1 8.4 against 9.4 us;
+  // M=2 10.0 against 14.4; M=4 10.0 against 22.5: the GEMV's time grows with
+  // M).  DSL_GEMM_SKINNY=stream|decode forces one of them (tests).
   bool prefer_stream;
   if (skinny_stream) {
     prefer_stream = true;
   } else if (skinny_decode) {
     prefer_stream = false;
   } else if (mode == MODE_NVFP4) {
-    prefer_stream = M > 4;
+    prefer_stream = M > 1;
   } else if (M <= 8 || M > 16 || mode == MODE_BF16) {
     prefer_stream = true;
   } else {

@@ -453,9 +453,10 @@ def test_decode_kernel_forced(mode, m, n, k, monkeypatch):
     assert_close(c, ref, what=f"{mode} forced decode {m}x{n}x{k}")
 
 
-# NVFP4 with M <= 4 and M * K/2048 <= 8 runs the GEMV kernel, 5 <= M <= 256
-# with K % 512 (M <= 32) or % 1024 the streaming kernel; the other shapes
-# here take the dense paths (same oracle).
+# NVFP4 with M = 1 and K/2048 <= 8 runs the GEMV kernel, 2 <= M <= 256 with
+# K % 256 the streaming kernel (DSL_GEMM_SKINNY=decode puts M = 2..4 back on
+# the GEMV: test_nvfp4_gemv_forced); the other shapes here take the dense
+# paths (same oracle).
 @pytest.mark.parametrize("m,n,k", [(1, 14336, 4096), (2, 1000, 2048), (3, 530, 4096),
                                    (4, 64, 4096), (1, 33, 16384), (3, 520, 8192), (4, 100, 8192),
                                    (16, 14336, 4096), (8, 1000, 2048), (128, 4096, 4096),
@@ -468,6 +469,19 @@ def test_nvfp4_decode(m, n, k):
     c = G.fp4_gemm_packed(qa, sa, qw, sw, fmt="nvfp4", global_a=ga, global_w=gw)
     ref = OG.ref_nvfp4(np_u8(qa), np_u8(sa), np_f32(ga)[0], np_u8(qw), np_u8(sw), np_f32(gw)[0])
     assert_close(c, ref, what=f"nvfp4 decode {m}x{n}x{k}")
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 1000, 2048), (3, 530, 4096), (4, 64, 4096), (4, 100, 8192),
+                                   (2, 14336, 4096)])
+def test_nvfp4_gemv_forced(m, n, k, monkeypatch):
+    monkeypatch.setenv("DSL_GEMM_SKINNY", "decode")
+    a = W.randn_bf16((m, k), 453)
+    w = W.randn_bf16((n, k), 454, 0.02)
+    qa, sa, ga = Q.quant_nvfp4(a.to(DEV))
+    qw, sw, gw = Q.quant_nvfp4(w.to(DEV))
+    c = G.fp4_gemm_packed(qa, sa, qw, sw, fmt="nvfp4", global_a=ga, global_w=gw)
+    ref = OG.ref_nvfp4(np_u8(qa), np_u8(sa), np_f32(ga)[0], np_u8(qw), np_u8(sw), np_f32(gw)[0])
+    assert_close(c, ref, what=f"nvfp4 forced GEMV {m}x{n}x{k}")
 
 
 def test_grouped_moe_skewed_counts_pipelined():
