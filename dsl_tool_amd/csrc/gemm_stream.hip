@@ -1,4 +1,5 @@
-// Streaming quantized GEMMs for gfx950 at skinny and mid M (M <= 256):
+// Streaming quantized GEMMs for gfx950 at skinny and mid M (M <= 1024; the
+// router takes it while ceil(M/64) * N stays small):
 // C[M,N] = A[M,K] . W[N,K]^T, FP8 per-tensor, FP8 1x128/128x128 block,
 // MXFP4, NVFP4 and bf16, one launch, deterministic.  BASELINE config 1 (M=128,
 // N=K=4096) and the decode shapes (M=16) run here.
@@ -582,7 +583,7 @@ hipError_t launch_grouped_stream(const GroupedArgs &gp, hipStream_t st) {
 }
 
 bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
-  if (M < 1 || M > 256 || N < 1) return false;
+  if (M < 1 || M > 1024 || N < 1) return false;
   if (Kb % 256 != 0) return false;   // 512-byte chunks where they fit, else 256
   if (mode == MODE_FP8_TENSOR || mode == MODE_BF16) return true;
   // block scales and E8M0 rows move by 16-byte direct loads (K % 512)

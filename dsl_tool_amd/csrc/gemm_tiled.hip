@@ -225,16 +225,22 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   // blocks times N (each block streams all of W, and each W slice re-reads
   // its activation rows), while the 128x128 / persistent tiles stay at about
   // one round up to a few thousand rows.  Measured at K = 4096, N = 4096,
-  // 14336, 28672, M = 48..256 (the crossover does not move with K: both
-  // sides scale with it): past ceil(M/64) * N = 9 x 4096 (FP8 per-tensor,
-  // MXFP4), 7 x 4096 (FP8 block) or 18 x 4096 (bf16) the tiles are faster
-  // (FP8 block M=256 N=14336: 31.8 against 58.1 us).  Rows of an odd
+  // 7168, 14336, 28672, M = 48..1024 (the crossover does not move with K:
+  // both sides scale with it): past ceil(M/64) * N = 8.5 x 4096 (FP8
+  // per-tensor, MXFP4), 7.5 x 4096 (FP8 block) or 18 x 4096 (bf16) the tiles
+  // are faster (FP8 block M=256 N=14336: 31.8 against 58.1 us, M=256 N=7168
+  // streams: 33.1 against 36.4; MXFP4 M=320
+  // N=7168: 19.7 against 23.7; per-tensor M=512 N=4096 streams: 21.5
+  // against 26.7).  NVFP4 (dequantized to fp16 in the tiles) streams up to
+  // 256 rows whatever N, and above that below 15 x 4096 (M=768 N=4096: 61.8
+  // against 76.5 us; M=320 N=14336: 91.4 against 88.1).  Rows of an odd
   // number of 256-byte chunks stream in 32-row blocks: twice the blocks.
-  if (streamable && !skinny_stream && M > 32 && mode != MODE_NVFP4) {
+  if (streamable && !skinny_stream && M > 32 && (mode != MODE_NVFP4 || M > 256)) {
     const int bm = Kb % 512 == 0 ? 64 : 32;
-    const int64_t span = (int64_t)((M + bm - 1) / bm) * N;
-    const int64_t thr = mode == MODE_FP8_BLOCK ? 7 : (mode == MODE_BF16 ? 18 : 9);
-    if (span >= thr * 4096) streamable = false;
+    const int64_t span2 = 2 * (int64_t)((M + bm - 1) / bm) * N;   // twice the span
+    const int64_t thr2 = mode == MODE_FP8_BLOCK ? 15
+                         : (mode == MODE_BF16 ? 36 : (mode == MODE_NVFP4 ? 30 : 17));
+    if (span2 >= thr2 * 4096) streamable = false;
   }
   // Skinny M (measured, graph timing over rotating weights): the streaming
   // kernel is the faster one for M <= 8 (FP8, MXFP4: 4-25%), for bf16 at
@@ -305,6 +311,12 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
     }
   }
   return r;
+}
+
+bool gemm_routes_to_stream(int mode, int64_t M, int64_t N, int64_t K) {
+  const int Kb = (mode == MODE_MXFP4 || mode == MODE_NVFP4) ? (int)(K / 2)
+                                                            : (mode == MODE_BF16 ? (int)(2 * K) : (int)K);
+  return route_for(mode, (int)M, (int)N, (int)K, Kb, true, true).path == PATH_STREAM;
 }
 
 size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K, bool accumulate) {

@@ -36,6 +36,7 @@ SHAPES = [
     (128, 4096, 2048),
     (72, 1000, 512),
     (48, 4000, 1024),     # 33..64 rows in one round: two 32-row blocks of two W tiles
+    (520, 1000, 1024),    # more than 256 rows on the streaming kernel (small N)
 ]
 
 

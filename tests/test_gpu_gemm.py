@@ -558,7 +558,8 @@ def test_nvfp4_pipelined(m, n, k):
 # neighbouring M cover its 32- and 64-row activation blocks and its upper
 # bound (M = 256).
 MID_SHAPES = [(128, 4096, 4096), (33, 4096, 4096), (64, 4096, 4096), (256, 4096, 4096),
-              (96, 1000, 2048), (200, 2056, 1024), (128, 512, 16384)]
+              (96, 1000, 2048), (200, 2056, 1024), (128, 512, 16384), (512, 4096, 2048),
+              (320, 7168, 1024)]
 
 
 @pytest.mark.parametrize("m,n,k", MID_SHAPES)
@@ -633,7 +634,7 @@ def test_misaligned_scales_with_small_workspace():
 # workgroup (config-1-sized N) and one (small N), ragged M and N edges, and
 # M blocks whose last rows repeat the edge row.
 MID_MODE_SHAPES = [(128, 4096, 4096), (256, 7168, 4096), (40, 512, 2048), (97, 1000, 1024),
-                   (200, 2056, 3072)]
+                   (200, 2056, 3072), (384, 4096, 2048)]
 
 
 @pytest.mark.parametrize("m,n,k", MID_MODE_SHAPES)
@@ -667,7 +668,10 @@ STREAM_SHAPES = [("tensor", 16, 7168, 4096), ("block", 16, 7168, 4096), ("mxfp4"
                  ("nvfp4", 200, 1000, 3072), ("nvfp4", 40, 2056, 2048),
                  # rows of an odd number of 256-byte chunks: 32-row blocks at any M
                  ("tensor", 100, 1000, 768), ("mxfp4", 130, 2056, 1536), ("bf16", 200, 700, 1408),
-                 ("nvfp4", 72, 1000, 1536), ("bf16", 256, 520, 128)]
+                 ("nvfp4", 72, 1000, 1536), ("bf16", 256, 520, 128),
+                 # more than 256 rows (up to 1024 stream where ceil(M/64) * N is small)
+                 ("tensor", 300, 1000, 1024), ("block", 384, 1000, 1024), ("mxfp4", 1024, 520, 2048),
+                 ("nvfp4", 600, 520, 2048), ("bf16", 520, 700, 1024), ("tensor", 777, 264, 768)]
 
 
 @pytest.mark.parametrize("tn", ["1", "2", "4"])
