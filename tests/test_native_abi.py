@@ -119,13 +119,27 @@ def test_moe_glue_argument_validation(lib):
     rc = lib.dsl_moe_combine(fake, 32, 64, 32, fake, fake, 16, 2, fake, 64, 0, None)
     assert rc == N.DSL_ERR_ARG and "ldy" in _err(lib)
     assert lib.dsl_moe_combine(None, 0, 64, 64, None, None, 0, 2, None, 64, 0, None) == 0
+    # no tokens still needs one block's histogram when the route takes two passes
+    assert lib.dsl_moe_route_workspace_bytes(0, 8, 1500) >= 1500 * 4
+    rc = lib.dsl_moe_quant_tokens(fake, 16, 100, 104, fake, 2, 32, fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "multiple of 8" in _err(lib)
+    # the gather GEMM: whole 128-byte pairs of K, a row map, tokens < 2^24
+    rc = lib.dsl_moe_grouped_fp8_gemm(fake, 64, fake, fake, fake, fake, 4, 128, 256, 192, 256, 0,
+                                      fake, fake, None)
+    assert rc == N.DSL_ERR_UNSUPPORTED and "128" in _err(lib)
+    rc = lib.dsl_moe_grouped_fp8_gemm(fake, 64, None, fake, fake, fake, 4, 128, 256, 256, 256, 0,
+                                      fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "NULL" in _err(lib)
+    rc = lib.dsl_moe_grouped_fp8_gemm(fake, 1 << 24, fake, fake, fake, fake, 4, 128, 256, 256, 256, 0,
+                                      fake, fake, None)
+    assert rc == N.DSL_ERR_ARG and "tokens" in _err(lib)
 
 
 def test_workspace_query_matches_the_planned_path(lib):
     # skinny M with K a multiple of 1024 takes the single-pass decode kernel
     assert lib.dsl_gemm_workspace_bytes(N.OP_FP8, 16, 8192, 8192) == 0
-    # FP4 reports the larger of the MXFP4 and NVFP4 plans: NVFP4 with M <= 4
-    # runs the GEMV kernel and 5 <= M <= 256 the streaming kernel (no
+    # FP4 reports the larger of the MXFP4 and NVFP4 plans: NVFP4 with M = 1
+    # runs the GEMV kernel and larger skinny M the streaming kernel (no
     # workspace); a K neither skinny kernel takes (4352: not a multiple of
     # 512 elements) plans split-K over the register-staged tiles
     assert lib.dsl_gemm_workspace_bytes(N.OP_FP4, 1, 14336, 4096) == 0
