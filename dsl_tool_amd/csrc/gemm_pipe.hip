@@ -1,5 +1,6 @@
 // Dense pipelined GEMM kernels for gfx950 (FP8 per-tensor, FP8 block-scaled,
-// MXFP4); the mainloop, DMA ring and LDS layout are described in pipe_core.h.
+// MXFP4, NVFP4, bf16); the mainloop, DMA ring and LDS layout are described in
+// pipe_core.h.
 #include <type_traits>
 
 #include "pipe_core.h"
@@ -440,6 +441,7 @@ static hipError_t launch_pipe_cfg(const GemmArgs &p, hipStream_t st) {
 // grids, 1 the 128x128 tile for mid-sized ones; the others are kept as
 // alternatives for tuning (DSL_GEMM_PIPE).
 hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_t st) {
+  if (mode == MODE_BF16) return launch_pipe_cfg<PipeCfg<MODE_BF16, 128, 128, 2, 2, 4, 64>>(p, st);
   if (mode == MODE_FP8_BLOCK) {
     const bool ring_ok = p.K % 512 == 0 && p.K / 128 <= kBlockPfMaxGroups &&
                          (reinterpret_cast<uintptr_t>(p.sa) & 15) == 0;

@@ -233,13 +233,21 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   // N=7168: 19.7 against 23.7; per-tensor M=512 N=4096 streams: 21.5
   // against 26.7).  NVFP4 (dequantized to fp16 in the tiles) streams up to
   // 256 rows whatever N, and above that below 15 x 4096 (M=768 N=4096: 61.8
-  // against 76.5 us; M=320 N=14336: 91.4 against 88.1).  Rows of an odd
-  // number of 256-byte chunks stream in 32-row blocks: twice the blocks.
+  // against 76.5 us; M=320 N=14336: 91.4 against 88.1).  bf16 where one
+  // round of the 128x128 pipelined tiles holds the problem: below 10 x 4096
+  // (that round costs ~45-55 us at K = 4096 whatever its size: M=512
+  // N=7168 52.9 against 67.2 us streamed; M=512 N=4096 streams, 34.7 against
+  // 51.7).  Rows of an odd number of 256-byte chunks stream in 32-row
+  // blocks: twice the blocks.
+  const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
+  const bool bf16_pipe_round = mode == MODE_BF16 && pipe_forced != -2 && Kb % 128 == 0 && M > 64 &&
+                               N > 64 && t128 >= 40 && t128 <= device_cu_count();
   if (streamable && !skinny_stream && M > 32 && (mode != MODE_NVFP4 || M > 256)) {
     const int bm = Kb % 512 == 0 ? 64 : 32;
     const int64_t span2 = 2 * (int64_t)((M + bm - 1) / bm) * N;   // twice the span
     const int64_t thr2 = mode == MODE_FP8_BLOCK ? 15
-                         : (mode == MODE_BF16 ? 36 : (mode == MODE_NVFP4 ? 30 : 17));
+                         : (mode == MODE_BF16 ? (bf16_pipe_round ? 20 : 36)
+                                              : (mode == MODE_NVFP4 ? 30 : 17));
     if (span2 >= thr2 * 4096) streamable = false;
   }
   // Skinny M (measured, graph timing over rotating weights): the streaming
@@ -273,22 +281,30 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
     r.path = PATH_STREAM;
     return r;
   }
-  if (mode == MODE_BF16) {   // persistent kernel or the register-staged tiles
+  if (mode == MODE_BF16) {   // pipelined, persistent or register-staged tiles
     const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-    // one partial round of the persistent kernel beats the register-staged
-    // tiles from about a sixth of the CUs' worth of 256x256 tiles (M=768
-    // N=4096 K=4096: 77 against 102 us; M=2048 N=7168: 104 against 220) and
-    // about 2.4M outputs (M=288 N=7168, 56 tiles of which 28 hold 32 rows:
-    // 77 against 70 us; M=384: 78 against 89)
-    if (persist_on && 6 * t256 >= device_cu_count() && (int64_t)M * N >= 2400000 &&
-        persist_supported(mode, M, N, K, Kb, sc16))
+    // one round of 128x128 pipelined tiles (40 to one per CU) beats a
+    // partial round of 256x256 persistent tiles, which leaves 3/4 of the
+    // CUs idle (M=1536 N=2048 K=4096: 44.2 against 84.0 us; M=1024 N=4096:
+    // 54.7 against 73.9); past one round the persistent kernel (M=1536
+    // N=4096: 95.4 against 100.4).  Then one partial round of the persistent
+    // kernel beats the register-staged tiles from about a sixth of the CUs'
+    // worth of 256x256 tiles (M=768 N=4096 K=4096: 77 against 102 us;
+    // M=2048 N=7168: 104 against 220) and about 2.4M outputs (M=288 N=7168,
+    // 56 tiles of which 28 hold 32 rows: 77 against 70 us; M=384: 78 against
+    // 89)
+    if (bf16_pipe_round) {
+      r.path = PATH_PIPE;
+      r.variant = 1;
+    } else if (persist_on && 6 * t256 >= device_cu_count() && (int64_t)M * N >= 2400000 &&
+               persist_supported(mode, M, N, K, Kb, sc16)) {
       r.path = PATH_PERSIST;
+    }
     return r;
   }
   const bool pipe_ok = pipe_forced != -2 && Kb % 128 == 0 && (mode == MODE_FP8_TENSOR || sc4);
   if (pipe_ok) {
     const int64_t t256 = (int64_t)((M + 255) / 256) * ((N + 255) / 256);
-    const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
     // Rounds of tiles per CU: a round of 256x256 persistent tiles costs
     // about as much as 1.6 rounds of the 128x128 pipelined tiles (1.5-2 with
     // block scales), so the persistent kernel takes over once the 128x128

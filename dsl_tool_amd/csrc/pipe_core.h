@@ -92,6 +92,7 @@ struct PipeCfg {
   static constexpr bool MX = MODE == MODE_MXFP4;
   static constexpr bool NV = MODE == MODE_NVFP4;
   static constexpr bool FP4 = MX || NV;
+  static constexpr bool BF16 = MODE == MODE_BF16;           // 64-byte k-step = 32 bf16 of K
   static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;     // one 128-K scale group per stage
   static constexpr int CH = SKB / 16, RPI = 1024 / SKB;     // chunks per row, rows per DMA
   // MFMA steps per stage: 32x32x64 for FP8 / MXFP4; for NVFP4 a "step" is a
@@ -282,20 +283,38 @@ struct KFrag<Cfg, false> {
 #pragma unroll
     for (int t = 0; t < Cfg::TM; ++t) load_a(st, k, t, wm, r32, h);
   }
+  // bf16: the lane's 32 bytes are 16 bf16 of K, two 32x32x16 MFMAs (first
+  // and second 16-byte chunk; the same K order for A and W)
+  static DSL_DEV v16f mma_bf16(const v8i &x, const v8i &y, v16f c) {
+    const v8bf x0 = __builtin_bit_cast(v8bf, (v4i){x[0], x[1], x[2], x[3]});
+    const v8bf x1 = __builtin_bit_cast(v8bf, (v4i){x[4], x[5], x[6], x[7]});
+    const v8bf y0 = __builtin_bit_cast(v8bf, (v4i){y[0], y[1], y[2], y[3]});
+    const v8bf y1 = __builtin_bit_cast(v8bf, (v4i){y[4], y[5], y[6], y[7]});
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x0, y0, c, 0, 0, 0);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x1, y1, c, 0, 0, 0);
+  }
   DSL_DEV void mma_row(int, int i, v16f (&acc)[Cfg::TM][Cfg::TN]) const {
 #pragma unroll
-    for (int j = 0; j < Cfg::TN; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[i], b[j], acc[i][j], 0, 0, 0,
-                                                                  0, 0, 0);
+    for (int j = 0; j < Cfg::TN; ++j) {
+      if constexpr (Cfg::BF16)
+        acc[i][j] = mma_bf16(a[i], b[j], acc[i][j]);
+      else
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a[i], b[j], acc[i][j], 0, 0,
+                                                                    0, 0, 0, 0);
+    }
   }
   // operands swapped (W tile in the first slot): acc[i][j] holds C^T, so
   // lane l owns output row 32i + l%32 and register r the column
   // 32j + 8(r/4) + 4h + r%4
   DSL_DEV void mma_row_t(int i, v16f (&acc)[Cfg::TM][Cfg::TN]) const {
 #pragma unroll
-    for (int j = 0; j < Cfg::TN; ++j)
-      acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b[j], a[i], acc[i][j], 0, 0, 0,
-                                                                  0, 0, 0);
+    for (int j = 0; j < Cfg::TN; ++j) {
+      if constexpr (Cfg::BF16)
+        acc[i][j] = mma_bf16(b[j], a[i], acc[i][j]);
+      else
+        acc[i][j] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(b[j], a[i], acc[i][j], 0, 0,
+                                                                    0, 0, 0, 0);
+    }
   }
   DSL_DEV void mma(int k, v16f (&acc)[Cfg::TM][Cfg::TN]) const {
 #pragma unroll

@@ -37,6 +37,8 @@ SHAPES = [
     (72, 1000, 512),
     (48, 4000, 1024),     # 33..64 rows in one round: two 32-row blocks of two W tiles
     (520, 1000, 1024),    # more than 256 rows on the streaming kernel (small N)
+    (1536, 1024, 1024),   # pipelined 128x128 tiles (too few 256x256 tiles for a persistent round)
+    (1100, 2000, 512),    # the same with ragged M and N
 ]
 
 
