@@ -411,15 +411,16 @@ LoraPlan lora_plan(int64_t m, int64_t n, int64_t k, int64_t lr) {
   // enough to be its skinny M; its epilogue writes hi | lo itself.
   p.tt = lr <= 256 && dsl::stream_supported(dsl::MODE_BF16, (int)lr, (int)m, (int)k, (int)(2 * k), true);
   // One pass (the adapter term as a second K segment of the persistent
-  // kernel) unless both the base GEMM and the adapter add would stream (up
-  // to 256 rows, and to 1024 at small N): then the base GEMM takes the
-  // streaming kernel and the adapter term is added by a second streaming
-  // pass into the fp32 output (N=K=4096, 4 x rank 16: M=16 79.9 us in one
-  // pass, the base GEMM alone 7.3; M=512 100.2 in one pass, 58.8 in two;
-  // M=768, where the add would run on the register-staged tiles, 115.2 in
-  // two).
-  const bool both_stream = dsl::gemm_routes_to_stream(dsl::MODE_BF16, m, n, k) &&
-                           dsl::gemm_routes_to_stream(dsl::MODE_BF16, m, n, p.ld2);
+  // kernel) unless both the base GEMM and the adapter add would take the
+  // streaming kernel or the 128x128 pipelined tiles (up to 1024 rows at
+  // small N, and where one round of 128x128 tiles holds the problem): then
+  // the base GEMM takes its own kernel and the adapter term is added by a
+  // second pass into the fp32 output (N=K=4096, 4 x rank 16: M=16 79.9 us
+  // in one pass, the base GEMM alone 7.3; M=512 100.2 in one pass, 58.8 in
+  // two; M=768, where the add would run on the register-staged tiles, 115.2
+  // in two).
+  const bool both_stream = dsl::gemm_routes_to_stream(dsl::MODE_BF16, m, n, k, true) &&
+                           dsl::gemm_routes_to_stream(dsl::MODE_BF16, m, n, p.ld2, true, true);
   p.one_pass = dsl::persist_supported(dsl::MODE_BF16, (int)m, (int)n, (int)k, (int)(2 * (k + p.ld2)), true) &&
                (2 * k) % 128 == 0 && m > 256 && !both_stream;
   // hi | lo against B^T | B^T without the copy (one pass only): B^T's rows

@@ -63,8 +63,12 @@ void gemm_pipe_kernel(const GemmArgs p) {
         if (row >= p.M) continue;
         float v = acc[i][j][r];
         if constexpr (GLOBAL) v = (v * s1) * s2;
-        if (p.out_f32) static_cast<float *>(p.c)[(int64_t)row * p.ldc + col] = v;
-        else static_cast<uint16_t *>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16(v);
+        if (p.out_f32) {
+          float *d = static_cast<float *>(p.c) + (int64_t)row * p.ldc + col;
+          *d = p.accumulate ? *d + v : v;      // C += result: one writer per element
+        } else {
+          static_cast<uint16_t *>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16(v);
+        }
       }
     }
 }
@@ -441,6 +445,8 @@ static hipError_t launch_pipe_cfg(const GemmArgs &p, hipStream_t st) {
 // grids, 1 the 128x128 tile for mid-sized ones; the others are kept as
 // alternatives for tuning (DSL_GEMM_PIPE).
 hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_t st) {
+  // C += result: fp32 output through the plain epilogue only
+  if (p.accumulate && (!p.out_f32 || mode == MODE_FP8_BLOCK)) return hipErrorInvalidValue;
   if (mode == MODE_BF16) return launch_pipe_cfg<PipeCfg<MODE_BF16, 128, 128, 2, 2, 4, 64>>(p, st);
   if (mode == MODE_FP8_BLOCK) {
     const bool ring_ok = p.K % 512 == 0 && p.K / 128 <= kBlockPfMaxGroups &&

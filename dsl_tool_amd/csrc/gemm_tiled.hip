@@ -202,6 +202,8 @@ struct Route {
   Plan tiled;     // PATH_TILED plan
 };
 
+constexpr int kAccShortK = 512;   // C += result with K up to this streams where it can
+
 static bool stream_enabled() {
   static const bool on = !env_off("DSL_GEMM_STREAM");
   return on;
@@ -329,10 +331,13 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   return r;
 }
 
-bool gemm_routes_to_stream(int mode, int64_t M, int64_t N, int64_t K) {
+bool gemm_routes_to_stream(int mode, int64_t M, int64_t N, int64_t K, bool or_pipe, bool accumulate) {
   const int Kb = (mode == MODE_MXFP4 || mode == MODE_NVFP4) ? (int)(K / 2)
                                                             : (mode == MODE_BF16 ? (int)(2 * K) : (int)K);
-  return route_for(mode, (int)M, (int)N, (int)K, Kb, true, true).path == PATH_STREAM;
+  int path = route_for(mode, (int)M, (int)N, (int)K, Kb, true, true).path;
+  if (accumulate && K <= kAccShortK && stream_enabled() && stream_supported(mode, (int)M, (int)N, (int)K, Kb, true))
+    path = PATH_STREAM;   // as launch_gemm routes C += result
+  return path == PATH_STREAM || (or_pipe && path == PATH_PIPE && (!accumulate || mode != MODE_FP8_BLOCK));
 }
 
 size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K, bool accumulate) {
@@ -365,14 +370,18 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
       return hipErrorInvalidValue;
     return launch_gemm_stream(mode, p, st);
   }
-  // C += result: the streaming kernel where the router picks a skinny
-  // kernel (fp32 out, one writer per element), else the register-staged
-  // kernels
-  if (p.accumulate)
-    r.path = ((r.path == PATH_STREAM || r.path == PATH_DECODE) && p.out_f32 &&
-              stream_supported(mode, p.M, p.N, p.K, p.Kb, (sc & 15) == 0))
-                 ? PATH_STREAM
-                 : PATH_TILED;
+  // C += result (fp32 out, one writer per element): the streaming kernel
+  // where the router picks a skinny kernel or K is short (a LoRA adapter
+  // add: W is then small enough to stream once per activation block), the
+  // pipelined tiles where the router picks those (not block-scaled), else
+  // the register-staged kernels
+  if (p.accumulate) {
+    if ((r.path == PATH_STREAM || r.path == PATH_DECODE || p.K <= kAccShortK) && p.out_f32 &&
+        stream_enabled() && stream_supported(mode, p.M, p.N, p.K, p.Kb, (sc & 15) == 0))
+      r.path = PATH_STREAM;
+    else if (!(r.path == PATH_PIPE && p.out_f32 && mode != MODE_FP8_BLOCK))
+      r.path = PATH_TILED;
+  }
   p.ksplit = 1;
   if (r.path == PATH_DECODE) return launch_gemm_decode(mode, p, st);
   if (r.path == PATH_STREAM) return launch_gemm_stream(mode, p, st);

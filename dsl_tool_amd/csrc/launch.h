@@ -96,8 +96,10 @@ hipError_t launch_gemm_stream(int mode, const GemmArgs &p, hipStream_t st);
 hipError_t launch_gemm(int mode, GemmArgs args, hipStream_t st);
 // Workspace the launcher will need for this shape (0 if none).
 size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K, bool accumulate = false);
-// Whether launch_gemm takes the streaming kernel for this shape (aligned scales).
-bool gemm_routes_to_stream(int mode, int64_t M, int64_t N, int64_t K);
+// Whether launch_gemm takes the streaming kernel (or_pipe: or the pipelined
+// tiles) for this shape (aligned scales; accumulate: C += result, fp32 out).
+bool gemm_routes_to_stream(int mode, int64_t M, int64_t N, int64_t K, bool or_pipe = false,
+                           bool accumulate = false);
 
 constexpr int kMaxGroups = 2048;   // groups per grouped launch (LDS tables)
 

@@ -29,6 +29,8 @@ LORA_TOL = 2e-5
 # second streaming pass into the fp32 result (M = 8..256; N = 2056 leaves a
 # ragged column edge for that pass's scalar epilogue); M = 1, 2 add it on
 # the vector ALUs in fp32; L*R = 640 at M = 8 takes the register-staged T.
+# M = 1536 N = 1024 and M = 2000 N = 1100 run the base GEMM and the add on
+# the 128x128 pipelined tiles (one round of them).
 @pytest.mark.parametrize("m,n,k,r,l", [(512, 768, 1024, 16, 2), (300, 520, 264, 8, 3),
                                        (4096, 4352, 512, 16, 4), (16, 256, 2048, 64, 1),
                                        (256, 512, 1024, 64, 5), (1024, 1024, 4096, 16, 4),
@@ -36,7 +38,8 @@ LORA_TOL = 2e-5
                                        (300, 520, 3072, 24, 2), (700, 260, 2048, 8, 3),
                                        (1, 4096, 4096, 16, 4), (64, 2056, 1024, 32, 2),
                                        (40, 520, 1024, 8, 3), (2, 1000, 512, 8, 2),
-                                       (8, 512, 1024, 64, 10)])
+                                       (8, 512, 1024, 64, 10), (1536, 1024, 1024, 16, 4),
+                                       (2000, 1100, 512, 8, 3)])
 def test_lora_fused_gemm(m, n, k, r, l):
     x = W.randn_bf16((m, k), 500)
     w = W.randn_bf16((n, k), 501, 0.05)
