@@ -498,6 +498,52 @@ __global__ __launch_bounds__(128) void moe_permute_quant16_kernel(
   }
 }
 
+// Token-major quantize for rows of up to 2048 elements (k % 8 == 0): one
+// wave per token (four per workgroup), lane l holding chunks l + 64 j, the
+// amax by wave reduction alone; codes to the token's row, the scale to each
+// routed row by the lanes j < topk.  Same arithmetic as above, so the same
+// codes and scales.
+template <int CPL>
+__global__ __launch_bounds__(256) void moe_quant_tokens_wave_kernel(
+    const uint16_t *__restrict__ x, int64_t ldx, int k_dim, int tokens,
+    const int32_t *__restrict__ dest, int topk, int rows, uint8_t *__restrict__ qx,
+    float *__restrict__ sx) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= tokens) return;                       // whole waves: no barrier below
+  const int lane = threadIdx.x & 63;
+  const int nch = k_dim >> 3;
+  const uint4 *xr = reinterpret_cast<const uint4 *>(x + (int64_t)t * ldx);
+  uint4 d[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    d[j] = c < nch ? xr[c] : make_uint4(0, 0, 0, 0);
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    float f[8];
+    unpack8(d[j], f);
+    m = fmaxf(m, amax8(f));
+  }
+  const float s = fp8_scale_of(wave_max(m));
+  const float r = rcp_approx(s);
+  uint2 *qr = reinterpret_cast<uint2 *>(qx + (int64_t)t * k_dim);
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) {
+      float f[8];
+      unpack8(d[j], f);
+      qr[c] = e4m3_quot8(f, s, r);
+    }
+  }
+  for (int slot = lane; slot < topk; slot += 64) {
+    const int row = dest[(int64_t)t * topk + slot];
+    if (row >= 0 && row < rows) sx[row] = s;
+  }
+}
+
 // out[t] = sum_j w[t, j] * y[dest[t, j]] (dropped slots skipped), fp32 in
 // slot order with separate multiply and add, then bf16 or fp32.
 template <int CPL>
@@ -609,6 +655,17 @@ hipError_t launch_moe_permute_quant(const uint16_t *x, int64_t ldx, int k_dim, i
                                     const int32_t *dest, int topk, int rows, uint8_t *qx, float *sx,
                                     bool tok_major, hipStream_t st) {
   if (tokens == 0 || (rows == 0 && !tok_major)) return hipSuccess;
+  if (tok_major && k_dim <= 2048 && ldx % 8 == 0) {
+    const unsigned g = (unsigned)((tokens + 3) / 4);
+    const int per = (k_dim / 8 + 63) / 64;
+    if (per <= 1)
+      moe_quant_tokens_wave_kernel<1><<<g, 256, 0, st>>>(x, ldx, k_dim, tokens, dest, topk, rows, qx, sx);
+    else if (per <= 2)
+      moe_quant_tokens_wave_kernel<2><<<g, 256, 0, st>>>(x, ldx, k_dim, tokens, dest, topk, rows, qx, sx);
+    else
+      moe_quant_tokens_wave_kernel<4><<<g, 256, 0, st>>>(x, ldx, k_dim, tokens, dest, topk, rows, qx, sx);
+    return hipGetLastError();
+  }
   if (k_dim % 16 == 0 && ldx % 8 == 0) {
     // 16-element chunks over 128 threads: the chunk count per thread is
     // that of 8-element chunks over 256

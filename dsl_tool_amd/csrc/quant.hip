@@ -392,6 +392,50 @@ __global__ __launch_bounds__(256) void quant_fp8_wide_kernel(
   }
 }
 
+// Row groups of 264..2048 elements: one wave per group (four per
+// workgroup), lane l holding chunks l + 64 j, the amax by wave reduction
+// alone.  A workgroup per group left 3/4 of its threads idle at 1 x 512 and
+// waited on a barrier for each group.  Same arithmetic as the wide kernel,
+// so the same codes and scales.
+template <int CPL>
+__global__ __launch_bounds__(256) void quant_fp8_wavegroup_kernel(
+    const uint16_t *__restrict__ x, int64_t cols, int64_t sr, int gc, int64_t ngroups,
+    uint8_t *__restrict__ q, float *__restrict__ scales) {
+  const int64_t g = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (g >= ngroups) return;                       // whole waves: no barrier below
+  const int lane = threadIdx.x & 63;
+  const int64_t gpr = (cols + gc - 1) / gc;
+  const int64_t r = g / gpr, gi = g - r * gpr;
+  const int64_t c0 = gi * gc;
+  const int nch = (int)((c0 + gc < cols ? gc : cols - c0) >> 3);
+  const uint16_t *xr = x + r * sr + c0;
+  uint4 d[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    d[j] = c < nch ? reinterpret_cast<const uint4 *>(xr)[c] : make_uint4(0, 0, 0, 0);
+  }
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    float f[8];
+    unpack8(d[j], f);
+    m = fmaxf(m, amax8(f));
+  }
+  const float s = fp8_scale_of(wave_max(m));
+  const float rs = rcp_approx(s);
+  if (lane == 0) scales[g] = s;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) {
+      float f[8];
+      unpack8(d[j], f);
+      *reinterpret_cast<uint2 *>(q + r * cols + c0 + (int64_t)c * 8) = e4m3_quot8(f, s, rs);
+    }
+  }
+}
+
 // One workgroup per gr x gc FP8 tile of any size (two reads of the tile).
 // VEC (16-byte bf16 rows) divides by the reciprocal quotient; the other path
 // divides with __fdiv_rn and serves fp32 sources too (T = float).
@@ -618,6 +662,16 @@ hipError_t launch_quant_fp8_blocks(const void *xv, bool f32, int64_t rows, int64
     return hipGetLastError();
   }
   const bool tvec = vec && (gc % 8) == 0;
+  if (gr == 1 && tvec && gc > 256 && gc <= 2048) {
+    const unsigned g = (unsigned)((tiles + 3) / 4);
+    if (gc <= 512)
+      quant_fp8_wavegroup_kernel<1><<<g, 256, 0, st>>>(x, cols, sr, (int)gc, tiles, q, scales);
+    else if (gc <= 1024)
+      quant_fp8_wavegroup_kernel<2><<<g, 256, 0, st>>>(x, cols, sr, (int)gc, tiles, q, scales);
+    else
+      quant_fp8_wavegroup_kernel<4><<<g, 256, 0, st>>>(x, cols, sr, (int)gc, tiles, q, scales);
+    return hipGetLastError();
+  }
   if (gr == 1 && tvec && gc > 128 && gc <= 32768) {
     const int per = (int)((gc / 8 + 255) / 256);
     const unsigned g = (unsigned)tiles;

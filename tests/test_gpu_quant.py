@@ -113,7 +113,7 @@ def test_nvfp4_division_near_rounding_boundaries(amax, boost):
 
 
 @pytest.mark.parametrize("gr,gc", [(1, 128), (128, 128), (1, 4096), (1, 64), (16, 48), (1, 200), (1, 2048),
-                                   (1, 16384), (1, 32)])
+                                   (1, 16384), (1, 32), (1, 512), (1, 1024), (1, 264), (1, 1000)])
 def test_fp8_blocks_match_oracle(gr, gc):
     x = W.activations(2, 300, 4096, outliers=True)
     q, s = Q.quant_fp8_blocks(x.to(DEV), gr, gc)
