@@ -335,7 +335,8 @@ def build_cases(names, dev):
         stages = {"route": [route], "permute": [permute], "quant_tokens": [quant_tokens],
                   "combine": [combine], "grouped": [grouped], "grouped_gather": [grouped_gather],
                   "layer": [route, quant_tokens, grouped_gather, combine] if gather
-                  else [route, permute, grouped, combine]}[stage]
+                  else [route, permute, grouped, combine],
+                  "layer_permuted": [route, permute, grouped, combine]}[stage]
 
         def launch(i, stream):
             for f in stages:
@@ -345,7 +346,8 @@ def build_cases(names, dev):
             return 0
         counts = W.moe_counts(tokens=tokens)
         nonempty = int((counts > 0).sum())
-        flops = 2.0 * rows * Nn * K if stage in ("layer", "grouped", "grouped_gather") else 0.0
+        flops = 2.0 * rows * Nn * K if stage in ("layer", "layer_permuted", "grouped",
+                                                 "grouped_gather") else 0.0
         nbytes = {"route": 4 * rows * 3 + 4 * (E + 1),
                   "permute": 2 * T * K + rows * K + 4 * rows * 2,
                   "quant_tokens": 2 * T * K + T * K + 4 * rows * 2,
@@ -353,7 +355,8 @@ def build_cases(names, dev):
                   "grouped_gather": T * K + 4 * rows + nonempty * Nn * K + 4 * rows
                                     + 4 * nonempty * Nn + 2 * rows * Nn,
                   "combine": 2 * rows * Nn + 4 * rows * 2 + 2 * T * Nn,
-                  "layer": 2 * T * K + nonempty * Nn * K + 2 * T * Nn}[stage]
+                  "layer": 2 * T * K + nonempty * Nn * K + 2 * T * Nn,
+                  "layer_permuted": 2 * T * K + nonempty * Nn * K + 2 * T * Nn}[stage]
         what = {"route": "MoE route (stable counting sort) of 4096x8 ids over 64 experts",
                 "permute": "MoE permute + per-row E4M3: 4096 tokens quantized once, K=2048, "
                            "scattered to their 32768 routed rows",
@@ -362,14 +365,18 @@ def build_cases(names, dev):
                 "combine": "MoE weighted combine of 32768 rows, N=1536 -> 4096 tokens",
                 "layer": "MoE projection cfg5: route + per-token E4M3 + grouped FP8 GEMM reading A "
                          "through the row map + combine",
+                "layer_permuted": "MoE projection cfg5 over the permuted copy: route + permute/quant + "
+                                  "grouped FP8 GEMM + combine",
                 "grouped": f"grouped FP8 GEMM of the routed rows (permuted copy), {rot} weight copies "
                            "rotated",
                 "grouped_gather": f"grouped FP8 GEMM of the routed rows, A read through the row map "
                                   f"from 4096 token-major rows, {rot} weight copies rotated"}[stage]
         if decode:
+            glue = ("per-token E4M3 + grouped FP8 GEMM reading A through the row map"
+                    if stage == "layer" and gather else "permute/quant + grouped FP8 GEMM")
             what = (f"MoE projection at decode size ({tokens} tokens x top-8 over 64 experts, N=1536 "
-                    f"K=2048): route + permute/quant + grouped FP8 GEMM + combine, {rot} weight copies "
-                    f"rotated") if stage == "layer" else what.replace("4096", str(tokens)).replace(
+                    f"K=2048): route + {glue} + combine, {rot} weight copies rotated"
+                    ) if stage.startswith("layer") else what.replace("4096", str(tokens)).replace(
                         "32768", str(rows))
         return Case(name, flops, nbytes, PEAK_FP8_TFLOPS,
                     "mfma" if flops and not decode else "hbm", launch, rot, what)
@@ -436,6 +443,8 @@ def build_cases(names, dev):
         "moe_grouped_permuted": lambda: moe_case("moe_grouped_permuted", "grouped"),
         "moe_grouped_gather": lambda: moe_case("moe_grouped_gather", "grouped_gather"),
         "moe_layer_decode": lambda: moe_case("moe_layer_decode", "layer", tokens=32),
+        "moe_layer_decode_permuted": lambda: moe_case("moe_layer_decode_permuted", "layer_permuted",
+                                                      tokens=32),
         "moe_combine": lambda: moe_case("moe_combine", "combine"),
         "moe_layer_cfg5": lambda: moe_case("moe_layer_cfg5", "layer"),
         "quant_fp8_block128_w": lambda: quant_case("quant_fp8_block128_w", "fp8_block128", 7168, 4096),
@@ -455,7 +464,7 @@ ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor
              "bf16_8192", "bf16_m4096", "bf16_m16",
              "rmsnorm_quant_fp8", "rmsnorm_then_quant_fp8", "swiglu_quant_fp8", "swiglu_then_quant_fp8",
              "moe_route", "moe_permute_quant", "moe_quant_tokens", "moe_combine", "moe_grouped_permuted",
-             "moe_grouped_gather", "moe_layer_cfg5", "moe_layer_decode", "lora_m4096", "bf16_4096",
+             "moe_grouped_gather", "moe_layer_cfg5", "moe_layer_decode", "moe_layer_decode_permuted", "lora_m4096", "bf16_4096",
              "quant_fp8_block128_w", "quant_fp8_row128_a", "quant_fp8_tensor_w", "quant_mxfp4_w",
              "quant_nvfp4_w"]
 

@@ -660,7 +660,7 @@ int dsl_moe_grouped_fp8_gemm(const uint8_t *x, int64_t tokens, const int32_t *sr
   p.out_f32 = out_dtype == DSL_OUT_F32;
   p.arow = src_token;
   p.xrows = (int)tokens;
-  return hip_status(dsl::launch_grouped_persist(p, static_cast<hipStream_t>(stream)), fn);
+  return hip_status(dsl::launch_grouped_fp8(p, static_cast<hipStream_t>(stream)), fn);
 }
 
 int dsl_moe_combine(const void *y, int64_t rows, int64_t n, int64_t ldy, const int32_t *dest,

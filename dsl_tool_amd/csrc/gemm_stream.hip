@@ -99,10 +99,12 @@ struct StreamRegs {
 
 // One workgroup's tile: C rows [m0, m0 + BM) x columns [n0, n0 + BN) of the
 // problem p over all of K.  gsx / gsw (grouped FP8): the output is (acc *
-// gsx[row]) * gsw[col] instead of the per-tensor scaling.
-template <class Cfg>
+// gsx[row]) * gsw[col] instead of the per-tensor scaling.  GATHER: row m of
+// the problem reads activation row arow[m] (clamped to [0, xrows)) of p.a;
+// each lane's row offsets are loaded once, before the first copy.
+template <class Cfg, bool GATHER = false>
 DSL_DEV void stream_tile(const GemmArgs &p, const int m0, const int n0, const float *gsx,
-                         const float *gsw) {
+                         const float *gsw, const int *arow = nullptr, int xrows = 0) {
   constexpr int TMA = Cfg::TMA, TN = Cfg::TN, NW = Cfg::NW, P = Cfg::P, DPI = Cfg::DPI;
   constexpr int NR = Cfg::NR, CHUNK = Cfg::CHUNK, SROW = Cfg::SROW;
   __shared__ __align__(16) uint8_t lds[Cfg::LDS];
@@ -116,6 +118,20 @@ DSL_DEV void stream_tile(const GemmArgs &p, const int m0, const int n0, const fl
   const uint32_t R0 = dec::lds_addr(my);
   const int nkg = p.K / 128;                 // FP8 block: scale groups per row
   const int64_t sld = p.K / 32;              // MXFP4: E8M0 bytes per row
+  // GATHER: byte offset of the activation row each of the lane's direct
+  // loads reads, per activation tile (xrows * Kb < 2^32)
+  uint32_t aoff[GATHER ? Cfg::TMA : 1][Cfg::DATA_DMA];
+  if constexpr (GATHER) {
+    const int sub = lane / Cfg::SPR;
+#pragma unroll
+    for (int t = 0; t < Cfg::TMA; ++t)
+#pragma unroll
+      for (int j = 0; j < Cfg::DATA_DMA; ++j) {
+        // entries outside [0, xrows), negative ones included, read row xrows - 1
+        const uint32_t tok = (uint32_t)arow[min(m0 + t * 16 + Cfg::RPD * j + sub, p.M - 1)];
+        aoff[t][j] = (tok >= (uint32_t)xrows ? (uint32_t)xrows - 1 : tok) * (uint32_t)p.Kb;
+      }
+  }
 
   // item it: chunk c_begin + it / P; kind it % P (< TN: W tile, else
   // activation tile kind - TN); region it % NR
@@ -132,7 +148,17 @@ DSL_DEV void stream_tile(const GemmArgs &p, const int m0, const int n0, const fl
     for (int j = 0; j < Cfg::DATA_DMA; ++j) {  // rows RPD*j + sub
       const int r = Cfg::RPD * j + sub;
       const int row = min(rbase + r, rlim);    // rows past the edge re-read the last row
-      const uint8_t *s = src + (int64_t)row * p.Kb + kb0 + ((slot ^ r) << 4);
+      int64_t roff = (int64_t)row * p.Kb;
+      if constexpr (GATHER) {
+        if (!isW) {                            // the activation tile's gathered row
+          uint32_t o = aoff[0][j];
+#pragma unroll
+          for (int t = 1; t < Cfg::TMA; ++t)
+            if (kind - TN == t) o = aoff[t][j];
+          roff = o;
+        }
+      }
+      const uint8_t *s = src + roff + kb0 + ((slot ^ r) << 4);
       if (isW) dec::dma16_nt(s, dst + j * 1024);
       else dec::dma16(s, dst + j * 1024);
     }
@@ -408,7 +434,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_stream_kernel(const GemmArgs p) 
 // and made non-decreasing, as the persistent grouped kernel does); blocks
 // past the total exit before any load.  A group's W slice is streamed once
 // per row block, so at decode sizes (a few rows per group) W is read once.
-template <class Cfg>
+template <class Cfg, bool GATHER>
 __global__ __launch_bounds__(Cfg::NT) void gemm_stream_grouped_kernel(const GroupedArgs gp) {
   __shared__ int s_pre[kMaxGroups + 1];      // row blocks before group e
   __shared__ int s_sum[Cfg::NW];
@@ -464,7 +490,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_stream_grouped_kernel(const Grou
   const int e = __builtin_amdgcn_readfirstlane(l);
   const int lo = off_of(e), hi0 = off_of(e + 1), hi = hi0 < lo ? lo : hi0;
   GemmArgs q{};
-  q.a = gp.x + (int64_t)lo * gp.K;
+  q.a = GATHER ? gp.x : gp.x + (int64_t)lo * gp.K;   // gathered rows index x itself
   q.b = gp.w + (int64_t)e * gp.N * gp.K;
   q.c = static_cast<uint8_t *>(gp.y) + (int64_t)lo * gp.ldy * (gp.out_f32 ? 4 : 2);
   q.M = hi - lo;
@@ -473,8 +499,8 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_stream_grouped_kernel(const Grou
   q.Kb = gp.K;
   q.ldc = gp.ldy;
   q.out_f32 = gp.out_f32;
-  stream_tile<Cfg>(q, (id - s_pre[e]) * Cfg::BM, nblk * Cfg::BN, gp.sx + lo,
-                   gp.sw + (int64_t)e * gp.N);
+  stream_tile<Cfg, GATHER>(q, (id - s_pre[e]) * Cfg::BM, nblk * Cfg::BN, gp.sx + lo,
+                           gp.sw + (int64_t)e * gp.N, GATHER ? gp.arow + lo : nullptr, gp.xrows);
 }
 
 // ---------------------------------------------------------------- plans --
@@ -557,13 +583,17 @@ hipError_t launch_grouped_cfg(const GroupedArgs &gp, hipStream_t st) {
   const int64_t blocks = (gp.rows + Cfg::BM - 1) / Cfg::BM + gp.G;   // >= sum of per-group blocks
   const int64_t grid = blocks * nnb;
   if (grid >= ((int64_t)1 << 31)) return hipErrorInvalidValue;
-  gemm_stream_grouped_kernel<Cfg><<<(unsigned)grid, Cfg::NT, 0, st>>>(gp);
+  if (gp.arow)
+    gemm_stream_grouped_kernel<Cfg, true><<<(unsigned)grid, Cfg::NT, 0, st>>>(gp);
+  else
+    gemm_stream_grouped_kernel<Cfg, false><<<(unsigned)grid, Cfg::NT, 0, st>>>(gp);
   return hipGetLastError();
 }
 
 }  // namespace
 
 bool grouped_stream_supported(const GroupedArgs &gp) {
+  if (gp.arow && (gp.xrows < 1 || (int64_t)gp.xrows * gp.K >= ((int64_t)1 << 32))) return false;
   return gp.G >= 1 && gp.G <= kMaxGroups && gp.K % 256 == 0 && gp.K >= 256 && gp.N >= 1;
 }
 

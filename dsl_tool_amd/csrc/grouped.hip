@@ -233,9 +233,11 @@ static void launch_grouped_pipe_cfg(const GroupedArgs &p, hipStream_t st) {
 
 hipError_t launch_grouped_fp8(GroupedArgs p, hipStream_t st) {
   if (p.rows == 0 || p.N == 0) return hipSuccess;
-  if (p.arow)   // the gather form: the persistent kernel only
-    return grouped_persist_supported(p) ? launch_grouped_persist(p, st) : hipErrorInvalidValue;
   const int avg = p.rows / (p.G > 0 ? p.G : 1);
+  if (p.arow) {   // the gather form: streaming tiles at decode sizes, else the persistent kernel
+    if (avg < 48 && grouped_stream_supported(p)) return launch_grouped_stream(p, st);
+    return grouped_persist_supported(p) ? launch_grouped_persist(p, st) : hipErrorInvalidValue;
+  }
   // DSL_GEMM_PERSIST=0 keeps the per-tile pipelined walk below (tuning)
   static const bool persist_on = [] {
     const char *e = getenv("DSL_GEMM_PERSIST");

@@ -131,11 +131,11 @@ def moe_grouped_fp8_gemm(qx: torch.Tensor, sx: torch.Tensor, route: Route, qw: t
 
 
 def gather_applies(tokens: int, topk: int, num_experts: int, k: int) -> bool:
-    """Whether the routed GEMM reads A through the row map: the persistent
-    grouped kernel (groups averaging 48 rows or more; fewer take the
-    streaming tiles over the permuted copy), k % 128 == 0, tokens < 2^24 and
-    tokens * k < 2^32."""
-    return (k % 128 == 0 and (tokens * topk) // max(num_experts, 1) >= 48
+    """Whether the routed GEMM reads A through the row map: k % 128 == 0,
+    tokens < 2^24 and tokens * k < 2^32.  Groups averaging 48 rows or more
+    take the persistent grouped kernel, fewer the streaming grouped tiles
+    (k % 256 == 0; else the persistent kernel again)."""
+    return (k % 128 == 0 and 1 <= num_experts <= 2048
             and tokens < (1 << 24) and tokens * k < (1 << 32))
 
 

@@ -140,9 +140,15 @@ def _expert_weights(E, Nn, K, seed):
 # The gather kernel against the persistent kernel over the permuted copy:
 # the same codes, scales and MFMA order, so the same bits.  K = 128 is one
 # pair per tile (the next tile's row table is waited for before the first
-# copies); ragged N; one expert; config 5's routing and sizes.
+# copies); ragged N; one expert; config 5's routing and sizes.  Below 48
+# rows per group on average the gather streams (the streaming grouped tiles
+# over the permuted copy are the reference): decode sizes with 16- and
+# 32-row blocks, K of an odd number of 256-byte chunks, ragged N, and
+# K % 256 != 0 (the persistent kernel again).
 GATHER_CASES = [(512, 4, 16, 1024, 768), (300, 3, 2, 128, 520), (1000, 2, 5, 256, 256),
-                (2000, 1, 1, 384, 300), (4096, 8, 64, 2048, 1536)]
+                (2000, 1, 1, 384, 300), (4096, 8, 64, 2048, 1536),
+                (32, 8, 64, 2048, 1536), (1, 8, 64, 2048, 1536), (200, 8, 64, 2048, 1536),
+                (7, 2, 3, 256, 520), (40, 4, 8, 768, 300), (30, 2, 4, 384, 256)]
 
 
 @pytest.mark.parametrize("T,k,E,K,Nn", GATHER_CASES)
@@ -167,17 +173,18 @@ def test_gather_gemm_equals_permuted(T, k, E, K, Nn, out_dtype):
                        yp[:n].view(torch.int16 if out_dtype == torch.bfloat16 else torch.int32))
 
 
-def test_gather_gemm_clamps_bad_row_map():
+@pytest.mark.parametrize("T,k,E", [(700, 2, 3), (40, 4, 8)])   # persistent, streaming
+def test_gather_gemm_clamps_bad_row_map(T, k, E):
     # row-map entries outside [0, tokens) read the last token's row
     from dsl_tool_amd import gemm as G
-    T, k, E, K, Nn = 700, 2, 3, 256, 384
+    K, Nn = 256, 384
     ids = _ids(T, k, E, 460)
     x = W.randn_bf16((T, K), 461).to(DEV)
     qw, sw = _expert_weights(E, Nn, K, 462)
     r = M.moe_route(ids.to(DEV), E)
     qt, st = M.moe_quant_tokens(x, r)
     bad = r.src_token.clone()
-    bad[5], bad[300], bad[1000] = -7, T, 1 << 30          # first tile, later tiles
+    bad[5], bad[(T * k) // 2], bad[T * k - 1] = -7, T, 1 << 30   # first tile, later tiles
     rb = r._replace(src_token=bad)
     yg = M.moe_grouped_fp8_gemm(qt, st, rb, qw, sw)
     qp = qt[bad.clamp(0, T - 1).long()]                    # -7 -> 2^32 - 7 -> last token too
