@@ -118,19 +118,18 @@ DSL_DEV void stream_tile(const GemmArgs &p, const int m0, const int n0, const fl
   const uint32_t R0 = dec::lds_addr(my);
   const int nkg = p.K / 128;                 // FP8 block: scale groups per row
   const int64_t sld = p.K / 32;              // MXFP4: E8M0 bytes per row
-  // GATHER: byte offset of the activation row each of the lane's direct
-  // loads reads, per activation tile (xrows * Kb < 2^32)
-  uint32_t aoff[GATHER ? Cfg::TMA : 1][Cfg::DATA_DMA];
+  // GATHER: the activation row each of the lane's direct loads reads, per
+  // activation tile, as loaded; clamped and scaled to a byte offset only
+  // where an activation copy is issued, so that the prologue's W copies
+  // (issued first) do not wait for these loads
+  int tokv[GATHER ? Cfg::TMA : 1][Cfg::DATA_DMA];
   if constexpr (GATHER) {
     const int sub = lane / Cfg::SPR;
 #pragma unroll
     for (int t = 0; t < Cfg::TMA; ++t)
 #pragma unroll
-      for (int j = 0; j < Cfg::DATA_DMA; ++j) {
-        // entries outside [0, xrows), negative ones included, read row xrows - 1
-        const uint32_t tok = (uint32_t)arow[min(m0 + t * 16 + Cfg::RPD * j + sub, p.M - 1)];
-        aoff[t][j] = (tok >= (uint32_t)xrows ? (uint32_t)xrows - 1 : tok) * (uint32_t)p.Kb;
-      }
+      for (int j = 0; j < Cfg::DATA_DMA; ++j)
+        tokv[t][j] = arow[min(m0 + t * 16 + Cfg::RPD * j + sub, p.M - 1)];
   }
 
   // item it: chunk c_begin + it / P; kind it % P (< TN: W tile, else
@@ -151,11 +150,13 @@ DSL_DEV void stream_tile(const GemmArgs &p, const int m0, const int n0, const fl
       int64_t roff = (int64_t)row * p.Kb;
       if constexpr (GATHER) {
         if (!isW) {                            // the activation tile's gathered row
-          uint32_t o = aoff[0][j];
+          uint32_t tok = (uint32_t)tokv[0][j];
 #pragma unroll
           for (int t = 1; t < Cfg::TMA; ++t)
-            if (kind - TN == t) o = aoff[t][j];
-          roff = o;
+            if (kind - TN == t) tok = (uint32_t)tokv[t][j];
+          // entries outside [0, xrows), negative ones included, read row
+          // xrows - 1 (xrows * Kb < 2^32)
+          roff = (tok >= (uint32_t)xrows ? (uint32_t)xrows - 1 : tok) * (uint32_t)p.Kb;
         }
       }
       const uint8_t *s = src + roff + kb0 + ((slot ^ r) << 4);
