@@ -27,13 +27,13 @@ DSL_ERR_UNSUPPORTED = -2
 DSL_ERR_WORKSPACE = -3
 DSL_ERR_HIP = -4
 OUT_BF16, OUT_F32 = 0, 1
-SCALE_TENSOR, SCALE_BLOCK128 = 0, 1
+SCALE_TENSOR, SCALE_BLOCK128, SCALE_GROUP128 = 0, 1, 2
 FMT_MXFP4, FMT_NVFP4 = 0, 1
 OP_FP8, OP_FP4, OP_GROUPED_FP8, OP_BF16 = 0, 1, 2, 3
 QFMT_FP8_G128, QFMT_MXFP4 = 0, 1
 W_BF16, W_F32 = 0, 1
 IN_BF16, IN_F32 = 0, 1
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 
 class DslLibraryError(ImportError):

@@ -83,7 +83,7 @@ extern "C" {
 
 const char *dsl_last_error(void) { return g_err.c_str(); }
 
-int dsl_abi_version(void) { return 8; }
+int dsl_abi_version(void) { return 9; }
 
 size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
   (void)rows;
@@ -187,8 +187,9 @@ size_t dsl_gemm_workspace_bytes(int op, int64_t m, int64_t n, int64_t k) {
   // the larger of the two plans
   auto mx = [](size_t a, size_t b) { return a > b ? a : b; };
   if (op == DSL_OP_FP8)
-    return mx(dsl::gemm_workspace_bytes(dsl::MODE_FP8_TENSOR, m, n, k),
-              dsl::gemm_workspace_bytes(dsl::MODE_FP8_BLOCK, m, n, k));
+    return mx(mx(dsl::gemm_workspace_bytes(dsl::MODE_FP8_TENSOR, m, n, k),
+                 dsl::gemm_workspace_bytes(dsl::MODE_FP8_BLOCK, m, n, k)),
+              dsl::gemm_workspace_bytes(dsl::MODE_FP8_GCOL, m, n, k));
   if (op == DSL_OP_FP4)
     return mx(dsl::gemm_workspace_bytes(dsl::MODE_MXFP4, m, n, k),
               dsl::gemm_workspace_bytes(dsl::MODE_NVFP4, m, n, k));
@@ -246,6 +247,12 @@ int dsl_fp8_gemm(const uint8_t *a, const uint8_t *b, void *c, int64_t m, int64_t
   if (scale_mode == DSL_SCALE_BLOCK128)
     return run_gemm(fn, dsl::MODE_FP8_BLOCK, a, b, c, m, n, k, ldc, out_dtype, scale_a, scale_b,
                     nullptr, nullptr, ws, ws_bytes, stream);
+  if (scale_mode == DSL_SCALE_GROUP128) {
+    if (!aligned(scale_a, 4) || !aligned(scale_b, 4))
+      return fail(DSL_ERR_ARG, "%s: scale arrays must be 4-byte aligned", fn);
+    return run_gemm(fn, dsl::MODE_FP8_GCOL, a, b, c, m, n, k, ldc, out_dtype, scale_a, scale_b,
+                    nullptr, nullptr, ws, ws_bytes, stream);
+  }
   return fail(DSL_ERR_ARG, "%s: unknown scale_mode %d", fn, scale_mode);
 }
 

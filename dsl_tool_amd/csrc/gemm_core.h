@@ -14,6 +14,7 @@
 //   FP8_TENSOR  unscaled fp8 MFMA over all K, (acc * sa) * sb in the epilogue;
 //   FP8_BLOCK   one fresh MFMA partial per 128-K group, folded into the fp32
 //               accumulator as acc += part * (sa[m,g] * sb[n/128,g]);
+//   FP8_GCOL    the same with one weight scale per column: sb[g,n];
 //   MXFP4       E8M0 bytes go straight into v_mfma_scale_f32_16x16x128_f8f6f4;
 //   NVFP4       E2M1 -> fp16 (hardware convert), times the E4M3 block scale
 //               in fp16 (exact), fp16 MFMA; global scales in the epilogue;
@@ -39,8 +40,9 @@ struct TileCfg {
   static constexpr int SCB = MODE == MODE_MXFP4 ? 8 : (MODE == MODE_NVFP4 ? 16 : 0);
   static constexpr int SBN = BN >= 128 ? BN / 128 : 1;           // FP8_BLOCK weight scales / stage
   static constexpr int A_BYTES = BM * 128, B_BYTES = BN * 128;
-  static constexpr int SA_BYTES = MODE == MODE_FP8_BLOCK ? BM * 4 : BM * SCB;
-  static constexpr int SB_BYTES = MODE == MODE_FP8_BLOCK ? 16 * ((SBN * 4 + 15) / 16) : BN * SCB;
+  static constexpr int SA_BYTES = mode_grouped_k(MODE) ? BM * 4 : BM * SCB;
+  static constexpr int SB_BYTES = MODE == MODE_FP8_BLOCK ? 16 * ((SBN * 4 + 15) / 16)
+                                  : (MODE == MODE_FP8_GCOL ? BN * 4 : BN * SCB);
   static constexpr int OFF_B = 2 * A_BYTES;
   static constexpr int OFF_SA = OFF_B + 2 * B_BYTES;
   static constexpr int OFF_SB = OFF_SA + 2 * SA_BYTES;
@@ -56,9 +58,9 @@ struct TileView {
   const uint8_t *b;     // row n0 of B
   int a_rows, b_rows;   // valid rows (<= BM / BN)
   int Kb, K;            // bytes per packed row, K in elements
-  const void *sa;       // MX/NV: scale row m0; FP8_BLOCK: float row m0 ([.][nkg])
-  const void *sb;       // MX/NV: scale row n0; FP8_BLOCK: float row n0/128
-  int64_t sa_ld, sb_ld; // scale row pitch (elements)
+  const void *sa;       // MX/NV: scale row m0; FP8_BLOCK / GCOL: float row m0 ([.][nkg])
+  const void *sb;       // MX/NV: scale row n0; FP8_BLOCK: float row n0/128; GCOL: &sb[0][n0]
+  int64_t sa_ld, sb_ld; // scale row pitch (elements; GCOL sb: N, one row per group)
 };
 
 DSL_DEV int swz(int row, int ch) { return (ch ^ (row & 7)) << 4; }
@@ -114,6 +116,15 @@ DSL_DEV void stage_load(const TileView &tv, int ks, StageRegs<Cfg> &r) {
       r.sa = load_row(static_cast<const uint8_t *>(tv.sa), tv.sa_ld, tid, tv.a_rows);
     if (tid < Cfg::BN)
       r.sb = load_row(static_cast<const uint8_t *>(tv.sb), tv.sb_ld, tid, tv.b_rows);
+  } else if constexpr (MODE == MODE_FP8_GCOL) {
+    if (tid < Cfg::BM)
+      r.sa.x = tid < tv.a_rows
+                   ? f2u(static_cast<const float *>(tv.sa)[(int64_t)tid * tv.sa_ld + ks])
+                   : 0u;
+    if (tid < Cfg::BN)
+      r.sb.x = tid < tv.b_rows
+                   ? f2u(static_cast<const float *>(tv.sb)[(int64_t)ks * tv.sb_ld + tid])
+                   : 0u;
   } else if constexpr (MODE == MODE_FP8_BLOCK) {
     if (tid < Cfg::BM)
       r.sa.x = tid < tv.a_rows
@@ -170,6 +181,9 @@ DSL_DEV void stage_store(uint8_t *smem, int buf, const StageRegs<Cfg> &r) {
   } else if constexpr (MODE == MODE_FP8_BLOCK) {
     if (tid < Cfg::BM) reinterpret_cast<uint32_t *>(sSa)[tid] = r.sa.x;
     if (tid < Cfg::SBN) reinterpret_cast<uint32_t *>(sSb)[tid] = r.sb.x;
+  } else if constexpr (MODE == MODE_FP8_GCOL) {
+    if (tid < Cfg::BM) reinterpret_cast<uint32_t *>(sSa)[tid] = r.sa.x;
+    if (tid < Cfg::BN) reinterpret_cast<uint32_t *>(sSb)[tid] = r.sb.x;
   }
 }
 
@@ -220,7 +234,7 @@ DSL_DEV void stage_compute(const uint8_t *smem, int buf, v4f (&acc)[Cfg::TM][Cfg
   const uint8_t *sSb = smem + Cfg::OFF_SB + buf * Cfg::SB_BYTES;
   const int arow0 = wm * Cfg::WM + r16, brow0 = wn * Cfg::WN + r16;
 
-  if constexpr (MODE == MODE_FP8_TENSOR || MODE == MODE_FP8_BLOCK || MODE == MODE_BF16) {
+  if constexpr (MODE == MODE_FP8_TENSOR || mode_grouped_k(MODE) || MODE == MODE_BF16) {
     v8i bop[Cfg::TN];
 #pragma unroll
     for (int tn = 0; tn < Cfg::TN; ++tn) {
@@ -230,9 +244,13 @@ DSL_DEV void stage_compute(const uint8_t *smem, int buf, v4f (&acc)[Cfg::TM][Cfg
       const v4i hi = *reinterpret_cast<const v4i *>(rp + swz(row, 2 * g + 1));
       bop[tn] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
-    float sbv = 0.f;
+    float sbv = 0.f, sbc[Cfg::TN];   // BLOCK: the wave's 128-column block; GCOL: per column
     if constexpr (MODE == MODE_FP8_BLOCK)
       sbv = reinterpret_cast<const float *>(sSb)[(wn * Cfg::WN) / 128];
+    if constexpr (MODE == MODE_FP8_GCOL) {
+#pragma unroll
+      for (int tn = 0; tn < Cfg::TN; ++tn) sbc[tn] = reinterpret_cast<const float *>(sSb)[brow0 + tn * 16];
+    }
 #pragma unroll
     for (int tm = 0; tm < Cfg::TM; ++tm) {
       const int row = arow0 + tm * 16;
@@ -254,7 +272,8 @@ DSL_DEV void stage_compute(const uint8_t *smem, int buf, v4f (&acc)[Cfg::TM][Cfg
 #pragma unroll
         for (int tn = 0; tn < Cfg::TN; ++tn) {
           const v4f part = mfma_fp8(aop, bop[tn], zero);
-          acc[tm][tn] = part * s4 + acc[tm][tn];
+          if constexpr (MODE == MODE_FP8_GCOL) acc[tm][tn] = part * (sa4 * sbc[tn]) + acc[tm][tn];
+          else acc[tm][tn] = part * s4 + acc[tm][tn];
         }
       }
     }

@@ -468,13 +468,14 @@ hipError_t launch_gemm_decode(int mode, const GemmArgs &p, hipStream_t st) {
     case MODE_FP8_BLOCK: return launch_decode_mode<MODE_FP8_BLOCK>(p, st);
     case MODE_MXFP4: return launch_decode_mode<MODE_MXFP4>(p, st);
     case MODE_BF16: return launch_decode_mode<MODE_BF16>(p, st);
-    default:
+    case MODE_NVFP4:
       switch (p.M) {
         case 1: return launch_gemv_nv_m<1>(p, st);
         case 2: return launch_gemv_nv_m<2>(p, st);
         case 3: return launch_gemv_nv_m<3>(p, st);
         default: return launch_gemv_nv_m<4>(p, st);
       }
+    default: return hipErrorInvalidValue;   // FP8_GCOL: decode_supported is false
   }
 }
 

@@ -78,11 +78,15 @@ void gemm_pipe_kernel(const GemmArgs p) {
 // folded at once into the fp32 accumulator as acc += part * sa[m,g] * sb[n/128,g]
 // (the group-partial form of cuda/gemm/fp8_gemm.cu:84-97).  Activation
 // scales travel with the stage; the weight scale of the wave's 128-column
-// block is one scalar load per stage.
+// block is one scalar load per stage.  With per-column weight scales
+// (MODE_FP8_GCOL, sb[g][n] as fp8_gemm_groupwise_kernel reads them) the
+// stage also carries the tile's BN weight scales of its group, and each
+// lane folds part * (sa[m,g] * sb[g,n]) for its own column.
 template <class Cfg>
 __global__ __launch_bounds__(Cfg::NT) __attribute__((amdgpu_waves_per_eu(Cfg::OCC, Cfg::OCC)))
 void gemm_pipe_block_kernel(const GemmArgs p) {
-  static_assert(Cfg::BLOCK && Cfg::WN <= 128 && 128 % Cfg::WN == 0, "block-scale tiling");
+  static_assert(Cfg::BLOCK && (Cfg::GCOL || (Cfg::WN <= 128 && 128 % Cfg::WN == 0)),
+                "block-scale tiling");
   constexpr int NS = Cfg::NS, D = Cfg::D, SKB = Cfg::SKB;
   constexpr int TM = Cfg::WM / 16, TN = Cfg::WN / 16;
   __shared__ __align__(16) uint8_t smem[Cfg::LDS];
@@ -115,7 +119,7 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     for (int j = 0; j < TN; ++j) acc[i][j] = (v4f){0.f, 0.f, 0.f, 0.f};
 
   for (int ks = 0; ks < nks; ++ks) {
-    const float sbv = sbp[ks];
+    const float sbv = Cfg::GCOL ? 1.f : sbp[ks];
     if (ks + NS - 2 < nks) pipe::wait_vmcnt<(NS - 2) * D>();
     else pipe::wait_vmcnt<0>();
     __syncthreads();
@@ -123,6 +127,11 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     const uint8_t *st = smem + (ks % NS) * Cfg::STAGE;
     const uint8_t *sA = st, *sB = st + Cfg::A_BYTES;
     const float *sSa = reinterpret_cast<const float *>(st + Cfg::A_BYTES + Cfg::B_BYTES);
+    float sbc[TN];                       // GCOL: the lane's column scale per 16-column tile
+    if constexpr (Cfg::GCOL) {
+#pragma unroll
+      for (int t = 0; t < TN; ++t) sbc[t] = sSa[Cfg::BM + wn * Cfg::WN + t * 16 + r16];
+    }
     auto ld = [&](const uint8_t *base, int row) {
       const int s = pipe::swz<SKB>(row);
       const v4i lo = *reinterpret_cast<const v4i *>(base + row * SKB + (((2 * g) ^ s) << 4));
@@ -142,7 +151,8 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
       for (int j = 0; j < TN; ++j) {
         const v4f part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], zero, 0, 0, 0,
                                                                           0, 0, 0);
-        acc[i][j] = part * s4 + acc[i][j];
+        if constexpr (Cfg::GCOL) acc[i][j] = part * (s4 * sbc[j]) + acc[i][j];
+        else acc[i][j] = part * s4 + acc[i][j];
       }
     }
   }
@@ -446,7 +456,13 @@ static hipError_t launch_pipe_cfg(const GemmArgs &p, hipStream_t st) {
 // alternatives for tuning (DSL_GEMM_PIPE).
 hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_t st) {
   // C += result: fp32 output through the plain epilogue only
-  if (p.accumulate && (!p.out_f32 || mode == MODE_FP8_BLOCK)) return hipErrorInvalidValue;
+  if (p.accumulate && (!p.out_f32 || mode_grouped_k(mode))) return hipErrorInvalidValue;
+  if (mode == MODE_FP8_GCOL) {
+    // per-column weight scales: the per-stage partial kernel (4-byte
+    // aligned scales, K % 128 == 0)
+    if (variant == 0) return launch_pipe_cfg<PipeCfg<MODE_FP8_GCOL, 256, 256, 2, 4, 2, 128>>(p, st);
+    return launch_pipe_cfg<PipeCfg<MODE_FP8_GCOL, 128, 128, 2, 2, 2, 128, 2>>(p, st);
+  }
   if (mode == MODE_BF16) return launch_pipe_cfg<PipeCfg<MODE_BF16, 128, 128, 2, 2, 4, 64>>(p, st);
   if (mode == MODE_FP8_BLOCK) {
     const bool ring_ok = p.K % 512 == 0 && p.K / 128 <= kBlockPfMaxGroups &&

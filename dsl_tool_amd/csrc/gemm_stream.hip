@@ -33,7 +33,9 @@
 // superblock, op_sel j picks the byte).  A and W share the order, so the
 // sum is unchanged.  FP8 block: each 128-byte step is one 128-K group,
 // folded as acc += part * (sa[m][grp] * sb[n/128][grp]), the group-partial
-// form of cuda/gemm/fp8_gemm.cu:84-97.  NVFP4: its E4M3 scales (one per
+// form of cuda/gemm/fp8_gemm.cu:84-97; FP8 groupwise with per-column weight
+// scales (that function's own layout sb[grp][n]) folds sa[m][grp] *
+// sb[grp][n], one weight scale per lane (its output column) and group.  NVFP4: its E4M3 scales (one per
 // 16 elements) are not powers of two, so both operands are dequantized
 // exactly to fp16 (E2M1 x E4M3 has at most 6 significant bits) and go to
 // v_mfma_f32_16x16x32_f16; a lane takes one 16-byte chunk per 128-element
@@ -55,7 +57,8 @@ struct StreamCfg {
   static constexpr int BM = 16 * TMA, BN = 16 * TN;
   static constexpr int NW = 4, NT = NW * 64;         // waves split K
   static constexpr bool MX = MODE == MODE_MXFP4;
-  static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;
+  static constexpr bool BLOCK = mode_grouped_k(MODE);   // fp32 scales per 128-K group
+  static constexpr bool GCOL = MODE == MODE_FP8_GCOL;   // ... per W row (output column)
   static constexpr bool NV = MODE == MODE_NVFP4;
   static constexpr int CHUNK = CHUNK_;               // bytes of one row per item
   static constexpr int STEPS = CHUNK / 128;          // 128-byte MFMA steps (FP8 block: groups)
@@ -91,7 +94,8 @@ struct StreamRegs {
   v8i wf[Cfg::TN][Cfg::STEPS];      // FP8 / bf16 W fragments of the current chunk
   v4i wq[Cfg::TN][Cfg::SBK][4];     // MXFP4 W fragments (16 bytes per step)
   int ws[Cfg::TN][Cfg::SBK];        // MXFP4 W E8M0 words
-  float sb[Cfg::STEPS];             // FP8 block: weight scales of the chunk's groups
+  float sb[Cfg::GCOL ? Cfg::TN : 1][Cfg::STEPS];   // FP8 block / groupwise: weight scales
+                                                   // of the chunk's groups (GCOL: the lane's column)
   v4i wn[Cfg::TN][Cfg::NSB];        // NVFP4: the lane's 16-byte W chunk of each superblock
   uint32_t wsn[Cfg::TN][Cfg::NSB];  // NVFP4: that chunk's two E4M3 block scales (low 16 bits)
   v4f acc[Cfg::TN][Cfg::TMA];
@@ -170,6 +174,17 @@ DSL_DEV void stream_tile(const GemmArgs &p, const int m0, const int n0, const fl
       const int sr = (lane / PARTS) & 15, part = lane % PARTS;
       const int row = isW ? (Cfg::BLOCK ? n0 : min(rbase + sr, rlim)) : min(rbase + sr, rlim);
       const uint8_t *sc;
+      if constexpr (Cfg::GCOL) {
+        if (isW) {
+          // sb[grp][n] of the tile's 16 columns and the chunk's STEPS groups:
+          // lane -> column lane % 16, group lane / 16 (repeated past STEPS),
+          // stored [group][column]; 16 lanes read 64 contiguous bytes
+          const int col = min(rbase + (lane & 15), rlim);
+          const int grp = ch * Cfg::STEPS + ((lane >> 4) & (Cfg::STEPS - 1));
+          dec::dma4(static_cast<const float *>(p.sb) + (int64_t)grp * p.N + col, dst + 16 * CHUNK);
+          return;
+        }
+      }
       if constexpr (Cfg::MX) {
         sc = static_cast<const uint8_t *>(isW ? p.sb : p.sa) + row * sld + kb0 / 16;
       } else if constexpr (Cfg::NV) {   // E4M3 per 16 elements: K/16 bytes per row
@@ -221,9 +236,13 @@ DSL_DEV void stream_tile(const GemmArgs &p, const int m0, const int n0, const fl
           const v4i lo = chunk16(base, s * 8 + g), hi = chunk16(base, s * 8 + g + 4);
           st.wf[KIND][s] = (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
-        if constexpr (Cfg::BLOCK) {
+        if constexpr (Cfg::GCOL) {
 #pragma unroll
-          for (int s = 0; s < Cfg::STEPS; ++s) st.sb[s] = reinterpret_cast<const float *>(aux)[s];
+          for (int s = 0; s < Cfg::STEPS; ++s)
+            st.sb[KIND][s] = reinterpret_cast<const float *>(aux)[s * 16 + r16];
+        } else if constexpr (Cfg::BLOCK) {
+#pragma unroll
+          for (int s = 0; s < Cfg::STEPS; ++s) st.sb[0][s] = reinterpret_cast<const float *>(aux)[s];
         }
       }
     } else {                                    // activation tile x the W tiles
@@ -285,7 +304,8 @@ DSL_DEV void stream_tile(const GemmArgs &p, const int m0, const int n0, const fl
             if constexpr (Cfg::BLOCK) {
               const v4f zero = {0.f, 0.f, 0.f, 0.f};
               const v4f part = mfma_fp8(af, st.wf[t][s], zero);
-              const v4f sc = (v4f){sa[0][s], sa[1][s], sa[2][s], sa[3][s]} * st.sb[s];
+              const v4f sc = (v4f){sa[0][s], sa[1][s], sa[2][s], sa[3][s]} *
+                             st.sb[Cfg::GCOL ? t : 0][s];
               st.acc[t][A] = part * sc + st.acc[t][A];
             } else if constexpr (Cfg::MODE == MODE_BF16) {
               st.acc[t][A] = mfma_bf16(af, st.wf[t][s], st.acc[t][A]);
@@ -543,7 +563,7 @@ StreamPlan plan_for(int mode, int M, int N, int Kb) {
   }
   const char *e = getenv("DSL_GEMM_STREAM_TN");
   if (e && (e[0] == '1' || e[0] == '2' || e[0] == '4') && !e[1]) pl.tn = e[0] - '0';
-  if (pl.tn == 4 && mode == MODE_FP8_BLOCK && pl.tma == 4) pl.tn = 2;   // register budget
+  if (pl.tn == 4 && mode_grouped_k(mode) && pl.tma == 4) pl.tn = 2;   // register budget
   if (pl.tn == 4 && mode == MODE_NVFP4 && pl.tma == 4) pl.tn = 2;      // register budget
   return pl;
 }
@@ -563,7 +583,7 @@ hipError_t launch_tn(const GemmArgs &p, int tn, hipStream_t st) {
   if (tn == 1) return launch_cfg<MODE, TMA, 1, CHUNK>(p, st);
   // four W tiles beside four activation tiles exceed the registers of the
   // FP8 block and NVFP4 forms (plan_for never asks for them)
-  constexpr bool four = !(TMA == 4 && (MODE == MODE_FP8_BLOCK || MODE == MODE_NVFP4));
+  constexpr bool four = !(TMA == 4 && (mode_grouped_k(MODE) || MODE == MODE_NVFP4));
   if constexpr (four) {
     if (tn == 4) return launch_cfg<MODE, TMA, 4, CHUNK>(p, st);
   }
@@ -618,7 +638,7 @@ bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16) {
   if (Kb % 256 != 0) return false;   // 512-byte chunks where they fit, else 256
   if (mode == MODE_FP8_TENSOR || mode == MODE_BF16) return true;
   // block scales and E8M0 rows move by 16-byte direct loads (K % 512)
-  if (mode == MODE_FP8_BLOCK || mode == MODE_MXFP4) return scales16 && K % 512 == 0;
+  if (mode_grouped_k(mode) || mode == MODE_MXFP4) return scales16 && K % 512 == 0;
   // E4M3 rows (K/16 bytes) move by 16-byte direct loads
   if (mode == MODE_NVFP4) return scales16 && K % 256 == 0;
   return false;
@@ -632,6 +652,7 @@ hipError_t launch_gemm_stream(int mode, const GemmArgs &p, hipStream_t st) {
   switch (mode) {
     case MODE_FP8_TENSOR: return launch_mode<MODE_FP8_TENSOR>(p, pl, st);
     case MODE_FP8_BLOCK: return launch_mode<MODE_FP8_BLOCK>(p, pl, st);
+    case MODE_FP8_GCOL: return launch_mode<MODE_FP8_GCOL>(p, pl, st);
     case MODE_MXFP4: return launch_mode<MODE_MXFP4>(p, pl, st);
     case MODE_BF16: return launch_mode<MODE_BF16>(p, pl, st);
     case MODE_NVFP4: return launch_mode<MODE_NVFP4>(p, pl, st);

@@ -35,6 +35,12 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_tiled_kernel(const GemmArgs p) {
     tv.sa = static_cast<const float *>(p.sa) + (int64_t)m0 * nkg;
     tv.sb = static_cast<const float *>(p.sb) + (int64_t)(n0 / 128) * nkg;
     tv.sa_ld = tv.sb_ld = nkg;
+  } else if constexpr (MODE == MODE_FP8_GCOL) {
+    const int64_t nkg = (p.K + 127) / 128;
+    tv.sa = static_cast<const float *>(p.sa) + (int64_t)m0 * nkg;
+    tv.sb = static_cast<const float *>(p.sb) + n0;
+    tv.sa_ld = nkg;
+    tv.sb_ld = p.N;
   }
 
   const int nks = (p.Kb + 127) / 128;
@@ -247,7 +253,7 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   if (streamable && !skinny_stream && M > 32 && (mode != MODE_NVFP4 || M > 256)) {
     const int bm = Kb % 512 == 0 ? 64 : 32;
     const int64_t span2 = 2 * (int64_t)((M + bm - 1) / bm) * N;   // twice the span
-    const int64_t thr2 = mode == MODE_FP8_BLOCK ? 15
+    const int64_t thr2 = mode_grouped_k(mode) ? 15
                          : (mode == MODE_BF16 ? (bf16_pipe_round ? 20 : 36)
                                               : (mode == MODE_NVFP4 ? 30 : 17));
     if (span2 >= thr2 * 4096) streamable = false;
@@ -317,7 +323,7 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
     // K = 4096 and 8192, M = 288..3072.
     const int64_t cus = device_cu_count();
     const int64_t r128 = (t128 + cus - 1) / cus, r256 = (t256 + cus - 1) / cus;
-    const bool persist_wins = t256 >= 240 || r128 >= (mode == MODE_FP8_BLOCK ? 3 : 2) * r256;
+    const bool persist_wins = t256 >= 240 || r128 >= (mode_grouped_k(mode) ? 3 : 2) * r256;
     if (persist_wins) {
       r.path = PATH_PIPE;
       r.variant = pipe_forced >= 0 ? pipe_forced : (t256 >= 240 ? 0 : 1);
@@ -337,7 +343,7 @@ bool gemm_routes_to_stream(int mode, int64_t M, int64_t N, int64_t K, bool or_pi
   int path = route_for(mode, (int)M, (int)N, (int)K, Kb, true, true).path;
   if (accumulate && K <= kAccShortK && stream_enabled() && stream_supported(mode, (int)M, (int)N, (int)K, Kb, true))
     path = PATH_STREAM;   // as launch_gemm routes C += result
-  return path == PATH_STREAM || (or_pipe && path == PATH_PIPE && (!accumulate || mode != MODE_FP8_BLOCK));
+  return path == PATH_STREAM || (or_pipe && path == PATH_PIPE && (!accumulate || !mode_grouped_k(mode)));
 }
 
 size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K, bool accumulate) {
@@ -379,7 +385,7 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
     if ((r.path == PATH_STREAM || r.path == PATH_DECODE || p.K <= kAccShortK) && p.out_f32 &&
         stream_enabled() && stream_supported(mode, p.M, p.N, p.K, p.Kb, (sc & 15) == 0))
       r.path = PATH_STREAM;
-    else if (!(r.path == PATH_PIPE && p.out_f32 && mode != MODE_FP8_BLOCK))
+    else if (!(r.path == PATH_PIPE && p.out_f32 && !mode_grouped_k(mode)))
       r.path = PATH_TILED;
   }
   p.ksplit = 1;
@@ -400,6 +406,7 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
   switch (mode) {
     case MODE_FP8_TENSOR: launch_mode<MODE_FP8_TENSOR>(pl, p, st); break;
     case MODE_FP8_BLOCK: launch_mode<MODE_FP8_BLOCK>(pl, p, st); break;
+    case MODE_FP8_GCOL: launch_mode<MODE_FP8_GCOL>(pl, p, st); break;
     case MODE_MXFP4: launch_mode<MODE_MXFP4>(pl, p, st); break;
     case MODE_NVFP4: launch_mode<MODE_NVFP4>(pl, p, st); break;
     case MODE_BF16: launch_mode<MODE_BF16>(pl, p, st); break;

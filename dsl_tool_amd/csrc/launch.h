@@ -28,7 +28,15 @@ float *quant_scratch(hipError_t *err);
 size_t quant_scratch_bytes();
 
 // ---------------------------------------------------------------- GEMMs --
-enum GemmMode { MODE_FP8_TENSOR = 0, MODE_FP8_BLOCK = 1, MODE_MXFP4 = 2, MODE_NVFP4 = 3, MODE_BF16 = 4 };
+// FP8_BLOCK: 1x128 activation groups and 128x128 weight blocks; FP8_GCOL:
+// 1x128 activation groups and one weight scale per output column per
+// 128-K group (the reference's groupwise layout sb[K/128][N]).
+enum GemmMode {
+  MODE_FP8_TENSOR = 0, MODE_FP8_BLOCK = 1, MODE_MXFP4 = 2, MODE_NVFP4 = 3, MODE_BF16 = 4,
+  MODE_FP8_GCOL = 5
+};
+// Both FP8 modes whose scales change with every 128-K group.
+constexpr bool mode_grouped_k(int mode) { return mode == MODE_FP8_BLOCK || mode == MODE_FP8_GCOL; }
 
 // Compute units of the current device (cached per device; 256 if the query
 // fails).
@@ -41,8 +49,9 @@ struct GemmArgs {
   int M, N, K;           // K in elements
   int Kb;                // bytes per packed row (FP8: K, FP4: K/2, BF16: 2K)
   int64_t ldc;
-  const void *sa;        // FP8_BLOCK: float [M][nkg]; MX: uint8 [M][K/32]; NV: uint8 [M][K/16]
-  const void *sb;        // FP8_BLOCK: float [ceil(N/128)][nkg]; MX/NV as sa for N
+  const void *sa;        // FP8_BLOCK / GCOL: float [M][nkg]; MX: uint8 [M][K/32]; NV: uint8 [M][K/16]
+  const void *sb;        // FP8_BLOCK: float [ceil(N/128)][nkg]; FP8_GCOL: float [nkg][N];
+                         // MX/NV as sa for N
   const float *ga;       // FP8_TENSOR: scale_a; NV: global_a
   const float *gb;       // FP8_TENSOR: scale_b; NV: global_b
   float *ws;             // split-K fp32 [M][N] accumulation buffer (zeroed by the launcher)
@@ -81,13 +90,15 @@ hipError_t launch_gemm_persist(int mode, const GemmArgs &p, hipStream_t st);
 // Skinny-M kernels, one launch, no workspace (Kb % 1024 == 0):
 //   M <= 32: FP8_TENSOR and BF16; FP8_BLOCK and MXFP4 with 16-byte aligned scales
 //            and K % 512 == 0;
-//   M <= 4:  NVFP4 GEMV with 4-byte aligned scales and M * Kb/1024 <= 8.
+//   M <= 4:  NVFP4 GEMV with 16-byte aligned scales and M * Kb/1024 <= 8.
 bool decode_supported(int mode, int M, int K, int Kb, bool scales4, bool scales16);
 hipError_t launch_gemm_decode(int mode, const GemmArgs &p, hipStream_t st);
 
-// Streaming kernel for M <= 256 (gemm_stream.hip), one launch, no
-// workspace, deterministic: FP8_TENSOR and BF16; FP8_BLOCK and MXFP4 with
-// 16-byte aligned scales and K % 512 == 0; Kb % 256 (M <= 32) or % 512.
+// Streaming kernel for M <= 1024 (gemm_stream.hip), one launch, no
+// workspace, deterministic, Kb % 256 == 0: FP8_TENSOR and BF16; FP8_BLOCK,
+// FP8_GCOL and MXFP4 with 16-byte aligned scales and K % 512 == 0; NVFP4
+// with 16-byte aligned scales and K % 256 == 0.  The router takes it while
+// ceil(M/64) * N stays below a per-mode edge (gemm_tiled.hip, route_for).
 bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16);
 hipError_t launch_gemm_stream(int mode, const GemmArgs &p, hipStream_t st);
 
@@ -114,7 +125,9 @@ struct GroupedArgs {
   const float *sw;       // [G][N]
   int out_f32;
   // gather form: x is [xrows][K] and sorted row r reads x row arow[r]
-  // (persistent kernel only)
+  // (persistent kernel, and the grouped streaming tiles; launch_grouped_fp8
+  // sends groups of fewer than 48 rows on average to the streaming tiles
+  // when K % 256 == 0, the rest to the persistent kernel)
   const int32_t *arow = nullptr;
   int xrows = 0;
 };
@@ -164,12 +177,10 @@ hipError_t launch_moe_combine(const uint16_t *y, int rows_y, int64_t ldy, int n,
                               int out_f32, hipStream_t st);
 
 // -------------------------------------------------------------- LoRA --
-// t32 [M][LR] fp32 (tt: its transpose [LR][M]) -> t2 [M][ld2] bf16:
-// cols [0, LR) hi = bf16(t * s), [LR, 2 LR) lo = bf16(t * s - hi), the rest
-// 0; s = scales[col / rank].
-// t32 [M][LR] -> t2 [M][ld2]: hi | lo of T*s, zero padded.
 // LoRA with few tokens: T = s * X A^T and Y += T B^T on the vector ALUs in
-// fp32 (lora.hip); L*R up to kLoraValuMaxLR.
+// fp32 (lora.hip); L*R up to kLoraValuMaxLR.  launch_lora_split: t32
+// [M][LR] fp32 -> t2 [M][ld2] bf16 with cols [0, LR) hi = bf16(t * s),
+// [LR, 2 LR) lo = bf16(t * s - hi), the rest 0; s = scales[col / rank].
 constexpr int kLoraValuMaxLR = 512;
 bool lora_valu_supported(int64_t M, int64_t K, int64_t LR);
 hipError_t launch_lora_t(const uint16_t *x, const uint16_t *a_t, int M, int K, int LR, int rank,

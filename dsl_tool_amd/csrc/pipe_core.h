@@ -93,7 +93,8 @@ struct PipeCfg {
   static constexpr bool NV = MODE == MODE_NVFP4;
   static constexpr bool FP4 = MX || NV;
   static constexpr bool BF16 = MODE == MODE_BF16;           // 64-byte k-step = 32 bf16 of K
-  static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;     // one 128-K scale group per stage
+  static constexpr bool BLOCK = mode_grouped_k(MODE);       // one 128-K scale group per stage
+  static constexpr bool GCOL = MODE == MODE_FP8_GCOL;       // ... with a weight scale per column
   static constexpr int CH = SKB / 16, RPI = 1024 / SKB;     // chunks per row, rows per DMA
   // MFMA steps per stage: 32x32x64 for FP8 / MXFP4; for NVFP4 a "step" is a
   // quad of four 32x32x16 fp16 MFMAs over 64 elements (32 bytes)
@@ -103,7 +104,8 @@ struct PipeCfg {
   // scales in a separate ring, SA_RING below, instead)
   static constexpr int SCW = MX ? SKB / 64 : (NV ? SKB / 32 : ((BLOCK && !PF) ? 1 : 0));
   static constexpr int A_BYTES = BM * SKB, B_BYTES = BN * SKB;
-  static constexpr int SA_BYTES = BM * 4 * SCW, SB_BYTES = FP4 ? BN * 4 * SCW : 0;
+  // GCOL: the stage's weight scales sb[grp][n0 .. n0 + BN) ride along too
+  static constexpr int SA_BYTES = BM * 4 * SCW, SB_BYTES = (FP4 || GCOL) ? BN * 4 * SCW : 0;
   static constexpr int STAGE = A_BYTES + B_BYTES + SA_BYTES + SB_BYTES;
   // block-scaled prefetch kernel: two slots of 4 groups x BM rows of fp32
   // activation scales, [slot][row][4 groups], plus a 1 KB dummy target
@@ -127,6 +129,7 @@ struct PipeCfg {
   static_assert(NS >= 2 && (NS - 1) * D < 64, "ring depth / vmcnt range");
   static_assert(!PF || !NV, "the prefetch schedule covers FP8 and MXFP4");
   static_assert(!BLOCK || SKB == 128 || PF, "64-byte block-scaled stages use the prefetch schedule");
+  static_assert(!GCOL || !PF, "per-column weight scales use the per-stage partial kernel");
 };
 
 namespace pipe {
@@ -180,7 +183,16 @@ struct Ring {
         const int lim = isA ? p.M - 1 : p.N - 1;
         int grow = (isA ? m0 : n0) + lrow;
         grow = grow > lim ? lim : grow;
-        if constexpr (Cfg::BLOCK) {        // fp32 sa[row][K/128]: one float per row per group
+        if constexpr (Cfg::GCOL) {
+          if (isA) {                       // fp32 sa[row][K/128]: one float per row per group
+            src[j] = reinterpret_cast<const uint8_t *>(static_cast<const float *>(p.sa) +
+                                                       (int64_t)grow * (p.K / 128));
+            step[j] = 4;
+          } else {                         // fp32 sb[K/128][N]: the tile's columns of a group
+            src[j] = reinterpret_cast<const uint8_t *>(static_cast<const float *>(p.sb) + grow);
+            step[j] = 4 * p.N;
+          }
+        } else if constexpr (Cfg::BLOCK) { // fp32 sa[row][K/128]: one float per row per group
           src[j] = reinterpret_cast<const uint8_t *>(static_cast<const float *>(p.sa) +
                                                      (int64_t)grow * (p.K / 128));
           step[j] = 4;

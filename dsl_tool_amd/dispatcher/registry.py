@@ -160,9 +160,12 @@ def gemm_input_schema(kernel_name: str) -> dict:
         s = {"A": "Tensor[M, K] bf16", "B": "Tensor[K, N] bf16 (W.t() of a K-major W[N, K] is read in place)",
              "out_dtype": "torch.float32 (default) | torch.bfloat16"}
     elif kernel_name.endswith("fp8_gemm"):
-        s.update({"scale_a": "float | Tensor[M, ceil(K/128)] fp32",
-                  "scale_b": "float | Tensor[ceil(N/128), ceil(K/128)] fp32",
-                  "granularity": "str 'tensor' | 'block' (bf16 inputs)",
+        s.update({"scale_a": "float | Tensor[M, ceil(K/128)] fp32 | Tensor[M, ceil(K/G)] fp32 (groupwise)",
+                  "scale_b": "float | Tensor[ceil(N/128), ceil(K/128)] fp32 (128x128 blocks) "
+                             "| Tensor[ceil(K/G), N] fp32 (groupwise, per output column)",
+                  "granularity": "str 'tensor' | 'block' | 'group' (bf16 inputs; "
+                                 "pre-quantized: inferred from scale_b's shape)",
+                  "group_size": "int G, a multiple of 128 (default 128; 'group' only)",
                   "out_dtype": "torch.bfloat16 (default) | torch.float32"})
     elif kernel_name.endswith("fp4_gemm"):
         s.update({"fmt": "str 'mxfp4' (default) | 'nvfp4'",

@@ -107,15 +107,40 @@ def _gemm_ws(op: int, m: int, n: int, k: int, device) -> torch.Tensor | None:
 
 # ----------------------------------------------------------- packed level --
 
-def fp8_gemm_packed(qa, qw, scale_a, scale_b, *, block: bool = False,
+def _expand_groups(s: torch.Tensor, group_size: int, K: int, dim: int) -> torch.Tensor:
+    """Scales of G-element K groups as scales of 128-element groups: the
+    128-group j lies inside G-group j // (G/128), so repeating each scale
+    G/128 times gives the same sum, sum_g (sum_{k in g} a*b) * sa * sb
+    (cuda/gemm/fp8_gemm.cu:84-97), split into 128-element partials."""
+    if group_size == 128:
+        return s
+    r = group_size // 128
+    return s.repeat_interleave(r, dim=dim).narrow(dim, 0, -(-K // 128)).contiguous()
+
+
+def _check_group_size(group_size) -> int:
+    if isinstance(group_size, bool) or not isinstance(group_size, numbers.Integral) \
+            or group_size < 128 or group_size % 128 != 0:
+        raise ValueError(f"group_size must be a positive multiple of 128 (got {group_size!r}): "
+                         "the FP8 MFMA sums 128 K per instruction, so scale groups are whole "
+                         "multiples of 128")
+    return int(group_size)
+
+
+def fp8_gemm_packed(qa, qw, scale_a, scale_b, *, block: bool = False, group: bool = False,
                     out_dtype=torch.bfloat16, out=None):
     """GEMM on packed E4M3 codes.
 
     qa [M, K] and qw [N, K] are contiguous uint8 (or float8_e4m3fn) codes.
-    Per-tensor (block=False): scale_a / scale_b are 1-element float32 device
+    Per-tensor (default): scale_a / scale_b are 1-element float32 device
     tensors.  Block-scaled (block=True): scale_a [M, ceil(K/128)] and
-    scale_b [ceil(N/128), ceil(K/128)] float32.
+    scale_b [ceil(N/128), ceil(K/128)] float32.  Groupwise (group=True, the
+    reference's fp8_gemm_groupwise layout with G = 128,
+    cuda/gemm/fp8_gemm.cu:67-75): scale_a [M, ceil(K/128)] and scale_b
+    [ceil(K/128), N], one weight scale per output column per group.
     """
+    if block and group:
+        raise ValueError("block and group scales are exclusive")
     dev = _require_gpu(qa, qw, scale_a, scale_b)
     qa, qw = _u8(qa).contiguous(), _u8(qw).contiguous()
     M, K = qa.shape
@@ -124,17 +149,20 @@ def fp8_gemm_packed(qa, qw, scale_a, scale_b, *, block: bool = False,
         raise ValueError(f"K mismatch: A has {K}, W has {K2}")
     scale_a = scale_a.contiguous().float()
     scale_b = scale_b.contiguous().float()
+    nkg = -(-K // 128)
     if block:
-        nkg = -(-K // 128)
         if tuple(scale_a.shape) != (M, nkg) or tuple(scale_b.shape) != (-(-Nn // 128), nkg):
             raise ValueError("block scales must be [M, ceil(K/128)] and [ceil(N/128), ceil(K/128)]")
+    if group:
+        if tuple(scale_a.shape) != (M, nkg) or tuple(scale_b.shape) != (nkg, Nn):
+            raise ValueError("groupwise scales must be [M, ceil(K/128)] and [ceil(K/128), N]")
+    mode = N.SCALE_BLOCK128 if block else (N.SCALE_GROUP128 if group else N.SCALE_TENSOR)
     c = out if out is not None else torch.empty((M, Nn), dtype=_as_dtype(out_dtype), device=dev)
     ws = _gemm_ws(N.OP_FP8, M, Nn, K, dev)
     with torch.cuda.device(dev):
         N.call("dsl_fp8_gemm", N.ptr(qa), N.ptr(qw), N.ptr(c), M, Nn, K, c.stride(0),
-               _out_code(c.dtype), N.SCALE_BLOCK128 if block else N.SCALE_TENSOR,
-               N.ptr(scale_a), N.ptr(scale_b), N.ptr(ws), 0 if ws is None else ws.numel() * 4,
-               N.stream_of(dev))
+               _out_code(c.dtype), mode, N.ptr(scale_a), N.ptr(scale_b), N.ptr(ws),
+               0 if ws is None else ws.numel() * 4, N.stream_of(dev))
     return c
 
 
@@ -269,16 +297,24 @@ def lora_fused_gemm(X: torch.Tensor, W: torch.Tensor, loraA: torch.Tensor, loraB
 
 
 def fp8_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=1.0, scale_b=1.0, *,
-             granularity: str = "tensor", out_dtype: torch.dtype = torch.bfloat16):
+             granularity: str | None = None, group_size: int = 128,
+             out_dtype: torch.dtype = torch.bfloat16):
     """FP8 E4M3 GEMM ``C = (A @ B) * scale_a * scale_b`` (bf16 by default).
 
-    * A [M, K], B [K, N] in bf16/fp16/fp32: both are quantized on the GPU
-      (granularity "tensor": amax/448 per tensor; "block": 1x128 activation
-      groups and 128x128 weight blocks); scale_a / scale_b stay extra
-      multipliers, as in the reference.
-    * A, B in float8_e4m3fn: scale_a / scale_b are the dequantization scales,
-      either numbers (per-tensor) or tensors [M, ceil(K/128)] and
-      [ceil(N/128), ceil(K/128)] (block-scaled).
+    * A [M, K], B [K, N] in bf16/fp16/fp32: both are quantized on the GPU.
+      granularity "tensor" (default): amax/448 per tensor; "block": 1x128
+      activation groups and 128x128 weight blocks; "group": the reference's
+      groupwise form (cuda/gemm/fp8_gemm.cu:67-99), 1 x group_size groups
+      along K for A and, for B, one scale per output column per group.
+      scale_a / scale_b stay extra multipliers, as in the reference.
+    * A, B in float8_e4m3fn: scale_a / scale_b are the dequantization scales:
+      numbers (per-tensor); tensors [M, ceil(K/128)] and
+      [ceil(N/128), ceil(K/128)] (block-scaled); or the reference's groupwise
+      layout, scale_a [M, ceil(K/G)] and scale_b [ceil(K/G), N] with G =
+      group_size.  2-D scales are told apart by scale_b's shape, or named
+      by granularity="block" / "group".
+    group_size must be a multiple of 128 (the FP8 MFMA sums 128 K at a time;
+    a larger G is the same sum with its scale repeated over G/128 groups).
     ``out_dtype=torch.float32`` reproduces the reference's fp32 output.
     """
     if A.dim() != 2 or B.dim() != 2:
@@ -287,34 +323,64 @@ def fp8_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=1.0, scale_b=1.0, *,
     K2, Nn = B.shape
     if K != K2:
         raise ValueError(f"K mismatch: A is [{M}, {K}], B is [{K2}, {Nn}]")
+    if granularity not in (None, "tensor", "block", "group"):
+        raise ValueError(f"granularity must be 'tensor', 'block' or 'group', got {granularity!r}")
+    G = _check_group_size(group_size)
+    if granularity == "block" and G != 128:
+        raise ValueError("block scales are 128 x 128; group_size applies to granularity='group'")
     dev = _require_gpu(A, B)
     if A.dtype in _HIGH and B.dtype in _HIGH:
-        if granularity == "tensor":
+        gran = granularity or "tensor"
+        if gran == "tensor":
             qa, sa = Q.quant_fp8_tensor(A)
             qw, sw = Q.quant_fp8_tensor(B.t())
-            block = False
-        elif granularity == "block":
+        elif gran == "block":
             qa, sa = Q.quant_fp8_blocks(A, 1, 128)
             qw, sw = Q.quant_fp8_blocks(B.t(), 128, 128)
-            block = True
         else:
-            raise ValueError(f"granularity must be 'tensor' or 'block', got {granularity!r}")
+            qa, sa = Q.quant_fp8_blocks(A, 1, G)
+            qw, sw_rows = Q.quant_fp8_blocks(B.t(), 1, G)      # [N, ceil(K/G)]
+            sa = _expand_groups(sa, G, K, 1)
+            sw = _expand_groups(sw_rows.t(), G, K, 0)           # [ceil(K/128), N]
         if not (isinstance(scale_a, numbers.Number) and isinstance(scale_b, numbers.Number)):
             raise ValueError("with high-precision inputs scale_a/scale_b must be numbers")
         if scale_a != 1.0:
             sa = sa * float(scale_a)
         if scale_b != 1.0:
             sw = sw * float(scale_b)
-        return fp8_gemm_packed(qa, qw, sa, sw, block=block, out_dtype=out_dtype)
+        return fp8_gemm_packed(qa, qw, sa, sw, block=gran == "block", group=gran == "group",
+                               out_dtype=out_dtype)
     if A.dtype == _FP8 and B.dtype == _FP8:
         qw = _k_major(B)
         if isinstance(scale_a, torch.Tensor) and scale_a.dim() == 2:
             if not (isinstance(scale_b, torch.Tensor) and scale_b.dim() == 2):
-                raise ValueError("block-scaled fp8 needs 2-D scale_a and scale_b")
-            return fp8_gemm_packed(A, qw, scale_a.to(dev), scale_b.to(dev), block=True,
+                raise ValueError("block-scaled / groupwise fp8 needs 2-D scale_a and scale_b")
+            if granularity == "tensor":
+                raise ValueError("granularity='tensor' needs scalar scales")
+            nkg, nkG = -(-K // 128), -(-K // G)
+            gran = granularity
+            if gran is None:
+                if G == 128 and tuple(scale_b.shape) == (-(-Nn // 128), nkg):
+                    gran = "block"
+                elif tuple(scale_b.shape) == (nkG, Nn):
+                    gran = "group"
+                else:
+                    raise ValueError(
+                        f"scale_b {tuple(scale_b.shape)} is neither a 128x128 block layout "
+                        f"[{-(-Nn // 128)}, {nkg}] nor the groupwise layout [{nkG}, {Nn}]")
+            sa, sb = scale_a.to(dev), scale_b.to(dev)
+            if gran == "group":
+                if tuple(sa.shape) != (M, nkG) or tuple(sb.shape) != (nkG, Nn):
+                    raise ValueError(f"groupwise scales must be [M, ceil(K/G)] = [{M}, {nkG}] "
+                                     f"and [ceil(K/G), N] = [{nkG}, {Nn}]")
+                sa = _expand_groups(sa.float(), G, K, 1)
+                sb = _expand_groups(sb.float(), G, K, 0)
+            return fp8_gemm_packed(A, qw, sa, sb, block=gran == "block", group=gran == "group",
                                    out_dtype=out_dtype)
+        if granularity in ("block", "group"):
+            raise ValueError(f"granularity={granularity!r} needs 2-D scale tensors")
         return fp8_gemm_packed(A, qw, _dev_scalar(scale_a, dev), _dev_scalar(scale_b, dev),
-                               block=False, out_dtype=out_dtype)
+                               out_dtype=out_dtype)
     raise TypeError(f"fp8_gemm: unsupported dtypes {A.dtype}, {B.dtype}")
 
 

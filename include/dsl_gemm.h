@@ -39,7 +39,7 @@ enum {
 };
 
 enum { DSL_OUT_BF16 = 0, DSL_OUT_F32 = 1 };
-enum { DSL_SCALE_TENSOR = 0, DSL_SCALE_BLOCK128 = 1 };
+enum { DSL_SCALE_TENSOR = 0, DSL_SCALE_BLOCK128 = 1, DSL_SCALE_GROUP128 = 2 };
 enum { DSL_FMT_MXFP4 = 0, DSL_FMT_NVFP4 = 1 };
 enum { DSL_OP_FP8 = 0, DSL_OP_FP4 = 1, DSL_OP_GROUPED_FP8 = 2, DSL_OP_BF16 = 3 };
 enum { DSL_QFMT_FP8_G128 = 0, DSL_QFMT_MXFP4 = 1 };
@@ -126,6 +126,14 @@ size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols);
  *                       scale_b [ceil(N/128)][ceil(K/128)] (128x128 blocks);
  *                       C = sum_g (sum_{k in g} a*w) * sa[m,g] * sb[n/128,g]
  *                       (cuda/gemm/fp8_gemm.cu:84-97).
+ *   DSL_SCALE_GROUP128: the reference groupwise layout with G = 128:
+ *                       scale_a [M][ceil(K/128)], scale_b [ceil(K/128)][N]
+ *                       (one weight scale per output column per group,
+ *                       cuda/gemm/fp8_gemm.cu:67-75);
+ *                       C = sum_g (sum_{k in g} a*w) * sa[m,g] * sb[g,n]
+ *                       (cuda/gemm/fp8_gemm.cu:84-97).  A group size G that
+ *                       is a multiple of 128 is the same sum with each scale
+ *                       repeated over G/128 groups of 128.
  * K % 16 == 0.  Replaces fp8_gemm (triton/gemm/gemm_kernels.py:104-122),
  * fp8_gemm_per_tensor (cuda/gemm/fp8_gemm.cu:102-108) and
  * fp8_gemm_groupwise (cuda/gemm/fp8_gemm.cu:110-116). */

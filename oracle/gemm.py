@@ -79,6 +79,19 @@ def ref_fp8_groupwise(qa, sa, qw, sw, f64=False):
                             dequant_fp8_blocks(qw, sw, 128, 128), f64)
 
 
+def ref_fp8_groupwise_cols(qa, sa, qw, sb, group_size=128, f64=False):
+    """The reference's own groupwise layout (cuda/gemm/fp8_gemm.cu:67-99):
+    sa [M, ceil(K/G)] per activation row and K group, sb [ceil(K/G), N] per
+    K group and output column (qw is W [N, K], so column n is row n of qw);
+    C[m, n] = sum_g (sum_{k in g} a*w) * sa[m, g] * sb[g, n], the last group
+    partial when G does not divide K (:84-86).  Computed as dequantize ->
+    matmul: A with 1 x G groups, W with its column scales as 1 x G groups of
+    its rows."""
+    sb = np.asarray(sb, F32)
+    return ref_gemm_dequant(dequant_fp8_blocks(qa, sa, 1, group_size),
+                            dequant_fp8_blocks(qw, sb.T, 1, group_size), f64)
+
+
 def ref_mxfp4(pa, ea, pw, ew, f64=False):
     return ref_gemm_dequant(dequant_mxfp4(pa, ea), dequant_mxfp4(pw, ew), f64)
 

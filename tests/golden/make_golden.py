@@ -191,6 +191,23 @@ def main():
                fp8b_qa=np.array(qa, np.uint8), fp8b_sa=np.array(sa, np.float32),
                fp8b_qw=np.array(qw, np.uint8), fp8b_sw=np.array(sw, np.float32),
                fp8b_c=np.array(matmul64(ad, wd)))
+    # FP8 groupwise in the reference's own layout (cuda/gemm/fp8_gemm.cu:67-99):
+    # sa [M][ceil(K/G)], sb [ceil(K/G)][N] (one scale per output column and
+    # K group), G = 128 and 256, K = 320 so the last group is partial (:84-86);
+    # C by the group-partial triple loop of that kernel, in float64
+    a, w = seeded_bf16((3, 320), 23, outliers=4), seeded_bf16((5, 320), 24, 0.02)
+    for G in (128, 256):
+        qa, sa = q_fp8_blocks(to_list(a), 1, G)
+        qw, swr = q_fp8_blocks(to_list(w), 1, G)          # [N][ceil(K/G)] per weight row
+        ng = len(sa[0])
+        sb = [[swr[n][g] for n in range(5)] for g in range(ng)]   # [ceil(K/G)][N]
+        c = [[math.fsum(math.fsum(e4m3_value(qa[m][k]) * e4m3_value(qw[n][k])
+                                  for k in range(g * G, min(g * G + G, 320))) * sa[m][g] * sb[g][n]
+                        for g in range(ng)) for n in range(5)] for m in range(3)]
+        kat.update({f"fp8g{G}_qa": np.array(qa, np.uint8), f"fp8g{G}_sa": np.array(sa, np.float32),
+                    f"fp8g{G}_qw": np.array(qw, np.uint8), f"fp8g{G}_sb": np.array(sb, np.float32),
+                    f"fp8g{G}_c": np.array(c)})
+    kat.update(fp8g_a=a.view(torch.int16).numpy(), fp8g_w=w.view(torch.int16).numpy())
     # MXFP4, M=2 N=3 K=64, rows spanning a wide dynamic range
     a = (seeded_bf16((2, 64), 31).float() * torch.tensor([[2.0 ** -20], [2.0 ** 30]])).bfloat16()
     w = seeded_bf16((3, 64), 32, 0.02)

@@ -54,6 +54,17 @@ def test_fp8_gemm_argument_validation(lib):
     assert rc == N.DSL_ERR_ARG and "aligned" in _err(lib)
     # empty problem is a no-op success
     assert lib.dsl_fp8_gemm(None, None, None, 0, 16, 16, 16, 0, 0, fake, fake, None, 0, None) == 0
+    # groupwise (per-column weight scales): 4-byte aligned scale arrays
+    rc = lib.dsl_fp8_gemm(fake, fake, fake, 16, 16, 16, 16, 0, N.SCALE_GROUP128, fake + 2, fake,
+                          None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "4-byte aligned" in _err(lib)
+    # a register-staged shape (K % 128 != 0, few tiles) asks for a split-K
+    # workspace, which covers the groupwise mode too; without one it is refused
+    need = lib.dsl_gemm_workspace_bytes(N.OP_FP8, 70, 300, 1040)
+    assert need >= 70 * 300 * 4
+    rc = lib.dsl_fp8_gemm(fake, fake, fake, 70, 300, 1040, 300, 0, N.SCALE_GROUP128, fake, fake,
+                          None, 0, None)
+    assert rc == N.DSL_ERR_WORKSPACE
 
 
 def test_bf16_gemm_argument_validation(lib):

@@ -195,6 +195,53 @@ def test_ref_fp8_groupwise_kat(kat):
     assert g < 4e-3 and e < 8e-3          # bf16 rounding of the output only
 
 
+@pytest.mark.parametrize("G", [128, 256])
+def test_fp8_groupwise_cols_kat(kat, G):
+    """The reference's own groupwise layout (cuda/gemm/fp8_gemm.cu:67-99),
+    K = 320 so the last group is partial: the 1 x G quantizer gives the
+    fixture's codes and scales (the weight's per-row scales are sb
+    transposed), and the dequantize -> matmul oracle equals the float64
+    group-partial triple loop of that kernel."""
+    a, w = bf16_from_bits(kat["fp8g_a"]), bf16_from_bits(kat["fp8g_w"])
+    qa, sa = OQ.quant_fp8_blockwise(a, 1, G)
+    qw, sw = OQ.quant_fp8_blockwise(w, 1, G)
+    assert np.array_equal(qa, kat[f"fp8g{G}_qa"]) and np.array_equal(sa, kat[f"fp8g{G}_sa"])
+    assert np.array_equal(qw, kat[f"fp8g{G}_qw"]) and np.array_equal(sw.T, kat[f"fp8g{G}_sb"])
+    c = OG.ref_fp8_groupwise_cols(kat[f"fp8g{G}_qa"], kat[f"fp8g{G}_sa"], kat[f"fp8g{G}_qw"],
+                                  kat[f"fp8g{G}_sb"], G, f64=True)
+    assert np.array_equal(c, F.round_to_bf16(kat[f"fp8g{G}_c"].astype(np.float32)))
+
+
+def test_fp8_groupwise_cols_kat_discriminates_slips(kat):
+    """Plausible slips in the groupwise oracle fail the fixture: the column
+    scales read as 128-column blocks (the block layout), scales transposed
+    onto the wrong axis, the partial last group dropped, and G = 256 scales
+    applied per 128."""
+    qa, sa, qw, sb = (kat[f"fp8g256_{k}"] for k in ("qa", "sa", "qw", "sb"))
+    want = kat["fp8g256_c"]
+
+    def far(c):
+        return OG.rel_errors(c, want)[0] > 1e-2
+
+    da = OG.dequant_fp8_blocks(qa, sa, 1, 256)
+    # one weight scale per 128-column block (column 0's), not per column
+    blockish = OG.dequant_fp8_blocks(qw, np.repeat(sb.T[:1], qw.shape[0], axis=0), 1, 256)
+    assert far(OG.ref_gemm_dequant(da, blockish, True))
+    # sb indexed [n][g] read as [g][n] (same values, wrong axis): swap via reshape
+    swapped = np.ascontiguousarray(sb).reshape(sb.shape[1], sb.shape[0])
+    assert far(OG.ref_gemm_dequant(da, OG.dequant_fp8_blocks(qw, swapped, 1, 256), True))
+    # partial last group (k = 256..319) dropped
+    qa0 = qa.copy()
+    qa0[:, 256:] = 0
+    assert far(OG.ref_fp8_groupwise_cols(qa0, sa, qw, sb, 256, f64=True))
+    # G = 256 scales expanded to 128-element groups: repeated twice each (what
+    # the GPU path does) passes, read once per 128 (the last padded) fails
+    sa2, sb2 = np.repeat(sa, 2, axis=1)[:, :3], np.repeat(sb, 2, axis=0)[:3]
+    assert not far(OG.ref_fp8_groupwise_cols(qa, sa2, qw, sb2, 128, f64=True))
+    sa1, sb1 = np.pad(sa, ((0, 0), (0, 1)), mode="edge"), np.pad(sb, ((0, 1), (0, 0)), mode="edge")
+    assert far(OG.ref_fp8_groupwise_cols(qa, sa1, qw, sb1, 128, f64=True))
+
+
 def test_ref_mxfp4_kat(kat):
     c = OG.ref_mxfp4(kat["mx_qa"], kat["mx_ea"], kat["mx_qw"], kat["mx_ew"], f64=True)
     want = kat["mx_c"]
