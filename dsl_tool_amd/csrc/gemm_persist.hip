@@ -306,6 +306,14 @@ struct Ring {
 // With that order lane half h takes all its scales from word h of the
 // row's two pair words, byte 2p + kk: the MFMA's op_sel selects it, so the
 // word goes to the MFMA as read, once per pair.
+//
+// Scale words are read two 32-row tiles at a time: lane half h reads the
+// whole 16-byte quad entry of its row in tile t + h (64 lanes, 64
+// consecutive entries, 1 KB contiguous: no bank conflicts), and one
+// v_permlane32_swap of the pair's two words leaves tile t's word in one
+// register and tile t+1's in the other, for both lane halves.  Reading one
+// 4-byte word per lane from 32 rows 16 bytes apart instead puts 4 lanes on
+// each bank (8 rows per 128 bytes) for the tile's word alone.
 template <class Cfg, int KIND = Cfg::MX ? 1 : (Cfg::NV ? 2 : 0)>
 struct Frag {
   v8i a[Cfg::TM], b[Cfg::TN];
@@ -335,12 +343,26 @@ struct Frag<Cfg, 1> {
   }
   // sq: quad slot; qw: first scale word of the pair in the row's 16 bytes
   // (2 x quad-local pair index).  The scale word is read with half 0.
+  static_assert(Cfg::TM % 2 == 0 && Cfg::TN == 2, "scale words are read two tiles at a time");
+  // words qw, qw + 1 (the pair's h = 0 / h = 1 words) of the quad entries of
+  // tiles t (first) and t + 1 (second) of a 64-row span starting at row0,
+  // for the calling lane's half
+  static DSL_DEV void scale_pair(const uint8_t *sqrows, int row0, int qw, int r32, int h, int &first,
+                                 int &second) {
+    const v4i e = *reinterpret_cast<const v4i *>(sqrows + (row0 + h * 32 + r32) * 16);
+    const int x = qw ? e[2] : e[0], y = qw ? e[3] : e[1];
+    const auto s = __builtin_amdgcn_permlane32_swap((unsigned)x, (unsigned)y, false, false);
+    first = (int)s[0];
+    second = (int)s[1];
+  }
+  // The pair's scale words of tiles i-1 and i are read with odd i (half 0
+  // only), after the MFMAs of both rows are issued.
   DSL_DEV void load_a(const uint8_t *slot, const uint8_t *sq, int qw, int p, int i, int wm,
                       int r32, int h) {
     const int row = wm * Cfg::WM + i * 32 + r32;
     a[i][0] = ld(slot, row, 4 * h + 2 * p);
     a[i][1] = ld(slot, row, 4 * h + 2 * p + 1);
-    if (p == 0) as[i] = *reinterpret_cast<const int *>(sq + row * 16 + (qw + h) * 4);
+    if (p == 0 && (i & 1)) scale_pair(sq, wm * Cfg::WM + (i - 1) * 32, qw, r32, h, as[i - 1], as[i]);
   }
   DSL_DEV void load_b(const uint8_t *slot, const uint8_t *sq, int qw, int p, int wn, int r32,
                       int h) {
@@ -349,8 +371,8 @@ struct Frag<Cfg, 1> {
       const int row = wn * Cfg::WN + j * 32 + r32;
       b[j][0] = ld(slot + Cfg::A_BYTES, row, 4 * h + 2 * p);
       b[j][1] = ld(slot + Cfg::A_BYTES, row, 4 * h + 2 * p + 1);
-      if (p == 0) bs[j] = *reinterpret_cast<const int *>(sq + Cfg::SQA + row * 16 + (qw + h) * 4);
     }
+    if (p == 0) scale_pair(sq + Cfg::SQA, wn * Cfg::WN, qw, r32, h, bs[0], bs[1]);
   }
   // half 1 of a pair uses the scale words read with its half 0
   DSL_DEV void share_scales(const Frag &half0) {
