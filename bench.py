@@ -99,10 +99,14 @@ def build_cases(names, dev):
         nb = L.dsl_gemm_workspace_bytes(op, m, n, k)
         return torch.empty(max(nb, 16) // 4, dtype=torch.float32, device=dev), nb
 
-    def fp8_case(name, m, n, k, block, a_bf16=None, w_bf16=None):
+    def fp8_case(name, m, n, k, block, a_bf16=None, w_bf16=None, group=False):
         a = a_bf16.to(dev) if a_bf16 is not None else rnd((m, k), 1)
         w = w_bf16.to(dev) if w_bf16 is not None else rnd((n, k), 2, 0.02)
-        if block:
+        if group:      # the reference groupwise layout: sb [K/128][N] per output column
+            qa, sa = Q.quant_fp8_blocks(a, 1, 128)
+            qw, swr = Q.quant_fp8_blocks(w, 1, 128)
+            sw = swr.t().contiguous()
+        elif block:
             qa, sa = Q.quant_fp8_blocks(a, 1, 128)
             qw, sw = Q.quant_fp8_blocks(w, 128, 128)
         else:
@@ -114,7 +118,7 @@ def build_cases(names, dev):
         qws = [qw] + [qw.clone() for _ in range(rot - 1)]
         c = torch.empty((m, n), dtype=torch.bfloat16, device=dev)
         ws, nb = ws_for(N.OP_FP8, m, n, k)
-        mode = N.SCALE_BLOCK128 if block else N.SCALE_TENSOR
+        mode = N.SCALE_GROUP128 if group else (N.SCALE_BLOCK128 if block else N.SCALE_TENSOR)
 
         def launch(i, stream):
             return L.dsl_fp8_gemm(qa.data_ptr(), qws[i % rot].data_ptr(), c.data_ptr(), m, n, k,
@@ -122,8 +126,10 @@ def build_cases(names, dev):
                                   ws.data_ptr(), nb, stream)
         nbytes = qa.numel() + wbytes + sa.numel() * 4 + 2 * m * n
         bound = "hbm" if 2 * m * n * k / nbytes < PEAK_FP8_TFLOPS * 1e12 / (PEAK_HBM_GBS * 1e9) else "mfma"
+        kind = ("1x128 / per-column 128x1 groupwise (scale_b [K/128][N])" if group
+                else ("1x128/128x128 block" if block else "per-tensor"))
         return Case(name, 2.0 * m * n * k, nbytes, PEAK_FP8_TFLOPS, bound, launch, rot,
-                    f"fp8 {'1x128/128x128 block' if block else 'per-tensor'} M={m} N={n} K={k}")
+                    f"fp8 {kind} M={m} N={n} K={k}")
 
     def fp4_case(name, m, n, k, fmt):
         a, w = rnd((m, k), 3), rnd((n, k), 4, 0.02)
@@ -201,9 +207,13 @@ def build_cases(names, dev):
                     + (f" ({tokens} tokens x top-8, decode)" if tokens < 1024 else "")
                     + f" N={Nn} K={K} ({E - nonempty} empty), {rot} weight copies rotated")
 
-    def quant_case(name, kind, r, k):
-        """One quantize/pack pass over a bf16 [r, k] operand resident in HBM."""
+    def quant_case(name, kind, r, k, f32=False):
+        """One quantize/pack pass over a bf16 (or fp32, the reference's own
+        input type) [r, k] operand resident in HBM."""
         x = rnd((r, k), 5, 0.02)
+        if f32:
+            x = x.float()
+        xin, esz = (N.IN_F32, 4) if f32 else (N.IN_BF16, 2)
         ws = torch.empty(L.dsl_quant_workspace_bytes(r, k) // 4, dtype=torch.float32, device=dev)
         if kind == "fp8_block128":
             q = torch.empty((r, k), dtype=torch.uint8, device=dev)
@@ -211,7 +221,7 @@ def build_cases(names, dev):
             out_b, passes = r * k + sc.numel() * 4, 1
 
             def launch(i, stream):
-                return L.dsl_quant_fp8_blocks(x.data_ptr(), r, k, k, 1, 0, 128, 128, q.data_ptr(),
+                return L.dsl_quant_fp8_blocks(x.data_ptr(), r, k, k, 1, xin, 128, 128, q.data_ptr(),
                                               sc.data_ptr(), stream)
         elif kind == "fp8_row128":
             q = torch.empty((r, k), dtype=torch.uint8, device=dev)
@@ -219,7 +229,7 @@ def build_cases(names, dev):
             out_b, passes = r * k + sc.numel() * 4, 1
 
             def launch(i, stream):
-                return L.dsl_quant_fp8_blocks(x.data_ptr(), r, k, k, 1, 0, 1, 128, q.data_ptr(),
+                return L.dsl_quant_fp8_blocks(x.data_ptr(), r, k, k, 1, xin, 1, 128, q.data_ptr(),
                                               sc.data_ptr(), stream)
         elif kind == "fp8_tensor":
             q = torch.empty((r, k), dtype=torch.uint8, device=dev)
@@ -227,7 +237,7 @@ def build_cases(names, dev):
             out_b, passes = r * k + 4, 2
 
             def launch(i, stream):
-                return L.dsl_quant_fp8_tensor(x.data_ptr(), r, k, k, 1, 0, q.data_ptr(), sc.data_ptr(),
+                return L.dsl_quant_fp8_tensor(x.data_ptr(), r, k, k, 1, xin, q.data_ptr(), sc.data_ptr(),
                                               ws.data_ptr(), ws.numel() * 4, stream)
         elif kind == "mxfp4":
             q = torch.empty((r, k // 2), dtype=torch.uint8, device=dev)
@@ -235,7 +245,7 @@ def build_cases(names, dev):
             out_b, passes = r * k // 2 + r * k // 32, 1
 
             def launch(i, stream):
-                return L.dsl_quant_mxfp4(x.data_ptr(), r, k, k, 1, 0, q.data_ptr(), sc.data_ptr(),
+                return L.dsl_quant_mxfp4(x.data_ptr(), r, k, k, 1, xin, q.data_ptr(), sc.data_ptr(),
                                          stream)
         else:
             q = torch.empty((r, k // 2), dtype=torch.uint8, device=dev)
@@ -244,11 +254,12 @@ def build_cases(names, dev):
             out_b, passes = r * k // 2 + r * k // 16 + 4, 2
 
             def launch(i, stream):
-                return L.dsl_quant_nvfp4(x.data_ptr(), r, k, k, 1, 0, q.data_ptr(), sc.data_ptr(),
+                return L.dsl_quant_nvfp4(x.data_ptr(), r, k, k, 1, xin, q.data_ptr(), sc.data_ptr(),
                                          g.data_ptr(), ws.data_ptr(), ws.numel() * 4, stream)
-        nbytes = passes * 2 * r * k + out_b
+        nbytes = passes * esz * r * k + out_b
         return Case(name, 0.0, nbytes, PEAK_FP8_TFLOPS, "hbm", launch, 1,
-                    f"quantize {kind} [{r}, {k}] bf16 ({passes} read pass{'es' if passes > 1 else ''})")
+                    f"quantize {kind} [{r}, {k}] {'fp32' if f32 else 'bf16'} "
+                    f"({passes} read pass{'es' if passes > 1 else ''})")
 
     def lora_case(name, m, n, k, r, l):
         x, w = rnd((m, k), 11), rnd((n, k), 12, 0.05)
@@ -417,6 +428,10 @@ def build_cases(names, dev):
                                             W.activations(2, 4096, 4096, outliers=True),
                                             W.weights(2, 7168, 4096)),
         "fp8_block_m16": lambda: fp8_case("fp8_block_m16", 16, 7168, 4096, True),
+        "fp8_group_m4096": lambda: fp8_case("fp8_group_m4096", 4096, 7168, 4096, False,
+                                            W.activations(2, 4096, 4096, outliers=True),
+                                            W.weights(2, 7168, 4096), group=True),
+        "fp8_group_m16": lambda: fp8_case("fp8_group_m16", 16, 7168, 4096, False, group=True),
         "fp8_tensor_m4096": lambda: fp8_case("fp8_tensor_m4096", 4096, 7168, 4096, False),
         "fp8_tensor_cfg1": lambda: fp8_case("fp8_tensor_cfg1", 128, 4096, 4096, False),
         "fp8_tensor_8192": lambda: fp8_case("fp8_tensor_8192", 8192, 8192, 8192, False),
@@ -452,13 +467,20 @@ def build_cases(names, dev):
         "quant_fp8_tensor_w": lambda: quant_case("quant_fp8_tensor_w", "fp8_tensor", 4096, 4096),
         "quant_mxfp4_w": lambda: quant_case("quant_mxfp4_w", "mxfp4", 8192, 8192),
         "quant_nvfp4_w": lambda: quant_case("quant_nvfp4_w", "nvfp4", 14336, 4096),
+        "quant_fp8_row128_a_f32": lambda: quant_case("quant_fp8_row128_a_f32", "fp8_row128", 4096,
+                                                     4096, f32=True),
+        "quant_fp8_tensor_w_f32": lambda: quant_case("quant_fp8_tensor_w_f32", "fp8_tensor", 4096,
+                                                     4096, f32=True),
+        "quant_mxfp4_w_f32": lambda: quant_case("quant_mxfp4_w_f32", "mxfp4", 8192, 8192, f32=True),
+        "quant_nvfp4_w_f32": lambda: quant_case("quant_nvfp4_w_f32", "nvfp4", 8192, 8192, f32=True),
     }
     for nm in names:
         cases[nm] = builders[nm]()
     return cases
 
 
-ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor_cfg1",
+ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_group_m4096", "fp8_group_m16",
+             "fp8_tensor_m4096", "fp8_tensor_cfg1",
              "fp8_tensor_8192",
              "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe", "grouped_moe_decode",
              "bf16_8192", "bf16_m4096", "bf16_m16",
@@ -466,7 +488,8 @@ ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_tensor_m4096", "fp8_tensor
              "moe_route", "moe_permute_quant", "moe_quant_tokens", "moe_combine", "moe_grouped_permuted",
              "moe_grouped_gather", "moe_layer_cfg5", "moe_layer_decode", "moe_layer_decode_permuted", "lora_m4096", "bf16_4096",
              "quant_fp8_block128_w", "quant_fp8_row128_a", "quant_fp8_tensor_w", "quant_mxfp4_w",
-             "quant_nvfp4_w"]
+             "quant_nvfp4_w", "quant_fp8_row128_a_f32", "quant_fp8_tensor_w_f32", "quant_mxfp4_w_f32",
+             "quant_nvfp4_w_f32"]
 
 
 def time_case(case, steps, warmup, dev, graph):

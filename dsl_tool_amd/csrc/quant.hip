@@ -1,9 +1,11 @@
 // Quantize/pack kernels: bf16 or fp32 -> E4M3 (per-tensor, block-scaled),
 // MXFP4 (E2M1 + E8M0 / 32), NVFP4 (E2M1 + E4M3 / 16 + fp32 global).
 //
-// All kernels read x[r*sr + c*sc] (bf16; fp32 sources take the strided
-// kernels, which divide with the IEEE division) and write K-major codes q[r*C + c]
-// (FP8) or packed nibbles q[r*C/2 + c/2] (FP4).  Code paths, fastest first:
+// All kernels read x[r*sr + c*sc] (bf16 or fp32) and write K-major codes
+// q[r*C + c] (FP8) or packed nibbles q[r*C/2 + c/2] (FP4).  fp32 sources
+// divide with the IEEE division: contiguous rows on the fp32 team kernel
+// (quant_f32_rowgroup_kernel), anything else on the strided kernels.  bf16
+// code paths, fastest first:
 //   * packed path (sc == 1, sr == C, C % 8 == 0, 16-B aligned x, fewer than
 //     2^31 chunks; row groups also need C % group == 0): the input is one run
 //     of 16-byte chunks and group g is chunks [g*CG, (g+1)*CG), so indices
@@ -55,7 +57,16 @@ __global__ __launch_bounds__(256) void amax_packed_kernel(
   if (threadIdx.x == 0) partial[blockIdx.x] = m;
 }
 
-// T = uint16_t (bf16 bits) or float; VEC (16-byte rows of bf16) only for bf16.
+// 8 consecutive source elements as fp32: one 16-byte load of bf16, or two of fp32.
+DSL_DEV void load8(const uint16_t *p, float *f) { unpack8(*reinterpret_cast<const uint4 *>(p), f); }
+DSL_DEV void load8(const float *p, float *f) {
+  const float4 a = reinterpret_cast<const float4 *>(p)[0], b = reinterpret_cast<const float4 *>(p)[1];
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
+// T = uint16_t (bf16 bits) or float; VEC: rows of whole 8-element chunks,
+// 16-byte aligned.
 template <bool VEC, typename T>
 __global__ __launch_bounds__(256) void amax_partial_kernel(
     const T *__restrict__ x, int64_t rows, int64_t cols, int64_t sr, int64_t sc,
@@ -68,7 +79,7 @@ __global__ __launch_bounds__(256) void amax_partial_kernel(
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
       const int64_t r = i / cpr, c8 = i - r * cpr;
       float f[8];
-      unpack8(*reinterpret_cast<const uint4 *>(x + r * sr + c8 * 8), f);
+      load8(x + r * sr + c8 * 8, f);
       m = fmaxf(m, amax8(f));
     }
   } else {
@@ -252,6 +263,98 @@ __global__ __launch_bounds__(256) void quant_rowgroup_kernel(
       if (lane == 0) reinterpret_cast<uint8_t *>(scales)[g] = (uint8_t)sb;
       const uint32_t p = d != 0.f ? e2m1_quot8(f, d, rcp_approx(d)) : 0u;
       if (ok) *reinterpret_cast<uint32_t *>(q + ((r * cols + c) >> 1)) = p;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 rows (unit column stride, 16-byte aligned rows, C % 8 == 0): a team
+// of T lanes (T | 64) owns one group of G = 8*T*U elements of a row, lane k
+// holding the runs of 8 consecutive elements k, k + T, ... (two 16-byte
+// loads each), so each load instruction of a wave reads whole contiguous
+// runs.  KIND_TENSOR: every group uses the per-tensor scale of the partials.
+// The scales and codes are those of the strided kernel below: IEEE
+// quotients (__fdiv_rn; the reciprocal quotient is only shown exact for
+// bf16 sources) encoded by the hardware converters, which return
+// e4m3_encode / e2m1_encode of every finite fp32 input.
+// ---------------------------------------------------------------------------
+DSL_DEV uint2 e4m3_div8(const float *f, float s) {
+  uint32_t lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__fdiv_rn(f[0], s), __fdiv_rn(f[1], s), 0, false);
+  lo = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__fdiv_rn(f[2], s), __fdiv_rn(f[3], s), (int)lo, true);
+  uint32_t hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__fdiv_rn(f[4], s), __fdiv_rn(f[5], s), 0, false);
+  hi = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(__fdiv_rn(f[6], s), __fdiv_rn(f[7], s), (int)hi, true);
+  return make_uint2(lo, hi);
+}
+
+DSL_DEV uint32_t e2m1_div8(const float *f, float d) {
+  uint32_t c = e2m1_pk_into<0>(0u, __fdiv_rn(f[0], d), __fdiv_rn(f[1], d));
+  c = e2m1_pk_into<1>(c, __fdiv_rn(f[2], d), __fdiv_rn(f[3], d));
+  c = e2m1_pk_into<2>(c, __fdiv_rn(f[4], d), __fdiv_rn(f[5], d));
+  return e2m1_pk_into<3>(c, __fdiv_rn(f[6], d), __fdiv_rn(f[7], d));
+}
+
+template <int KIND, int T, int U>
+__global__ __launch_bounds__(256) void quant_f32_rowgroup_kernel(
+    const float *__restrict__ x, int64_t rows, int64_t cols, int64_t sr,
+    uint8_t *__restrict__ q, void *__restrict__ scales,
+    const float *__restrict__ partial, int nparts, float *__restrict__ scale_out) {
+  constexpr int G = 8 * T * U;                  // elements per group
+  static_assert(64 % T == 0, "teams within a wave");
+  __shared__ float sh[4];
+  float st = 1.f;                               // per-tensor scale / NVFP4 global scale
+  if constexpr (KIND == KIND_TENSOR || KIND == KIND_NV) {
+    const float am = reduce_partials(partial, nparts, sh);
+    st = KIND == KIND_TENSOR ? fp8_scale_ieee(am) : nv_global_ieee(am);
+    if (blockIdx.x == 0 && threadIdx.x == 0) *scale_out = st;
+  }
+  const int64_t gpr = (cols + G - 1) / G;       // groups per row
+  const int64_t ngroups = rows * gpr;
+  const int lane = threadIdx.x % T;
+  const int64_t team0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) / T;
+  const int64_t nteams = (int64_t)gridDim.x * blockDim.x / T;
+  for (int64_t g = team0; g < ngroups; g += nteams) {   // uniform across a team
+    const int64_t r = g / gpr, gi = g - r * gpr;
+    float f[U][8];
+    float m = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = gi * G + (int64_t)(u * T + lane) * 8;
+      if (c < cols) {
+        load8(x + r * sr + c, f[u]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) f[u][j] = 0.f;
+      }
+      m = fmaxf(m, amax8(f[u]));
+    }
+    if constexpr (KIND != KIND_TENSOR) {
+#pragma unroll
+      for (int o = 1; o < T; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+    }
+    float s = st, d = 0.f, mul = 1.f;
+    if constexpr (KIND == KIND_FP8) {
+      s = fp8_scale_ieee(m);
+      if (lane == 0) reinterpret_cast<float *>(scales)[g] = s;
+    } else if constexpr (KIND == KIND_MX) {
+      const int e = mx_exponent(m);
+      mul = pow2_neg(e);
+      if (lane == 0) reinterpret_cast<uint8_t *>(scales)[g] = (uint8_t)(e + 127);
+    } else if constexpr (KIND == KIND_NV) {
+      const uint8_t sb = e4m3_encode(__fdiv_rn(__fdiv_rn(m, 6.0f), st));
+      d = e4m3_decode(sb) * st;
+      if (lane == 0) reinterpret_cast<uint8_t *>(scales)[g] = sb;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = gi * G + (int64_t)(u * T + lane) * 8;
+      if (c >= cols) continue;
+      if constexpr (KIND == KIND_FP8 || KIND == KIND_TENSOR) {
+        *reinterpret_cast<uint2 *>(q + r * cols + c) = e4m3_div8(f[u], s);
+      } else if constexpr (KIND == KIND_MX) {
+        *reinterpret_cast<uint32_t *>(q + ((r * cols + c) >> 1)) = e2m1_mul8(f[u], mul);
+      } else {
+        *reinterpret_cast<uint32_t *>(q + ((r * cols + c) >> 1)) = d != 0.f ? e2m1_div8(f[u], d) : 0u;
+      }
     }
   }
 }
@@ -510,6 +613,22 @@ static int grid_for(int64_t work, int per_block) {
   return (int)g;
 }
 
+// fp32 rows the vector fp32 kernels take: unit column stride, whole 8-element
+// runs, 16-byte aligned rows.
+static bool f32_vec_ok(const void *x, int64_t cols, int64_t sr, int64_t sc) {
+  return sc == 1 && (cols % 8) == 0 && (sr % 4) == 0 &&
+         (reinterpret_cast<uintptr_t>(x) % 16) == 0;
+}
+
+template <int KIND, int T, int U>
+static void launch_f32_rows(const float *x, int64_t rows, int64_t cols, int64_t sr, uint8_t *q,
+                            void *scales, const float *partial, int np, float *sout, hipStream_t st) {
+  constexpr int G = 8 * T * U;
+  const int64_t threads = rows * ((cols + G - 1) / G) * T;
+  quant_f32_rowgroup_kernel<KIND, T, U><<<grid_for(threads, 256 * 2), 256, 0, st>>>(
+      x, rows, cols, sr, q, scales, partial, np, sout);
+}
+
 template <int KIND, int CG, int TL, int V>
 static void launch_packed(const uint16_t *x, int64_t rows, int64_t cols, uint8_t *q, void *scales,
                           const float *partial, int np, float *sout, hipStream_t st) {
@@ -532,8 +651,12 @@ static hipError_t launch_amax_partials(const void *xv, bool f32, int64_t rows, i
                                        hipStream_t st) {
   if (f32) {
     *nparts = partial_blocks(rows * cols);
-    amax_partial_kernel<false, float><<<*nparts, 256, 0, st>>>(static_cast<const float *>(xv), rows,
-                                                                 cols, sr, sc, partial);
+    if (f32_vec_ok(xv, cols, sr, sc))
+      amax_partial_kernel<true, float><<<*nparts, 256, 0, st>>>(static_cast<const float *>(xv), rows,
+                                                                  cols, sr, sc, partial);
+    else
+      amax_partial_kernel<false, float><<<*nparts, 256, 0, st>>>(static_cast<const float *>(xv), rows,
+                                                                   cols, sr, sc, partial);
     return hipGetLastError();
   }
   const uint16_t *x = static_cast<const uint16_t *>(xv);
@@ -597,8 +720,12 @@ hipError_t launch_quant_fp8_tensor(const void *xv, bool f32, int64_t rows, int64
   hipError_t e = launch_amax_partials(xv, f32, rows, cols, sr, sc, partial, &np, st);
   if (e != hipSuccess) return e;
   if (f32) {
-    quant_fp8_tensor_kernel<false, float><<<grid_for(rows * cols, 256 * 16), 256, 0, st>>>(
-        static_cast<const float *>(xv), rows, cols, sr, sc, partial, np, q, scale);
+    if (f32_vec_ok(xv, cols, sr, sc))
+      launch_f32_rows<KIND_TENSOR, 1, 1>(static_cast<const float *>(xv), rows, cols, sr, q, nullptr,
+                                         partial, np, scale, st);
+    else
+      quant_fp8_tensor_kernel<false, float><<<grid_for(rows * cols, 256 * 16), 256, 0, st>>>(
+          static_cast<const float *>(xv), rows, cols, sr, sc, partial, np, q, scale);
     return hipGetLastError();
   }
   const uint16_t *x = static_cast<const uint16_t *>(xv);
@@ -627,6 +754,16 @@ hipError_t launch_quant_fp8_blocks(const void *xv, bool f32, int64_t rows, int64
   const int64_t tiles = ((rows + gr - 1) / gr) * ((cols + gc - 1) / gc);
   if (f32) {
     const float *xf = static_cast<const float *>(xv);
+    if (gr == 1 && f32_vec_ok(xv, cols, sr, sc) &&
+        (gc == 32 || gc == 64 || gc == 128 || gc == 256)) {
+      switch (gc) {
+        case 32: launch_f32_rows<KIND_FP8, 4, 1>(xf, rows, cols, sr, q, scales, nullptr, 0, nullptr, st); break;
+        case 64: launch_f32_rows<KIND_FP8, 8, 1>(xf, rows, cols, sr, q, scales, nullptr, 0, nullptr, st); break;
+        case 128: launch_f32_rows<KIND_FP8, 16, 1>(xf, rows, cols, sr, q, scales, nullptr, 0, nullptr, st); break;
+        default: launch_f32_rows<KIND_FP8, 16, 2>(xf, rows, cols, sr, q, scales, nullptr, 0, nullptr, st); break;
+      }
+      return hipGetLastError();
+    }
     if (gr == 1 && gc <= 256)
       quant_group_scalar_kernel<KIND_FP8, float><<<grid_for(tiles, 256), 256, 0, st>>>(
           xf, rows, cols, sr, sc, gc, q, scales, nullptr, 0, nullptr);
@@ -694,8 +831,12 @@ hipError_t launch_quant_fp8_blocks(const void *xv, bool f32, int64_t rows, int64
 hipError_t launch_quant_mxfp4(const void *xv, bool f32, int64_t rows, int64_t cols, int64_t sr,
                               int64_t sc, uint8_t *q, uint8_t *e8m0, hipStream_t st) {
   if (f32) {
-    quant_group_scalar_kernel<KIND_MX, float><<<grid_for(rows * (cols / 32), 256), 256, 0, st>>>(
-        static_cast<const float *>(xv), rows, cols, sr, sc, 32, q, e8m0, nullptr, 0, nullptr);
+    if (f32_vec_ok(xv, cols, sr, sc))
+      launch_f32_rows<KIND_MX, 4, 1>(static_cast<const float *>(xv), rows, cols, sr, q, e8m0,
+                                     nullptr, 0, nullptr, st);
+    else
+      quant_group_scalar_kernel<KIND_MX, float><<<grid_for(rows * (cols / 32), 256), 256, 0, st>>>(
+          static_cast<const float *>(xv), rows, cols, sr, sc, 32, q, e8m0, nullptr, 0, nullptr);
     return hipGetLastError();
   }
   const uint16_t *x = static_cast<const uint16_t *>(xv);
@@ -718,8 +859,12 @@ hipError_t launch_quant_nvfp4(const void *xv, bool f32, int64_t rows, int64_t co
   hipError_t e = launch_amax_partials(xv, f32, rows, cols, sr, sc, partial, &np, st);
   if (e != hipSuccess) return e;
   if (f32) {
-    quant_group_scalar_kernel<KIND_NV, float><<<grid_for(rows * (cols / 16), 256), 256, 0, st>>>(
-        static_cast<const float *>(xv), rows, cols, sr, sc, 16, q, e4m3s, partial, np, gscale);
+    if (f32_vec_ok(xv, cols, sr, sc))
+      launch_f32_rows<KIND_NV, 2, 1>(static_cast<const float *>(xv), rows, cols, sr, q, e4m3s,
+                                     partial, np, gscale, st);
+    else
+      quant_group_scalar_kernel<KIND_NV, float><<<grid_for(rows * (cols / 16), 256), 256, 0, st>>>(
+          static_cast<const float *>(xv), rows, cols, sr, sc, 16, q, e4m3s, partial, np, gscale);
     return hipGetLastError();
   }
   const uint16_t *x = static_cast<const uint16_t *>(xv);

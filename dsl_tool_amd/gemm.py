@@ -34,6 +34,9 @@ there is no CPU or eager fallback.
 from __future__ import annotations
 
 import numbers
+import threading
+import weakref
+from collections import OrderedDict
 
 import torch
 
@@ -94,6 +97,50 @@ def _k_major(b_kn: torch.Tensor) -> torch.Tensor:
     """[K, N] operand -> contiguous [N, K] (free when B is W.t())."""
     w = b_kn.t()
     return w if w.is_contiguous() else w.contiguous()
+
+
+# K-major copies of weight operands passed in the reference's [.., K, N]
+# layout, kept per source tensor (see _k_major_weight).
+_WEIGHT_CACHE: "OrderedDict[tuple, tuple]" = OrderedDict()
+_WEIGHT_CACHE_SLOTS = 4
+_weight_lock = threading.Lock()
+
+
+def clear_weight_cache() -> None:
+    """Drop the K-major weight copies _k_major_weight keeps."""
+    with _weight_lock:
+        _WEIGHT_CACHE.clear()
+
+
+def _k_major_weight(b: torch.Tensor) -> torch.Tensor:
+    """A weight operand whose last two dims are [K, N] (the reference's
+    layout, triton/gemm/gemm_kernels.py:104-108, :164-169) as contiguous
+    [.., N, K].  Free when b is the transpose view of K-major storage
+    (W.t(), W.transpose(1, 2)).  Otherwise the transposed copy is made once
+    and kept while the source tensor is alive and unmodified -- keyed by its
+    address and view geometry, checked against a weak reference to its
+    storage's tensor and its version counter (which in-place writes bump) --
+    so a weight held in the [K, N] layout is not transposed again on every
+    call.  At most _WEIGHT_CACHE_SLOTS copies are kept (least recently used
+    dropped first); clear_weight_cache() drops them."""
+    w = b.transpose(-1, -2)
+    if w.is_contiguous():
+        return w
+    base = b._base if b._base is not None else b
+    key = (b.data_ptr(), tuple(b.shape), tuple(b.stride()), b.dtype, str(b.device))
+    ver = b._version
+    with _weight_lock:
+        hit = _WEIGHT_CACHE.get(key)
+        if hit is not None and hit[0]() is base and hit[1] == ver:
+            _WEIGHT_CACHE.move_to_end(key)
+            return hit[2]
+    packed = w.contiguous()
+    with _weight_lock:
+        _WEIGHT_CACHE[key] = (weakref.ref(base), ver, packed)
+        _WEIGHT_CACHE.move_to_end(key)
+        while len(_WEIGHT_CACHE) > _WEIGHT_CACHE_SLOTS:
+            _WEIGHT_CACHE.popitem(last=False)
+    return packed
 
 
 def _u8(t: torch.Tensor) -> torch.Tensor:
@@ -248,7 +295,7 @@ def bf16_gemm(A: torch.Tensor, B: torch.Tensor, *, out_dtype: torch.dtype = torc
         raise ValueError(f"K mismatch: A is [{M}, {K}], B is [{K2}, {Nn}]")
     dev = _require_gpu(A, B)
     a = A if A.is_contiguous() else A.contiguous()
-    w = _k_major(B)
+    w = _k_major_weight(B)
     c = out if out is not None else torch.empty((M, Nn), dtype=_as_dtype(out_dtype), device=dev)
     ws = _gemm_ws(N.OP_BF16, M, Nn, K, dev)
     with torch.cuda.device(dev):
@@ -351,7 +398,7 @@ def fp8_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=1.0, scale_b=1.0, *,
         return fp8_gemm_packed(qa, qw, sa, sw, block=gran == "block", group=gran == "group",
                                out_dtype=out_dtype)
     if A.dtype == _FP8 and B.dtype == _FP8:
-        qw = _k_major(B)
+        qw = _k_major_weight(B)
         if isinstance(scale_a, torch.Tensor) and scale_a.dim() == 2:
             if not (isinstance(scale_b, torch.Tensor) and scale_b.dim() == 2):
                 raise ValueError("block-scaled / groupwise fp8 needs 2-D scale_a and scale_b")
@@ -420,7 +467,7 @@ def fp4_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=None, scale_b=None, *,
     if A.dtype == torch.uint8 and B.dtype == torch.uint8:
         if not (isinstance(scale_a, torch.Tensor) and isinstance(scale_b, torch.Tensor)):
             raise ValueError("pre-packed fp4 inputs need scale_a and scale_b tensors")
-        return fp4_gemm_packed(A, scale_a, _k_major(B), scale_b, fmt=fmt, global_a=global_a,
+        return fp4_gemm_packed(A, scale_a, _k_major_weight(B), scale_b, fmt=fmt, global_a=global_a,
                                global_w=global_b, out_dtype=out_dtype)
     raise TypeError(f"fp4_gemm: unsupported dtypes {A.dtype}, {B.dtype}")
 
@@ -435,12 +482,17 @@ def grouped_gemm(A: torch.Tensor, B: torch.Tensor, num_groups, scale_a=None, sca
       groups, A [T, K] with rows sorted by group, B [G, K, N] -> C [T, N];
       empty groups are allowed.
     High-precision inputs are quantized to E4M3 with per-row activation and
-    per-channel weight scales.  float8_e4m3fn inputs need scale_a [T] and
-    scale_b [G, N].  The output dtype defaults to A.dtype (bf16 for fp8
-    and fp16 inputs).  scale_a / scale_b are positional after the third
-    argument, so a pre-quantized problem travels over ``run_from_spec`` as
-    five tensor specs [X, B, offsets, scale_a, scale_b]
-    (dispatcher.py:285-294).
+    per-channel weight scales, so bf16 inputs give an FP8 product, not the
+    reference's unquantized bf16 batched product (grouped_gemm_kernel,
+    triton/gemm/gemm_kernels.py:125-182): expect FP8 rounding (about 3% of
+    an entry's magnitude per product, ~1e-2 of max|C| over K), not bf16's.
+    float8_e4m3fn inputs need scale_a [T] and scale_b [G, N]; an fp8 B
+    [G, K, N] that is not the transpose view of K-major [G, N, K] storage is
+    transposed once and the copy kept (_k_major_weight).  The output dtype
+    defaults to A.dtype (bf16 for fp8 and fp16 inputs).  scale_a / scale_b
+    are positional after the third argument, so a pre-quantized problem
+    travels over ``run_from_spec`` as five tensor specs [X, B, offsets,
+    scale_a, scale_b] (dispatcher.py:285-294).
     """
     if isinstance(num_groups, torch.Tensor):
         offsets = num_groups
@@ -469,15 +521,17 @@ def grouped_gemm(A: torch.Tensor, B: torch.Tensor, num_groups, scale_a=None, sca
     if out_dtype is None:
         out_dtype = torch.float32 if A.dtype == torch.float32 else torch.bfloat16
     out_dtype = _as_dtype(out_dtype)
-    Wt = B.transpose(1, 2).reshape(G * Nn, K)          # W[g, n, k] rows
     if X.dtype in _HIGH and B.dtype in _HIGH:
+        # W[g, n, k] rows (a view when B is the transpose of K-major [G, N, K]
+        # storage, else a copy; the high-precision weight is quantized on
+        # every call anyway)
         qx, sx = Q.quant_fp8_blocks(X, 1, K)
-        qw, sw = Q.quant_fp8_blocks(Wt, 1, K)
+        qw, sw = Q.quant_fp8_blocks(B.transpose(1, 2).reshape(G * Nn, K), 1, K)
     elif X.dtype == _FP8 and B.dtype == _FP8:
         if scale_a is None or scale_b is None:
             raise ValueError("fp8 grouped_gemm needs scale_a [T] and scale_b [G, N]")
         qx, sx = X, scale_a.to(dev)
-        qw, sw = Wt, scale_b.to(dev)
+        qw, sw = _k_major_weight(B), scale_b.to(dev)    # [G, N, K]
     else:
         raise TypeError(f"grouped_gemm: unsupported dtypes {A.dtype}, {B.dtype}")
     y = grouped_fp8_gemm_packed(qx, sx, qw.reshape(G, Nn, K), sw.reshape(G, Nn), offsets,

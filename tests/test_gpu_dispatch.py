@@ -146,3 +146,28 @@ def test_rest_prequantized_grouped_fp8():
     ref = OG.ref_grouped_fp8(qx, sx[:, 0], qw.reshape(3, n, k), sw.reshape(3, n), off)
     glob, elem = OG.rel_errors(_out(r.json()), ref)
     assert glob <= 1e-2 and elem <= 1e-2, (glob, elem)
+
+
+def test_rest_prequantized_fp8_groupwise_reference_layout():
+    """E4M3 codes with the reference groupwise scales (scale_a [M, ceil(K/G)],
+    scale_b [ceil(K/G), N], cuda/gemm/fp8_gemm.cu:67-99) posted as four tensor
+    specs in the positional order A, B, scale_a, scale_b with group_size as a
+    scalar param; the layout is told from scale_b's shape."""
+    from fastapi.testclient import TestClient
+
+    from dsl_tool_amd.dispatcher.api import app
+    G = 256
+    a, w = _seeded((40, 640), 917).float().numpy(), _seeded((72, 640), 918, 0.02).float().numpy()
+    qa, sa = OQ.quant_fp8_blockwise(a, 1, G)
+    qw, swr = OQ.quant_fp8_blockwise(w, 1, G)
+    sb = np.ascontiguousarray(swr.T)                                   # [ceil(K/G), N]
+    req = {"kernel_name": "gemm.fp8_gemm", "backend": "hip",
+           "inputs": [_raw(qa, "float8_e4m3fn"), _raw(qw.T, "float8_e4m3fn"), _raw(sa, "float32"),
+                      _raw(sb, "float32")],
+           "params": {"group_size": G, "out_dtype": "float32"}}
+    with TestClient(app) as c:
+        r = c.post("/api/v1/kernels/run", json=req)
+    assert r.status_code == 200, r.text
+    ref = OG._mm(OG.dequant_fp8_blocks(qa, sa, 1, G), OG.dequant_fp8_blocks(qw, swr, 1, G))
+    glob, elem = OG.rel_errors(_out(r.json()), ref)
+    assert glob <= 1e-2 and elem <= 1e-2, (glob, elem)

@@ -91,6 +91,15 @@ def test_combine_matches_oracle(out_dtype):
 
 
 def test_routed_grouped_gemm_end_to_end():
+    """The routed chain stage by stage, each to its own bar: routing tables
+    and token codes bit-exact, the grouped GEMM's rows y against the grouped
+    oracle (max-relative and elementwise 1e-2), the combine of that y
+    bit-exact against the oracle combine of the same y, and the one-call
+    routed_grouped_gemm equal to the chain bit for bit; end to end against
+    the all-oracle chain the north-star max-relative bound (the combine sums
+    topk bf16-rounded GEMM rows, and one bf16 ulp of a large row lands whole
+    on a sum that cancels, so elementwise the end-to-end error is the
+    GEMM's, carried through the exact combine)."""
     T, k, E, K, Nn = 512, 4, 16, 1024, 768
     ids = _ids(T, k, E, 430)
     wts = torch.softmax(torch.randn((T, k), generator=torch.Generator().manual_seed(431)), 1)
@@ -104,12 +113,37 @@ def test_routed_grouped_gemm_end_to_end():
     from oracle import quant as OQ
     wt = w.float().numpy().transpose(0, 2, 1).reshape(E * Nn, K)
     qw, sw = OQ.quant_fp8_blockwise(wt, 1, K)
-    y = OG.ref_grouped_fp8(qx, sx, qw.reshape(E, Nn, K), sw.reshape(E, Nn), off)
-    ref = OM.combine(y, dest, wts.numpy(), T, k, out_bf16=False)
-    # The combine adds topk bf16-rounded GEMM rows; one bf16 ulp of a large
-    # term (a rounding flip from the GEMM's own fp32 order) lands whole on a
-    # sum that cancels, so only the global north-star bound is meaningful.
-    assert_close(out, ref, what="routed grouped gemm", elem_tol=float("inf"))
+    y_ref = OG.ref_grouped_fp8(qx, sx, qw.reshape(E, Nn, K), sw.reshape(E, Nn), off)
+    ref = OM.combine(y_ref, dest, wts.numpy(), T, k, out_bf16=False)
+    # the same chain on the GPU, stage by stage
+    from dsl_tool_amd import quant as Q
+    r = M.moe_route(ids.to(DEV), E)
+    assert np.array_equal(r.offsets.cpu().numpy(), off)
+    assert np.array_equal(r.dest.cpu().numpy(), dest)
+    qwd, swd = Q.quant_fp8_blocks(w.to(DEV).transpose(1, 2).reshape(E * Nn, K), 1, K)
+    assert np.array_equal(np_u8(qwd), qw) and np.array_equal(np_f32(swd), sw)
+    qt, sxt = M.moe_quant_tokens(x.to(DEV), r)
+    n = int(off[-1])
+    assert np.array_equal(np_u8(qt)[src[:n]], qx) and np.array_equal(np_f32(sxt)[:n], sx)
+    y = M.moe_grouped_fp8_gemm(qt, sxt, r, qwd.reshape(E, Nn, K), swd.reshape(E, Nn))
+    assert_close(y[:n], y_ref, what="routed grouped gemm: grouped rows")
+    comb = M.moe_combine(y, r, wts.to(DEV), out_dtype=torch.float32)
+    assert np.array_equal(np_f32(comb), OM.combine(np_f32(y), dest, wts.numpy(), T, k,
+                                                   out_bf16=False))
+    assert torch.equal(comb, out)
+    # end to end: the north-star max-relative bound, and per entry the error
+    # is the grouped rows' error carried through the (positive) combine
+    # weights, sum_j w_tj |y - y_ref|[dest], up to the combine's fp32 rounding
+    glob, _ = OG.rel_errors(np_f32(out), ref)
+    assert glob <= 1e-2, glob
+    yerr = np.zeros((T * k, Nn), np.float32)
+    yerr[:n] = np.abs(np_f32(y)[:n].astype(np.float64) - y_ref)
+    carried = OM.combine(yerr, dest, wts.numpy(), T, k, out_bf16=False).astype(np.float64)
+    # fp32 rounding of the two combines: a few ulps of sum_j w_tj |y_ref|
+    mag = OM.combine(np.abs(y_ref).astype(np.float32), dest, wts.numpy(), T, k,
+                     out_bf16=False).astype(np.float64)
+    err = np.abs(np_f32(out).astype(np.float64) - ref)
+    assert (err <= carried * (1 + 1e-5) + 1e-6 * mag + 1e-30).all()
 
 
 @pytest.mark.parametrize("T,k,E,K,pad", [(300, 4, 9, 2048, 0), (64, 2, 3, 136, 8), (1000, 8, 64, 2048, 0),

@@ -309,6 +309,46 @@ def test_fp8_blocks_fp32_source(gr, gc):
     assert np.array_equal(np_f32(s2), s_ref) and np.array_equal(np_u8(q2), q_ref)
 
 
+def _f32_rows_dev(x: np.ndarray, pad: int) -> torch.Tensor:
+    """x on the GPU as a view with row stride cols + pad."""
+    t = torch.from_numpy(np.ascontiguousarray(x)).to(DEV)
+    return torch.nn.functional.pad(t, (0, pad))[:, :x.shape[1]] if pad else t
+
+
+# fp32 rows with unit column stride take the vector fp32 kernels (a team of
+# lanes per group, IEEE quotients); other layouts the strided kernels
+@pytest.mark.parametrize("gc", [32, 64, 128, 256])
+@pytest.mark.parametrize("cols,pad", [(384, 0), (200, 0), (520, 12)])
+def test_fp8_row_groups_fp32_source(gc, cols, pad):
+    rng = np.random.default_rng(gc + cols)
+    x = (rng.standard_normal((97, cols)) * 3).astype(np.float32)
+    x[::5, ::3] *= np.float32(1.0009765)       # mantissa bits bf16 does not hold
+    x[7] = 0.0                                  # an all-zero row: the 1e-12 floor
+    q, s = Q.quant_fp8_blocks(_f32_rows_dev(x, pad), 1, gc)
+    q_ref, s_ref = OQ.quant_fp8_blockwise(x, 1, gc)
+    assert np.array_equal(np_f32(s), s_ref)
+    assert np.array_equal(np_u8(q), q_ref)
+
+
+@pytest.mark.parametrize("pad", [0, 4])
+def test_fp32_source_padded_rows_all_formats(pad):
+    rng = np.random.default_rng(pad + 3)
+    x = (rng.standard_normal((65, 256)) * 2).astype(np.float32)
+    x[3, :32] *= np.float32(1e-30)              # tiny block
+    x[9, 16:32] = 0.0                           # zero NVFP4 block
+    xd = _f32_rows_dev(x, pad)
+    q, sc = Q.quant_fp8_tensor(xd)
+    q_ref, s_ref = OQ.quant_fp8_per_tensor(x)
+    assert np_f32(sc)[0] == s_ref and np.array_equal(np_u8(q), q_ref)
+    q, e = Q.quant_mxfp4(xd)
+    q_ref, e_ref = OQ.quant_mxfp4(x)
+    assert np.array_equal(np_u8(e), e_ref) and np.array_equal(np_u8(q), q_ref)
+    q, sb, g = Q.quant_nvfp4(xd)
+    q_ref, sb_ref, g_ref = OQ.quant_nvfp4(x)
+    assert np_f32(g)[0] == g_ref
+    assert np.array_equal(np_u8(sb), sb_ref) and np.array_equal(np_u8(q), q_ref)
+
+
 def test_mxfp4_fp32_source_near_midpoints():
     # blocks of 32 whose amax 5.5 * 2^k fixes the shared exponent k, the other
     # 31 elements one ulp around the E2M1 midpoints of that exponent
