@@ -73,10 +73,14 @@ def _rotations(bytes_per_copy: int) -> int:
 
 
 class Case:
-    def __init__(self, name, flops, nbytes, peak_tflops, bound, launch, rot, note=""):
+    def __init__(self, name, flops, nbytes, peak_tflops, bound, launch, rot, note="",
+                 format_peak=None):
         self.name, self.flops, self.nbytes = name, flops, nbytes
         self.peak_tflops, self.bound, self.launch, self.rot = peak_tflops, bound, launch, rot
         self.note = note
+        # the peak of the data format itself where the kernel runs on a
+        # wider MFMA (NVFP4 dequantized to fp16): reported beside frac_mfma
+        self.format_peak = format_peak
 
 
 def build_cases(names, dev):
@@ -161,7 +165,10 @@ def build_cases(names, dev):
         ridge = peak * 1e12 / (PEAK_HBM_GBS * 1e9)
         bound = "hbm" if 2 * m * n * k / nbytes < ridge else "mfma"
         return Case(name, 2.0 * m * n * k, nbytes, peak, bound, launch, rot,
-                    f"{fmt} M={m} N={n} K={k}" + ("" if fmt == "mxfp4" else " (fp16 MFMA peak)"))
+                    f"{fmt} M={m} N={n} K={k}" + ("" if fmt == "mxfp4" else
+                                                   " (frac_mfma of the fp16 MFMA peak it runs on, "
+                                                   "frac_fp4 of the FP4 peak)"),
+                    format_peak=None if fmt == "mxfp4" else PEAK_FP4_TFLOPS)
 
     def bf16_case(name, m, n, k):
         a, w = rnd((m, k), 6), rnd((n, k), 7, 0.02)
@@ -293,7 +300,10 @@ def build_cases(names, dev):
         qw, sw = Q.quant_fp8_blocks(w, 1, K)
         del w
         decode = tokens < 1024
-        rot = _rotations(qw.numel()) if decode or stage.startswith("grouped") else 1
+        # every stage that runs the grouped GEMM reads its weights from
+        # copies rotated past the Infinity Cache (the layer as well as the
+        # grouped stage alone, so the two are timed on the same footing)
+        rot = _rotations(qw.numel()) if stage.startswith(("grouped", "layer")) else 1
         qws = [qw] + [qw.clone() for _ in range(rot - 1)]
         rows = T * k
         off = torch.empty(E + 1, dtype=torch.int32, device=dev)
@@ -375,9 +385,9 @@ def build_cases(names, dev):
                                 "to their 32768 routed rows",
                 "combine": "MoE weighted combine of 32768 rows, N=1536 -> 4096 tokens",
                 "layer": "MoE projection cfg5: route + per-token E4M3 + grouped FP8 GEMM reading A "
-                         "through the row map + combine",
+                         f"through the row map + combine, {rot} weight copies rotated",
                 "layer_permuted": "MoE projection cfg5 over the permuted copy: route + permute/quant + "
-                                  "grouped FP8 GEMM + combine",
+                                  f"grouped FP8 GEMM + combine, {rot} weight copies rotated",
                 "grouped": f"grouped FP8 GEMM of the routed rows (permuted copy), {rot} weight copies "
                            "rotated",
                 "grouped_gather": f"grouped FP8 GEMM of the routed rows, A read through the row map "
@@ -492,6 +502,16 @@ ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_group_m4096", "fp8_group_m
              "quant_nvfp4_w_f32"]
 
 
+def _host_ns():
+    """Host timestamps bracketing a timed region, in both clocks a kernel
+    trace may use (CLOCK_MONOTONIC and CLOCK_BOOTTIME)."""
+    return {"monotonic": time.clock_gettime_ns(time.CLOCK_MONOTONIC),
+            "boottime": time.clock_gettime_ns(time.CLOCK_BOOTTIME)}
+
+
+TRACE_WINDOWS: list = []       # (case, steps, start clocks, end clocks) of each timed region
+
+
 def time_case(case, steps, warmup, dev, graph):
     """Average step time (ms) over `steps` launches, HIP events on the launch stream."""
     import torch
@@ -536,18 +556,45 @@ def time_case(case, steps, warmup, dev, graph):
         torch.cuda.synchronize(dev)
         g.replay()                                    # warm replay
         torch.cuda.synchronize(dev)
+        t0 = _host_ns()
         with torch.cuda.stream(stream):
             start.record(stream)
             g.replay()
             end.record(stream)
     else:
+        torch.cuda.synchronize(dev)
+        t0 = _host_ns()
         with torch.cuda.stream(stream):
             start.record(stream)
             for i in range(steps):
                 run(i, sp)
             end.record(stream)
     torch.cuda.synchronize(dev)
+    TRACE_WINDOWS.append((case.name, steps, t0, _host_ns()))
     return start.elapsed_time(end) / steps
+
+
+TRACE_FILE = os.path.join(ROOT, "profiles", "bench_default_kernel_trace.txt")
+
+
+def read_trace_medians(path: str = TRACE_FILE) -> dict:
+    """case -> (kernel, median us) of the case's main kernel in the committed
+    kernel-trace summary (an earlier profiled run of this bench), or {}."""
+    import re
+    out, case = {}, None
+    try:
+        lines = open(path).read().splitlines()
+    except OSError:
+        return out
+    for line in lines:
+        m = re.match(r"case (\S+): ", line)
+        if m:
+            case = m.group(1)
+            continue
+        m = re.match(r"\s+(\S.*?)\s+n=\s*\d+ median\s+([\d.]+)", line)
+        if m and case and case not in out:          # kernels are listed by total time
+            out[case] = (m.group(1), float(m.group(2)))
+    return out
 
 
 def read_traffic(path: str = TRAFFIC_FILE):
@@ -733,30 +780,67 @@ def summarize_counters(dirs, commands) -> int:
     return 0
 
 
-def summarize_trace(trace_dir: str, bench_log: str, command: str) -> int:
+def summarize_trace(trace_dir: str, bench_log: str, windows: str, command: str) -> int:
     """Write profiles/bench_default_kernel_trace.txt from a rocprofv3
-    --kernel-trace --stats csv dir of a bench run and that run's stderr."""
+    --kernel-trace --stats csv dir of a bench run, that run's stderr and its
+    --trace-windows file: per case, the dispatches that ran inside the
+    case's timed region (host clock bounds; warm-up launches excluded), their
+    count and median duration per kernel, and for the headline the roofline
+    fraction recomputed from that median beside the one the bench line
+    reported from HIP events."""
     import csv
     import glob
     import re
+    import statistics
 
-    stats = glob.glob(os.path.join(trace_dir, "**", "*kernel_stats.csv"), recursive=True)
-    rows = list(csv.DictReader(open(stats[0])))
-    out = ["# rocprofv3 kernel-trace summary: default bench run (all cases)",
-           f"# command (run from the repository root on one MI355X): {command}",
-           "", "Per-kernel durations (microseconds, every launch of the run incl. warm-up):", "",
-           f"{'kernel':100s} {'calls':>6s} {'avg':>9s} {'min':>9s} {'max':>9s}"]
+    trace = glob.glob(os.path.join(trace_dir, "**", "*kernel_trace.csv"), recursive=True)
+    rows = list(csv.DictReader(open(trace[0])))
+    disp = []
     for r in rows:
-        n = r["Name"]
+        n = r.get("Kernel_Name") or r.get("Name") or ""
         if "dsl::" not in n:
             continue
-        n = re.sub(r"\(.*\)$", "", n.replace("void ", ""))[:100]
-        out.append(f"{n:100s} {int(r['Calls']):6d} {float(r['AverageNs']) / 1e3:9.2f} "
-                   f"{float(r['MinNs']) / 1e3:9.2f} {float(r['MaxNs']) / 1e3:9.2f}")
+        n = re.sub(r"\(.*\)$", "", n.replace("void ", ""))
+        disp.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), n))
+    wins = [json.loads(line) for line in open(windows) if line.strip()]
+    # the clock the trace uses: the one under which the most dispatches fall
+    # inside some window
+    def inside(clock):
+        return sum(1 for s0, e0, _ in disp
+                   for w in wins if w["t0"][clock] <= s0 and e0 <= w["t1"][clock])
+    clock = max(("monotonic", "boottime"), key=inside)
     text = open(bench_log).read()
-    cases = re.findall(r"\[bench\] case (\S+): \{'us': ([\d.]+), 'tflops': ([\d.]+).*?'what': '([^']*)'", text)
-    out += ["", "bench.py timings of every case in the same (profiled) run, microseconds:"]
-    out += [f"    {c[0]:26s} {float(c[1]):9.2f}   {c[3]}" for c in cases]
+    bench_us = {c[0]: float(c[1]) for c in
+                re.findall(r"\[bench\] case (\S+): \{'us': ([\d.]+)", text)}
+    whats = dict(re.findall(r"\[bench\] case (\S+): \{.*?'what': '([^']*)'", text))
+    out = ["# rocprofv3 kernel-trace summary: default bench run (all cases)",
+           f"# command (run from the repository root on one MI355X): {command}",
+           f"# dispatches inside each case's timed region ({clock} clock), warm-up excluded;",
+           "# median / mean kernel duration in microseconds; bench_us = the case's HIP-event",
+           "# time per step in the same run (kernel time plus any launch gaps)", ""]
+    head = None
+    for w in wins:
+        sel = [(e0 - s0) / 1e3 for s0, e0, _ in disp
+               if w["t0"][clock] <= s0 and e0 <= w["t1"][clock]]
+        per = {}
+        for s0, e0, n in disp:
+            if w["t0"][clock] <= s0 and e0 <= w["t1"][clock]:
+                per.setdefault(n, []).append((e0 - s0) / 1e3)
+        out.append(f"case {w['case']}: {w['steps']} timed steps, bench_us "
+                   f"{bench_us.get(w['case'], float('nan')):.2f}   ({whats.get(w['case'], '')})")
+        for n, d in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+            out.append(f"    {n[:110]:110s} n={len(d):4d} median {statistics.median(d):9.2f} "
+                       f"mean {statistics.fmean(d):9.2f}")
+        if w["case"] == HEADLINE and per:
+            main = max(per.items(), key=lambda kv: sum(kv[1]))
+            head = (main[0], statistics.median(main[1]), len(sel))
+    if head:
+        flops = 2.0 * 4096 * 7168 * 4096
+        frac_trace = flops / (head[1] * 1e-6) / 1e12 / PEAK_FP8_TFLOPS
+        frac_bench = flops / (bench_us[HEADLINE] * 1e-6) / 1e12 / PEAK_FP8_TFLOPS
+        out += ["", f"headline kernel {head[0]}: median {head[1]:.2f} us over its timed launches "
+                f"-> roofline frac {frac_trace:.4f}; the bench line's frac from HIP events "
+                f"{frac_bench:.4f} (ratio {frac_bench / frac_trace:.4f})"]
     with open(os.path.join(ROOT, "profiles", "bench_default_kernel_trace.txt"), "w") as f:
         f.write("\n".join(out) + "\n")
     log("wrote profiles/bench_default_kernel_trace.txt")
@@ -885,8 +969,11 @@ def main(argv=None):
                     help="write profiles/<case>_counters.txt from rocprofv3 --pmc output dirs")
     ap.add_argument("--commands", nargs="*", default=[],
                     help="with --summarize-counters: the commands to record in the summaries")
-    ap.add_argument("--summarize-trace", nargs=2, metavar=("TRACE_DIR", "BENCH_LOG"),
-                    help="write profiles/bench_default_kernel_trace.txt from a kernel-trace run")
+    ap.add_argument("--summarize-trace", nargs=3, metavar=("TRACE_DIR", "BENCH_LOG", "WINDOWS"),
+                    help="write profiles/bench_default_kernel_trace.txt from a kernel-trace run, "
+                         "its stderr and its --trace-windows file")
+    ap.add_argument("--trace-windows", metavar="FILE",
+                    help="write each case's timed region (host clock bounds) to FILE as JSON lines")
     args = ap.parse_args(argv)
     if args.summarize_counters:
         return summarize_counters(args.summarize_counters, args.commands)
@@ -917,6 +1004,7 @@ def main(argv=None):
     log(f"device {props.name} CUs={props.multi_processor_count} cases={names}")
 
     results = {}
+    traced = read_trace_medians()
     head_ms = None
     for nm in names:
         log(f"case {nm}: build")
@@ -930,6 +1018,12 @@ def main(argv=None):
                        "gbs": round(gbs, 1), "frac_hbm": round(gbs / PEAK_HBM_GBS, 4),
                        "bound": case.bound, "rot": case.rot, "timing": "graph" if graph else "eager",
                        "what": case.note}
+        if case.format_peak:
+            results[nm]["frac_fp4"] = round(tflops / case.format_peak, 4)
+        if nm in traced:
+            # the case's main kernel as the committed rocprofv3 summary
+            # timed it (median of its timed launches in that run)
+            results[nm]["rocprof_kernel_us"] = traced[nm][1]
         log(f"case {nm}: {results[nm]}")
         if nm == HEADLINE:
             head_ms, head = ms, case
@@ -961,6 +1055,10 @@ def main(argv=None):
         "cases": results,
     }
     print(json.dumps(line), flush=True)
+    if args.trace_windows:
+        with open(args.trace_windows, "w") as f:
+            for nm, steps, t0, t1 in TRACE_WINDOWS:
+                f.write(json.dumps({"case": nm, "steps": steps, "t0": t0, "t1": t1}) + "\n")
     return 0
 
 

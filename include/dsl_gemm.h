@@ -77,7 +77,10 @@ int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols,
  * that forbid hipMalloc).  Results are identical to dsl_quant_fp8_tensor.
  * Every call on one GPU uses that GPU's array, so calls that overlap on one
  * GPU (different streams, threads or graph replays in flight together) race
- * and must be serialized by the caller. */
+ * and must be serialized by the caller.  The array used is the current
+ * device's: the current device must be the device of `stream` and of the
+ * data.  The first call on a device looks up the array's address
+ * (hipGetSymbolAddress); that call may be made inside HIP graph capture. */
 int dsl_quant_fp8_tensor_noalloc(const void *x, int64_t rows, int64_t cols,
                                  int64_t stride_row, int64_t stride_col, int x_dtype,
                                  uint8_t *q, float *scale, void *stream);

@@ -59,3 +59,51 @@ def test_no_alloc_fp32_source_and_strided_view():
     assert _same(_no_alloc(b_kn, N.IN_F32), _with_workspace(b_kn, N.IN_F32))
     x16 = x32[:64, :256].contiguous().bfloat16().to(DEV)
     assert _same(_no_alloc(x16, N.IN_BF16), _with_workspace(x16, N.IN_BF16))
+
+
+_CAPTURE_CHILD = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from dsl_tool_amd import _native as N
+dev = torch.device("cuda:0")
+torch.cuda.set_device(dev)
+g0 = torch.Generator().manual_seed(5)
+x = (torch.randn((1024, 2048), generator=g0) * 3).bfloat16().to(dev)
+q = torch.empty((1024, 2048), dtype=torch.uint8, device=dev)
+s = torch.empty(1, dtype=torch.float32, device=dev)
+side = torch.cuda.Stream(device=dev)          # capture stream, default priority
+graph = torch.cuda.CUDAGraph()
+# the process's first call of the entry point happens inside the capture
+with torch.cuda.graph(graph, stream=side):
+    N.call("dsl_quant_fp8_tensor_noalloc", N.ptr(x), 1024, 2048, 2048, 1, N.IN_BF16, N.ptr(q),
+           N.ptr(s), torch.cuda.current_stream(dev).cuda_stream)
+nb = N.lib().dsl_quant_workspace_bytes(1024, 2048)
+ws = torch.empty(nb // 4, dtype=torch.float32, device=dev)
+for rep in range(3):
+    if rep == 2:
+        x.mul_(0.25)                            # new input between replays
+    graph.replay()
+    torch.cuda.synchronize()
+    q2 = torch.empty_like(q)
+    s2 = torch.empty_like(s)
+    N.call("dsl_quant_fp8_tensor", N.ptr(x), 1024, 2048, 2048, 1, N.IN_BF16, N.ptr(q2), N.ptr(s2),
+           N.ptr(ws), nb, torch.cuda.current_stream(dev).cuda_stream)
+    torch.cuda.synchronize()
+    assert torch.equal(q, q2) and torch.equal(s.view(torch.int32), s2.view(torch.int32)), rep
+print("capture ok")
+"""
+
+
+def test_no_alloc_first_call_inside_graph_capture():
+    """In a fresh process, the entry point's first call (which looks up the
+    library-held array's device address) is made inside HIP graph capture;
+    the captured graph, replayed three times with the input changed before
+    the last replay, matches dsl_quant_fp8_tensor byte for byte each time."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, "-c", _CAPTURE_CHILD, root], capture_output=True,
+                         text=True, timeout=300)
+    assert res.returncode == 0 and "capture ok" in res.stdout, res.stdout + res.stderr
