@@ -173,15 +173,19 @@ def gemm_input_schema(kernel_name: str) -> dict:
                   "scale_b": "uint8 Tensor (pre-packed inputs only)",
                   "global_a": "float (nvfp4, pre-packed)", "global_b": "float (nvfp4, pre-packed)"})
     elif kernel_name.endswith("grouped_gemm"):
-        s = {"A": "Tensor[G, M, K] (fixed) | Tensor[T, K] rows sorted by group (variable)",
-             "B": "Tensor[G, K, N]",
-             "num_groups": "int G (fixed) | int32 Tensor[G+1] group offsets (variable)"}
+        s = {"A": "Tensor[G, M, K] (fixed) | Tensor[T, K] rows sorted by group (variable) "
+                  "| flat Tensor (descriptors)",
+             "B": "Tensor[G, K, N] | flat Tensor (descriptors)",
+             "num_groups": "int G (fixed) | int32 Tensor[G+1] group offsets (variable) | "
+                           "int32 Tensor[G, 6] GemmProblem descriptors (M, N, K, A_offset, "
+                           "B_offset, C_offset; per-group N and K)"}
     return s
 
 
 def gemm_output_schema(kernel_name: str) -> dict:
     if kernel_name.endswith("grouped_gemm"):
-        return {"C": "Tensor[G, M, N] | Tensor[T, N], bf16 (fp32 for fp32 inputs)"}
+        return {"C": "Tensor[G, M, N] | Tensor[T, N] | flat Tensor (descriptors), bf16 "
+                     "(fp32 for fp32 inputs)"}
     if kernel_name.endswith("bf16_gemm"):
         return {"C": "Tensor[M, N] fp32 (out_dtype=torch.bfloat16 for bf16)"}
     if kernel_name.endswith("lora_fused_gemm"):

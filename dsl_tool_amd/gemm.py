@@ -472,6 +472,60 @@ def fp4_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=None, scale_b=None, *,
     raise TypeError(f"fp4_gemm: unsupported dtypes {A.dtype}, {B.dtype}")
 
 
+def _grouped_problems(A: torch.Tensor, B: torch.Tensor, problems: torch.Tensor, out_dtype):
+    """Variable-size grouped GEMM over GemmProblem descriptors, the
+    reference's grouped_gemm_variable (cuda/gemm/grouped_gemm.cu:26-32,
+    :77-104, :150-156): problems [G, 6] integers (M, N, K, A_offset,
+    B_offset, C_offset), offsets in elements of the flat A, B and C buffers
+    (:95-97 use them as element offsets); group g computes C_g [M][N] =
+    A_g [M][K] @ B_g [K][N], all row-major.  A and B are bf16 / fp16 / fp32
+    and are quantized to E4M3 like the other grouped forms (per-row
+    activation, per-channel weight scales).  C is a new flat buffer of
+    max(C_offset + M*N) elements (fp32 for fp32 inputs, else bf16, or
+    out_dtype), zero where no group writes.
+
+    The descriptors are read on the host (their sizes choose the launches):
+    groups that share (N, K) run as one grouped FP8 GEMM over the device
+    offset table, one launch per distinct (N, K); M = 0, N = 0 groups are
+    skipped and K = 0 groups leave their C block at zero.  K % 16 == 0."""
+    if problems.shape[-1] != 6 or problems.dtype not in (torch.int32, torch.int64):
+        raise ValueError("problems must be an int tensor [G, 6]: M, N, K, A_offset, B_offset, C_offset")
+    if A.dim() != 1 or B.dim() != 1:
+        raise ValueError("with problem descriptors A and B are flat 1-D buffers")
+    if A.dtype not in _HIGH or B.dtype not in _HIGH:
+        raise TypeError(f"grouped_gemm problems: A and B must be bf16, fp16 or fp32 (got {A.dtype}, {B.dtype})")
+    dev = _require_gpu(A, B)
+    P = problems.to("cpu", torch.int64).tolist()
+    if out_dtype is None:
+        out_dtype = torch.float32 if A.dtype == torch.float32 else torch.bfloat16
+    out_dtype = _as_dtype(out_dtype)
+    c_len = 0
+    buckets: dict = {}
+    for g, (m, n, k, ao, bo, co) in enumerate(P):
+        if min(m, n, k, ao, bo, co) < 0:
+            raise ValueError(f"problem {g}: negative size or offset {P[g]}")
+        if ao + m * k > A.numel() or bo + k * n > B.numel():
+            raise ValueError(f"problem {g}: A / B range outside the buffers")
+        if m and n:
+            c_len = max(c_len, co + m * n)
+            if k:
+                if k % 16:
+                    raise ValueError(f"problem {g}: K={k} must be a multiple of 16")
+                buckets.setdefault((n, k), []).append(g)
+    C = torch.zeros(c_len, dtype=out_dtype, device=dev)
+    for (n, k), gs in buckets.items():
+        xs = [A[P[g][3]:P[g][3] + P[g][0] * k].view(P[g][0], k) for g in gs]
+        X = xs[0] if len(xs) == 1 else torch.cat(xs)
+        Bs = torch.stack([B[P[g][4]:P[g][4] + k * n].view(k, n) for g in gs])     # [Gb, K, N]
+        rows = torch.tensor([0] + [P[g][0] for g in gs], dtype=torch.int64).cumsum(0)
+        offsets = rows.to(device=dev, dtype=torch.int32)
+        Y = grouped_gemm(X, Bs, offsets, out_dtype=out_dtype)
+        for i, g in enumerate(gs):
+            m, co = P[g][0], P[g][5]
+            C[co:co + m * n].view(m, n).copy_(Y[int(rows[i]):int(rows[i + 1])])
+    return C
+
+
 def grouped_gemm(A: torch.Tensor, B: torch.Tensor, num_groups, scale_a=None, scale_b=None, *,
                  out_dtype: torch.dtype | None = None):
     """Grouped FP8 GEMM (MoE experts / LoRA adapters), one W per group.
@@ -481,6 +535,10 @@ def grouped_gemm(A: torch.Tensor, B: torch.Tensor, num_groups, scale_a=None, sca
     * ``num_groups`` a 1-D integer tensor of G+1 offsets: variable-size
       groups, A [T, K] with rows sorted by group, B [G, K, N] -> C [T, N];
       empty groups are allowed.
+    * ``num_groups`` a 2-D integer tensor [G, 6] of GemmProblem descriptors
+      (M, N, K, A_offset, B_offset, C_offset; cuda/gemm/grouped_gemm.cu:26-32):
+      every group has its own M, N and K, over flat A, B and C buffers (see
+      _grouped_problems).
     High-precision inputs are quantized to E4M3 with per-row activation and
     per-channel weight scales, so bf16 inputs give an FP8 product, not the
     reference's unquantized bf16 batched product (grouped_gemm_kernel,
@@ -494,6 +552,8 @@ def grouped_gemm(A: torch.Tensor, B: torch.Tensor, num_groups, scale_a=None, sca
     travels over ``run_from_spec`` as five tensor specs [X, B, offsets,
     scale_a, scale_b] (dispatcher.py:285-294).
     """
+    if isinstance(num_groups, torch.Tensor) and num_groups.dim() == 2:
+        return _grouped_problems(A, B, num_groups, out_dtype)
     if isinstance(num_groups, torch.Tensor):
         offsets = num_groups
         if A.dim() != 2 or B.dim() != 3:

@@ -171,3 +171,36 @@ def test_rest_prequantized_fp8_groupwise_reference_layout():
     ref = OG._mm(OG.dequant_fp8_blocks(qa, sa, 1, G), OG.dequant_fp8_blocks(qw, swr, 1, G))
     glob, elem = OG.rel_errors(_out(r.json()), ref)
     assert glob <= 1e-2 and elem <= 1e-2, (glob, elem)
+
+
+def test_rest_grouped_problem_descriptors():
+    """grouped_gemm with GemmProblem descriptors over the REST wire: flat A
+    and B bf16 specs and an int32 [G, 6] spec (M, N, K, A_offset, B_offset,
+    C_offset; cuda/gemm/grouped_gemm.cu:26-32), per-group N and K."""
+    from fastapi.testclient import TestClient
+
+    from dsl_tool_amd.dispatcher.api import app
+    specs = [(24, 32, 256), (9, 64, 512), (0, 16, 256)]
+    probs, ao, bo, co = [], 0, 0, 0
+    for m, n, k in specs:
+        probs.append([m, n, k, ao, bo, co])
+        ao, bo, co = ao + m * k, bo + k * n, co + m * n
+    a, b = _seeded((ao,), 931), _seeded((bo,), 932, 0.02)
+    P = np.array(probs, np.int32)
+    req = {"kernel_name": "gemm.grouped_gemm", "backend": "hip",
+           "inputs": [_spec(a), _spec(b), _raw(P, "int32")],
+           "params": {"out_dtype": "float32"}}
+    with TestClient(app) as c:
+        r = c.post("/api/v1/kernels/run", json=req)
+    assert r.status_code == 200, r.text
+    got = _out(r.json()).reshape(-1)
+    for m, n, k, a0, b0, c0 in probs:
+        if m == 0:
+            continue
+        ag = a[a0:a0 + m * k].reshape(m, k).float().numpy()
+        wg = b[b0:b0 + k * n].reshape(k, n).t().contiguous().float().numpy()
+        qa, sa = OQ.quant_fp8_blockwise(ag, 1, k)
+        qw, sw = OQ.quant_fp8_blockwise(wg, 1, k)
+        ref = OG._mm(OG.dequant_fp8_blocks(qa, sa, 1, k), OG.dequant_fp8_blocks(qw, sw, 1, k))
+        glob, elem = OG.rel_errors(got[c0:c0 + m * n].reshape(m, n), ref)
+        assert glob <= 1e-2 and elem <= 1e-2, (glob, elem)

@@ -224,6 +224,50 @@ def test_grouped_registered_variable_and_fixed():
     assert_close(y3.reshape(-1, 96), ref3, what="grouped_gemm fixed")
 
 
+def test_grouped_problem_descriptors_per_group_n_and_k():
+    """GemmProblem descriptors (cuda/gemm/grouped_gemm.cu:26-32): every group
+    with its own M, N and K over flat buffers at element offsets (LoRA-style
+    ranks 16..128, K 512..2048), an empty group, a K = 0 group and gaps in
+    the buffers; each C block against the oracle on the same per-row /
+    per-channel E4M3 codes, the rest of C zero."""
+    specs = [(40, 16, 1024), (0, 32, 1024), (70, 64, 2048), (33, 16, 1024), (5, 48, 0),
+             (100, 128, 512), (1, 16, 2048)]
+    rng = np.random.default_rng(621)
+    a_off, b_off, probs = 0, 0, []
+    order = rng.permutation(len(specs))              # C blocks in a shuffled order
+    sizes = [specs[g][0] * specs[g][1] + 7 for g in order]
+    c_off = dict(zip(order, np.cumsum([0] + sizes)[:-1]))
+    for g, (m, n, k) in enumerate(specs):
+        probs.append([m, n, k, a_off, b_off, int(c_off[g])])
+        a_off += m * k + 24
+        b_off += k * n + 40
+    A = W.randn_bf16((a_off,), 622)
+    B = W.randn_bf16((b_off,), 623, 0.02)
+    P = torch.tensor(probs, dtype=torch.int32)
+    C = G.grouped_gemm(A.to(DEV), B.to(DEV), P.to(DEV), out_dtype=torch.float32)
+    got = np_f32(C)
+    covered = np.zeros(got.size, bool)
+    for g, (m, n, k, ao, bo, co) in enumerate(probs):
+        if m == 0 or n == 0:
+            continue
+        covered[co:co + m * n] = True
+        blk = got[co:co + m * n].reshape(m, n)
+        if k == 0:
+            assert not blk.any()
+            continue
+        ag = _f32(A[ao:ao + m * k].reshape(m, k))
+        wg = _f32(B[bo:bo + k * n].reshape(k, n).t().contiguous())
+        qa, sa = OQ.quant_fp8_blockwise(ag, 1, k)
+        qw, sw = OQ.quant_fp8_blockwise(wg, 1, k)
+        ref = OG._mm(OG.dequant_fp8_blocks(qa, sa, 1, k), OG.dequant_fp8_blocks(qw, sw, 1, k))
+        assert_close(torch.from_numpy(blk), ref, what=f"grouped problem {g} ({m}x{n}x{k})")
+    assert not got[~covered].any()
+    with pytest.raises(ValueError, match="multiple of 16"):
+        G.grouped_gemm(A.to(DEV), B.to(DEV), torch.tensor([[4, 16, 40, 0, 0, 0]]))
+    with pytest.raises(ValueError, match="outside"):
+        G.grouped_gemm(A.to(DEV), B.to(DEV), torch.tensor([[4, 16, 64, a_off, 0, 0]]))
+
+
 def test_weights_in_kn_layout_are_transposed_once_and_follow_writes():
     """Pre-quantized weights held in the reference's [K, N] / [G, K, N]
     layout (not transpose views of K-major storage): the K-major copy is
