@@ -122,10 +122,13 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_decode_kernel(const GemmArgs p) 
       else dec::dma16_nt(s, dst + r * CHUNK);
     }
     if constexpr (Cfg::MX) {
-      // 16 rows x 64 E8M0 bytes: lane -> row lane/4, 16 bytes lane%4
+      // 16 rows x 64 E8M0 bytes (4 superblocks x 16): lane -> row r =
+      // lane/4, superblock (lane - r/4) % 4, so superblock b of row r sits
+      // in 16-byte slot (b + r/4) % 4 of the row (mx_scale_word)
       const int row = min(rbase + (lane >> 2), rlim);
       const uint8_t *sc = static_cast<const uint8_t *>(isA ? p.sa : p.sb);
-      dec::dma16(sc + row * sld + kb0 / 16 + ((lane & 3) << 4), dst + 16 * CHUNK);
+      dec::dma16(sc + row * sld + kb0 / 16 + ((((lane & 3) - (lane >> 4)) & 3) << 4),
+                 dst + 16 * CHUNK);
     } else if constexpr (Cfg::BLOCK) {
       // activation tile: sa[row][8 groups of the chunk], 32 bytes per row
       // (lanes 32..63 repeat lanes 0..31); W tile: sb[n/128][8 groups]
@@ -150,6 +153,12 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_decode_kernel(const GemmArgs p) 
   auto chunk16 = [&](const uint8_t *base, int c) {      // row r16's logical chunk c
     return *reinterpret_cast<const v4i *>(base + r16 * CHUNK + ((c ^ r16) << 4));
   };
+  // MXFP4: the E8M0 word of lane group g in superblock b of row r16.  The
+  // rotation by r16/4 puts the 64 lanes of one read on 64 distinct banks
+  // (rows 64 bytes apart would otherwise put rows r, r+4, r+8, r+12 on one).
+  auto mx_scale_word = [&](const uint8_t *aux, int b) {
+    return *reinterpret_cast<const int *>(aux + r16 * 64 + (((b + (r16 >> 2)) & 3) << 4) + g * 4);
+  };
 
   // consume item of kind KIND from `base`
   auto consume = [&](auto kind_tag, const uint8_t *base) {
@@ -161,7 +170,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_decode_kernel(const GemmArgs p) 
         for (int b = 0; b < 4; ++b) {
 #pragma unroll
           for (int j = 0; j < 4; ++j) st.ad[KIND][b][j] = chunk16(base, b * 16 + 4 * g + j);
-          st.as[KIND][b] = *reinterpret_cast<const int *>(aux + r16 * 64 + b * 16 + g * 4);
+          st.as[KIND][b] = mx_scale_word(aux, b);
         }
       } else {
 #pragma unroll
@@ -188,7 +197,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_decode_kernel(const GemmArgs p) 
       if constexpr (Cfg::MX) {
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
-          const int wsv = *reinterpret_cast<const int *>(aux + r16 * 64 + b * 16 + g * 4);
+          const int wsv = mx_scale_word(aux, b);
           v4i wd[4];
 #pragma unroll
           for (int j = 0; j < 4; ++j) wd[j] = chunk16(base, b * 16 + 4 * g + j);
