@@ -636,7 +636,8 @@ def profile_traffic(steps: int) -> int:
 # targets (FP8 and MXFP4 8192^3, decode M=16), the grouped MoE GEMM and
 # BASELINE config 1.
 PROFILE_CASES = ["fp8_block_m4096", "fp8_tensor_8192", "mxfp4_8192", "grouped_moe",
-                 "fp8_block_m16", "mxfp4_m16", "fp8_tensor_cfg1"]
+                 "fp8_block_m16", "mxfp4_m16", "fp8_tensor_cfg1", "fp8_group_m4096",
+                 "nvfp4_m2048"]
 PROFILE_PASSES = [
     ["MfmaUtil", "GRBM_GUI_ACTIVE", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_INSTS_LDS",
      "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "SQ_INSTS_VALU_MFMA_MOPS_F8",

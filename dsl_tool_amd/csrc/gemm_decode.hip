@@ -1,8 +1,8 @@
 // Skinny-M ("decode") quantized GEMMs for gfx950: C[M,N] = A[M,K] . W[N,K]^T
 // with few activation rows, bound by streaming W from HBM.
 //
-// gemm_decode_kernel (FP8 per-tensor, FP8 1x128/128x128 block, MXFP4, bf16;
-// M <= 32)
+// gemm_decode_kernel (FP8 per-tensor, FP8 1x128/128x128 block, FP8 1x128
+// groups with a weight scale per output column, MXFP4, bf16; M <= 32)
 //   One workgroup owns 32 rows of W (two 16-row MFMA tiles) over the whole
 //   of K; its four waves split K into contiguous ranges of whole 1 KB chunks
 //   (1 KB of every row: 1024 FP8 or 2048 FP4 elements).  A wave streams a
@@ -27,7 +27,8 @@
 //       chunks g and 4+g of the step (the same K order for A and W, so the
 //       sum is unchanged; for block scales a step is exactly one 128-K scale
 //       group, folded as acc += part * sa[m][grp] * sb[n/128][grp], the
-//       group-partial form of cuda/gemm/fp8_gemm.cu:84-97).
+//       group-partial form of cuda/gemm/fp8_gemm.cu:84-97; with per-column
+//       weight scales sb[grp][n], each lane's column scale of the group).
 //     bf16: as FP8 per-tensor with 64 elements per 128-byte step; the lane's
 //       32 bytes feed two v_mfma_f32_16x16x32_bf16 (first and second chunk).
 //     MXFP4: K is taken in 512-element superblocks of 4 steps; at step j of
@@ -66,10 +67,15 @@ struct DecodeCfg {
   static constexpr int TN = 2;                      // 16-row W tiles per workgroup
   static constexpr int NW = 4, NT = NW * 64;        // waves split K
   static constexpr bool MX = MODE == MODE_MXFP4;
-  static constexpr bool BLOCK = MODE == MODE_FP8_BLOCK;
+  static constexpr bool BLOCK = mode_grouped_k(MODE);     // fp32 scales per 128-K group
+  static constexpr bool GCOL = MODE == MODE_FP8_GCOL;     // ... per W row (output column)
   static constexpr int CHUNK = 1024;                // bytes of one row per item
   static constexpr int AUX = (MX || BLOCK) ? 1024 : 0;   // scale bytes per item (DMA target)
-  static constexpr int DPI = 16 + (AUX ? 1 : 0);    // DMA instructions per item
+  // scale DMAs per item (GCOL: two 4-byte copies of the W tile's 16 x 8
+  // column scales; activation items repeat their one copy, so that every
+  // item is the same number of loads for the vmcnt count)
+  static constexpr int ADMA = GCOL ? 2 : (AUX ? 1 : 0);
+  static constexpr int DPI = 16 + ADMA;             // DMA instructions per item
   static constexpr int REGION = 16 * CHUNK + AUX;
   static constexpr int P = TMA + TN;                // items per chunk
   static_assert(2 * NW * REGION + NW * TN * TMA * 1024 <= 160 * 1024, "LDS budget");
@@ -129,6 +135,23 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_decode_kernel(const GemmArgs p) 
       const uint8_t *sc = static_cast<const uint8_t *>(isA ? p.sa : p.sb);
       dec::dma16(sc + row * sld + kb0 / 16 + ((((lane & 3) - (lane >> 4)) & 3) << 4),
                  dst + 16 * CHUNK);
+    } else if constexpr (Cfg::GCOL) {
+      if (isA) {
+        // sa[row][8 groups of the chunk], as the block form (twice)
+        const int row = min(rbase + ((lane >> 1) & 15), rlim);
+        const float *sc = static_cast<const float *>(p.sa) + (int64_t)row * nkg + ch * 8 + ((lane & 1) << 2);
+        dec::dma16(sc, dst + 16 * CHUNK);
+        dec::dma16(sc, dst + 16 * CHUNK);
+      } else {
+        // sb[group][column] of the tile's 16 columns and the chunk's 8
+        // groups, stored [group][column]: lane -> column lane % 16, group
+        // 4d + lane / 16 (columns past the last clamped)
+        const int col = min(rbase + (lane & 15), rlim);
+#pragma unroll
+        for (int d = 0; d < 2; ++d)
+          dec::dma4(static_cast<const float *>(p.sb) + (int64_t)(ch * 8 + 4 * d + (lane >> 4)) * p.N + col,
+                    dst + 16 * CHUNK + d * 256);
+      }
     } else if constexpr (Cfg::BLOCK) {
       // activation tile: sa[row][8 groups of the chunk], 32 bytes per row
       // (lanes 32..63 repeat lanes 0..31); W tile: sb[n/128][8 groups]
@@ -211,7 +234,11 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_decode_kernel(const GemmArgs p) 
         }
       } else {
         v4f sb0, sb1;
-        if constexpr (Cfg::BLOCK) {
+        float sbc[8];                  // GCOL: this lane's column scale per group
+        if constexpr (Cfg::GCOL) {
+#pragma unroll
+          for (int s = 0; s < 8; ++s) sbc[s] = reinterpret_cast<const float *>(aux)[s * 16 + r16];
+        } else if constexpr (Cfg::BLOCK) {
           sb0 = *reinterpret_cast<const v4f *>(aux);
           sb1 = *reinterpret_cast<const v4f *>(aux + 16);
         }
@@ -224,7 +251,7 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_decode_kernel(const GemmArgs p) 
             if constexpr (Cfg::BLOCK) {
               const v4f zero = {0.f, 0.f, 0.f, 0.f};
               const v4f part = mfma_fp8(st.af[a][s], wf, zero);
-              const float sbv = s < 4 ? sb0[s & 3] : sb1[s & 3];
+              const float sbv = Cfg::GCOL ? sbc[s] : (s < 4 ? sb0[s & 3] : sb1[s & 3]);
               st.acc[T][a] = part * (st.sa[a][s] * sbv) + st.acc[T][a];
             } else if constexpr (Cfg::MODE == MODE_BF16) {
               st.acc[T][a] = mfma_bf16(st.af[a][s], wf, st.acc[T][a]);
@@ -466,7 +493,7 @@ bool decode_supported(int mode, int M, int K, int Kb, bool scales4, bool scales1
   if (M > 32) return false;
   if (mode == MODE_FP8_TENSOR || mode == MODE_BF16) return true;
   // block scales and E8M0 rows move by 16-byte direct loads
-  if (mode == MODE_FP8_BLOCK) return scales16 && K % 512 == 0;
+  if (mode_grouped_k(mode)) return scales16 && K % 512 == 0;
   if (mode == MODE_MXFP4) return scales16 && K % 512 == 0;
   return false;
 }
@@ -475,6 +502,7 @@ hipError_t launch_gemm_decode(int mode, const GemmArgs &p, hipStream_t st) {
   switch (mode) {
     case MODE_FP8_TENSOR: return launch_decode_mode<MODE_FP8_TENSOR>(p, st);
     case MODE_FP8_BLOCK: return launch_decode_mode<MODE_FP8_BLOCK>(p, st);
+    case MODE_FP8_GCOL: return launch_decode_mode<MODE_FP8_GCOL>(p, st);
     case MODE_MXFP4: return launch_decode_mode<MODE_MXFP4>(p, st);
     case MODE_BF16: return launch_decode_mode<MODE_BF16>(p, st);
     case MODE_NVFP4:
@@ -484,7 +512,7 @@ hipError_t launch_gemm_decode(int mode, const GemmArgs &p, hipStream_t st) {
         case 3: return launch_gemv_nv_m<3>(p, st);
         default: return launch_gemv_nv_m<4>(p, st);
       }
-    default: return hipErrorInvalidValue;   // FP8_GCOL: decode_supported is false
+    default: return hipErrorInvalidValue;
   }
 }
 

@@ -529,7 +529,7 @@ def test_mxfp4_decode(m, n, k):
 # kernel (DSL_GEMM_SKINNY=decode, read at every launch).
 @pytest.mark.parametrize("m,n,k", [(2, 4096, 4096), (7, 2048, 1024), (8, 1000, 2048), (16, 5000, 2048),
                                    (9, 6200, 1024), (5, 16, 3072), (32, 1040, 2048), (16, 14336, 1024)])
-@pytest.mark.parametrize("mode", ["tensor", "block", "mxfp4", "bf16"])
+@pytest.mark.parametrize("mode", ["tensor", "block", "group", "mxfp4", "bf16"])
 def test_decode_kernel_forced(mode, m, n, k, monkeypatch):
     monkeypatch.setenv("DSL_GEMM_SKINNY", "decode")
     a = W.randn_bf16((m, k), 631)
@@ -544,6 +544,13 @@ def test_decode_kernel_forced(mode, m, n, k, monkeypatch):
         qw, sw = Q.quant_fp8_blocks(w.to(DEV), 128, 128)
         c = G.fp8_gemm_packed(qa, qw, sa, sw, block=True)
         ref = OG.ref_fp8_groupwise(np_u8(qa), np_f32(sa), np_u8(qw), np_f32(sw))
+    elif mode == "group":
+        # per-column weight scales sb[K/128][N] (the reference's groupwise layout)
+        qa, sa = Q.quant_fp8_blocks(a.to(DEV), 1, 128)
+        qw, swr = Q.quant_fp8_blocks(w.to(DEV), 1, 128)
+        sb = swr.t().contiguous()
+        c = G.fp8_gemm_packed(qa, qw, sa, sb, group=True)
+        ref = OG.ref_fp8_groupwise_cols(np_u8(qa), np_f32(sa), np_u8(qw), np_f32(sb), 128)
     elif mode == "mxfp4":
         qa, ea = Q.quant_mxfp4(a.to(DEV))
         qw, ew = Q.quant_mxfp4(w.to(DEV))

@@ -7,8 +7,9 @@ The operands are quantized on the GPU (1 x G groups along K, the weight
 per output column) and checked byte for byte against the oracle quantizer;
 the GEMM output is then held to the dequantize -> matmul oracle
 (oracle.gemm.ref_fp8_groupwise_cols) on the same codes.  Shapes are chosen
-to take every kernel that serves the mode: the streaming kernel (M <= 1024
-while ceil(M/64) N stays small, the decode sizes included), the pipelined
+to take every kernel that serves the mode: the decode kernel (9 <= M <= 16
+where its 32-row grid fills the CUs), the streaming kernel (M <= 1024 while
+ceil(M/64) N stays small, the other skinny sizes), the pipelined
 128x128 and 256x256 per-stage partial kernels, and the register-staged tiles
 (K % 128 != 0, with and without split-K).  Every kernel here starts each
 group's MFMA sum from zero, so the elementwise bound is the plain 1e-2.
@@ -44,7 +45,7 @@ def _quant_cols(a, w, gsize):
 
 # (m, n, k): kernel the default route takes
 GROUP_SHAPES = [
-    (16, 7168, 4096),     # streaming, config 2's decode shape
+    (16, 7168, 4096),     # decode kernel, config 2's decode shape
     (1, 1000, 2048),      # streaming, one row, ragged N
     (128, 4096, 4096),    # streaming, 64-row blocks
     (33, 4100, 1536),     # streaming, ragged N (column scales clamped at the edge)
