@@ -141,10 +141,13 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     v8i bf[TN];
 #pragma unroll
     for (int t = 0; t < TN; ++t) bf[t] = ld(sB, wn * Cfg::WN + t * 16 + r16);
+    // the next row's A fragment is read while this row's MFMAs run
+    v8i afn = ld(sA, wm * Cfg::WM + r16);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int arow = wm * Cfg::WM + i * 16;
-      const v8i af = ld(sA, arow + r16);
+      const v8i af = afn;
+      if (i + 1 < TM) afn = ld(sA, arow + 16 + r16);
       const v4f s4 = *reinterpret_cast<const v4f *>(sSa + arow + 4 * g) * sbv;
       const v4f zero = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
