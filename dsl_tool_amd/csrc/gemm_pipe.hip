@@ -123,7 +123,6 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     if (ks + NS - 2 < nks) pipe::wait_vmcnt<(NS - 2) * D>();
     else pipe::wait_vmcnt<0>();
     __syncthreads();
-    if (ks + NS - 1 < nks) ring.issue(ks + NS - 1, lds0);
     const uint8_t *st = smem + (ks % NS) * Cfg::STAGE;
     const uint8_t *sA = st, *sB = st + Cfg::A_BYTES;
     const float *sSa = reinterpret_cast<const float *>(st + Cfg::A_BYTES + Cfg::B_BYTES);
@@ -143,6 +142,9 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     for (int t = 0; t < TN; ++t) bf[t] = ld(sB, wn * Cfg::WN + t * 16 + r16);
     // the next row's A fragment is read while this row's MFMAs run
     v8i afn = ld(sA, wm * Cfg::WM + r16);
+    // the next stage's copies go out after this stage's first fragment
+    // reads, so that those are not queued behind the copy burst
+    if (ks + NS - 1 < nks) ring.issue(ks + NS - 1, lds0);
 #pragma unroll
     for (int i = 0; i < TM; ++i) {
       const int arow = wm * Cfg::WM + i * 16;
