@@ -332,6 +332,14 @@ def build_cases(names, dev):
             return L.dsl_moe_quant_tokens(x.data_ptr(), T, K, K, dest.data_ptr(), k, rows,
                                           qt.data_ptr(), sx.data_ptr(), st)
 
+        # decode sizes: route and per-token quantize in one launch
+        fused = gather and MOE.route_quant_applies(T, k, E, K)
+
+        def route_quant(st):
+            return L.dsl_moe_route_quant_tokens(ids.data_ptr(), T, k, E, x.data_ptr(), K, K,
+                                                off.data_ptr(), dest.data_ptr(), src.data_ptr(),
+                                                qt.data_ptr(), sx.data_ptr(), st)
+
         it = [0]
 
         def grouped(st):
@@ -351,11 +359,13 @@ def build_cases(names, dev):
                                      out.data_ptr(), Nn, N.OUT_BF16, st)
         s0 = torch.cuda.current_stream().cuda_stream
         # tables and buffers valid before timing
-        for f in (route, permute, grouped, quant_tokens) + ((grouped_gather,) if gather else ()) + (combine,):
+        for f in ((route, permute, grouped, quant_tokens) + ((grouped_gather,) if gather else ())
+                  + ((route_quant,) if fused else ()) + (combine,)):
             assert f(s0) == 0
         stages = {"route": [route], "permute": [permute], "quant_tokens": [quant_tokens],
                   "combine": [combine], "grouped": [grouped], "grouped_gather": [grouped_gather],
-                  "layer": [route, quant_tokens, grouped_gather, combine] if gather
+                  "layer": ([route_quant, grouped_gather, combine] if fused
+                            else [route, quant_tokens, grouped_gather, combine]) if gather
                   else [route, permute, grouped, combine],
                   "layer_permuted": [route, permute, grouped, combine]}[stage]
 
@@ -393,10 +403,12 @@ def build_cases(names, dev):
                 "grouped_gather": f"grouped FP8 GEMM of the routed rows, A read through the row map "
                                   f"from 4096 token-major rows, {rot} weight copies rotated"}[stage]
         if decode:
-            glue = ("per-token E4M3 + grouped FP8 GEMM reading A through the row map"
-                    if stage == "layer" and gather else "permute/quant + grouped FP8 GEMM")
+            glue = ("route + per-token E4M3 in one launch + grouped FP8 GEMM reading A through "
+                    "the row map" if stage == "layer" and fused else
+                    "route + per-token E4M3 + grouped FP8 GEMM reading A through the row map"
+                    if stage == "layer" and gather else "route + permute/quant + grouped FP8 GEMM")
             what = (f"MoE projection at decode size ({tokens} tokens x top-8 over 64 experts, N=1536 "
-                    f"K=2048): route + {glue} + combine, {rot} weight copies rotated"
+                    f"K=2048): {glue} + combine, {rot} weight copies rotated"
                     ) if stage.startswith("layer") else what.replace("4096", str(tokens)).replace(
                         "32768", str(rows))
         return Case(name, flops, nbytes, PEAK_FP8_TFLOPS,

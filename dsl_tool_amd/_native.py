@@ -33,7 +33,7 @@ OP_FP8, OP_FP4, OP_GROUPED_FP8, OP_BF16 = 0, 1, 2, 3
 QFMT_FP8_G128, QFMT_MXFP4 = 0, 1
 W_BF16, W_F32 = 0, 1
 IN_BF16, IN_F32 = 0, 1
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 
 class DslLibraryError(ImportError):
@@ -78,6 +78,8 @@ SIGNATURES = {
     "dsl_moe_route": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _vp, _vp, _sz, _vp]),
     "dsl_moe_permute_quant": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp]),
     "dsl_moe_quant_tokens": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp]),
+    "dsl_moe_route_quant_tokens": (_i32, [_vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp,
+                                          _vp, _vp, _vp]),
     "dsl_moe_grouped_fp8_gemm": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                         _i64, _i32, _vp, _vp, _vp]),
     "dsl_moe_combine": (_i32, [_vp, _i64, _i64, _i64, _vp, _vp, _i64, _i64, _vp, _i64, _i32, _vp]),

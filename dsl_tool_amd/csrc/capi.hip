@@ -83,7 +83,7 @@ extern "C" {
 
 const char *dsl_last_error(void) { return g_err.c_str(); }
 
-int dsl_abi_version(void) { return 9; }
+int dsl_abi_version(void) { return 10; }
 
 size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols) {
   (void)rows;
@@ -631,6 +631,38 @@ int dsl_moe_quant_tokens(const void *x, int64_t tokens, int64_t k, int64_t ldx,
                          void *stream) {
   return run_moe_quant("dsl_moe_quant_tokens", x, tokens, k, ldx, dest, topk, rows, qx, sx, true,
                        stream);
+}
+
+int dsl_moe_route_quant_tokens(const int32_t *topk_ids, int64_t tokens, int64_t topk,
+                               int64_t num_experts, const void *x, int64_t k, int64_t ldx,
+                               int32_t *offsets, int32_t *dest, int32_t *src_token, uint8_t *qx,
+                               float *sx, void *stream) {
+  const char *fn = "dsl_moe_route_quant_tokens";
+  if (tokens < 0 || topk <= 0 || num_experts <= 0 || num_experts > dsl::kMaxGroups)
+    return fail(DSL_ERR_ARG, "%s: need tokens >= 0, topk > 0, 1 <= num_experts <= %d", fn,
+                dsl::kMaxGroups);
+  if (k <= 0 || k % 8 != 0 || ldx < k || ldx % 8 != 0)
+    return fail(DSL_ERR_ARG, "%s: k must be a positive multiple of 8, ldx >= k a multiple of 8", fn);
+  if (tokens * topk >= ((int64_t)1 << 31)) return fail(DSL_ERR_ARG, "%s: too many assignments", fn);
+  if (!offsets) return fail(DSL_ERR_ARG, "%s: offsets is NULL", fn);
+  const int64_t n = tokens * topk;
+  if (n > dsl::moe_route_quant_max_assignments || num_experts > 2047 || k > 2048)
+    return fail(DSL_ERR_UNSUPPORTED,
+                "%s: one launch covers tokens * topk <= %d, num_experts <= 2047, k <= 2048 "
+                "(dsl_moe_route + dsl_moe_quant_tokens cover the rest)", fn,
+                dsl::moe_route_quant_max_assignments);
+  if (tokens == 0)   // no token: the zero offsets only (the one-wave route needs no workspace)
+    return hip_status(dsl::launch_moe_route(topk_ids, 0, (int)topk, (int)num_experts, offsets,
+                                            dest, src_token, nullptr,
+                                            static_cast<hipStream_t>(stream)), fn);
+  int rc;
+  if ((rc = check_out(fn, x, "x")) || (rc = check_out(fn, qx, "qx"))) return rc;
+  if (!topk_ids || !dest || !src_token || !sx) return fail(DSL_ERR_ARG, "%s: NULL pointer argument", fn);
+  return hip_status(dsl::launch_moe_route_quant(topk_ids, (int)n, (int)topk, (int)num_experts,
+                                                static_cast<const uint16_t *>(x), ldx, (int)k,
+                                                (int)tokens, offsets, dest, src_token, qx, sx,
+                                                static_cast<hipStream_t>(stream)),
+                    fn);
 }
 
 int dsl_moe_grouped_fp8_gemm(const uint8_t *x, int64_t tokens, const int32_t *src_token,

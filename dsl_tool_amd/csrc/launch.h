@@ -171,6 +171,15 @@ hipError_t launch_moe_route(const int32_t *ids, int n, int topk, int E, int32_t 
 hipError_t launch_moe_permute_quant(const uint16_t *x, int64_t ldx, int k_dim, int tokens,
                                     const int32_t *dest, int topk, int rows, uint8_t *qx, float *sx,
                                     bool tok_major, hipStream_t st);
+// launch_moe_route and the tok_major launch_moe_permute_quant in one launch
+// for decode-size batches: n <= moe_route_quant_max_assignments, E <= 2047,
+// k_dim <= 2048, ldx % 8 == 0, tokens >= 1 (else hipErrorInvalidValue, and
+// nothing is launched).  Same offsets, dest, src_token, codes and scales.
+constexpr int moe_route_quant_max_assignments = 1024;
+hipError_t launch_moe_route_quant(const int32_t *ids, int n, int topk, int E,
+                                  const uint16_t *x, int64_t ldx, int k_dim, int tokens,
+                                  int32_t *offsets, int32_t *dest, int32_t *src_token,
+                                  uint8_t *qx, float *sx, hipStream_t st);
 // n <= 32768; slots whose row is < 0 or >= rows_y are skipped.
 hipError_t launch_moe_combine(const uint16_t *y, int rows_y, int64_t ldy, int n, const int32_t *dest,
                               const float *w, int tokens, int topk, void *out, int64_t ldo,

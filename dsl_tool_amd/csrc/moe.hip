@@ -544,6 +544,129 @@ __global__ __launch_bounds__(256) void moe_quant_tokens_wave_kernel(
   }
 }
 
+// Route and per-token quantize in one launch for decode-size batches (up to
+// 64 * kWaveSteps assignments, k <= 2048): one wave per token, four per
+// workgroup.  Every wave ranks all the assignments exactly as
+// moe_route_wave_kernel does (ballots per step, per-expert counts in its own
+// LDS slice, the exclusive scan over the experts) -- a few hundred
+// instructions at these sizes, issued while the token's row is loading --
+// and then writes its own token's part only: dest and src_token of the
+// token's assignments, the token's codes (as moe_quant_tokens_wave_kernel),
+// and its scale at each of the token's sorted rows.  Token 0's wave writes
+// the offsets.  So the tables, codes and scales are those of the two
+// launches it replaces, bit for bit.
+template <int CPL>
+__global__ __launch_bounds__(256) void moe_route_quant_wave_kernel(
+    const int32_t *__restrict__ ids, int n, int E, int topk, const uint16_t *__restrict__ x,
+    int64_t ldx, int k_dim, int tokens, int32_t *__restrict__ offsets,
+    int32_t *__restrict__ dest, int32_t *__restrict__ src_token, uint8_t *__restrict__ qx,
+    float *__restrict__ sx) {
+  extern __shared__ int slices[];        // [4 waves][E] counts, then first rows
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= tokens) return;               // whole waves: no barrier below
+  const int lane = threadIdx.x & 63;
+  int *cnt = slices + (threadIdx.x >> 6) * E;
+  // the token's row first: its loads are in flight during the ranking
+  const int nch = k_dim >> 3;
+  const uint4 *xr = reinterpret_cast<const uint4 *>(x + (int64_t)t * ldx);
+  uint4 d[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    d[j] = c < nch ? xr[c] : make_uint4(0, 0, 0, 0);
+  }
+  for (int e = lane; e < E; e += 64) cnt[e] = 0;
+  int bits = 0;
+  while ((1 << bits) < E + 1) ++bits;
+  const uint64_t below = (1ull << lane) - 1ull;
+  const int steps = (n + 63) / 64;
+  int kr[kWaveSteps];                    // key (12 bits, E for dropped) | rank << 12
+#pragma unroll
+  for (int st = 0; st < kWaveSteps; ++st) {
+    kr[st] = E;
+    if (st < steps) {                    // uniform
+      const int a = st * 64 + lane;
+      const int e = a < n ? ids[a] : -1;
+      kr[st] = (e >= 0 && e < E) ? e : E;
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);    // lgkmcnt(0): the zeroed counts are in LDS
+  __builtin_amdgcn_wave_barrier();
+#pragma unroll
+  for (int st = 0; st < kWaveSteps; ++st) {
+    if (st < steps) {                    // uniform
+      const int k = kr[st];
+      uint64_t same = ~0ull;
+      for (int b = 0; b < bits; ++b) {
+        const uint64_t m = __ballot((k >> b) & 1);
+        same &= ((k >> b) & 1) ? m : ~m;
+      }
+      int r = 0;
+      if (k < E) r = cnt[k] + __popcll(same & below);
+      __builtin_amdgcn_s_waitcnt(0xc07f);  // every lane's read of cnt is back
+      __builtin_amdgcn_wave_barrier();
+      if (k < E && (same >> lane) == 1ull) cnt[k] = r + 1;
+      kr[st] = k | (r << 12);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  int carry = 0;
+  for (int e0 = 0; e0 < E; e0 += 64) {   // exclusive scan over the experts
+    const int e = e0 + lane;
+    const int c = e < E ? cnt[e] : 0;
+    int incl = c;
+#pragma unroll
+    for (int dd = 1; dd < 64; dd <<= 1) {
+      const int v = __shfl_up(incl, dd, 64);
+      if (lane >= dd) incl += v;
+    }
+    if (e < E) {
+      cnt[e] = carry + incl - c;
+      if (t == 0) offsets[e] = carry + incl - c;
+    }
+    carry += __shfl(incl, 63, 64);
+  }
+  if (t == 0 && lane == 0) offsets[E] = carry;
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  // the token's codes and scale (moe_quant_tokens_wave_kernel's arithmetic)
+  float m = 0.f;
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    float f[8];
+    unpack8(d[j], f);
+    m = fmaxf(m, amax8(f));
+  }
+  const float s = fp8_scale_of(wave_max(m));
+  const float rq = rcp_approx(s);
+  uint2 *qr = reinterpret_cast<uint2 *>(qx + (int64_t)t * k_dim);
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) {
+    const int c = lane + 64 * j;
+    if (c < nch) {
+      float f[8];
+      unpack8(d[j], f);
+      qr[c] = e4m3_quot8(f, s, rq);
+    }
+  }
+  // the token's assignments t*topk .. t*topk+topk-1, held by lane a % 64 at
+  // step a / 64: their rows, and the scale at each
+#pragma unroll
+  for (int st = 0; st < kWaveSteps; ++st) {
+    const int a = st * 64 + lane;
+    if (st < steps && a < n && a / topk == t) {
+      const int k = kr[st] & 0xfff, r = kr[st] >> 12;
+      const int row = k < E ? cnt[k] + r : -1;
+      dest[a] = row;
+      if (row >= 0) {
+        src_token[row] = t;
+        sx[row] = s;
+      }
+    }
+  }
+}
+
 // out[t] = sum_j w[t, j] * y[dest[t, j]] (dropped slots skipped), fp32 in
 // slot order with separate multiply and add, then bf16 or fp32.
 template <int CPL>
@@ -681,6 +804,29 @@ hipError_t launch_moe_permute_quant(const uint16_t *x, int64_t ldx, int k_dim, i
                                                                              tok_major ? 1 : 0);
     });
   }
+  return hipGetLastError();
+}
+
+hipError_t launch_moe_route_quant(const int32_t *ids, int n, int topk, int E,
+                                  const uint16_t *x, int64_t ldx, int k_dim, int tokens,
+                                  int32_t *offsets, int32_t *dest, int32_t *src_token,
+                                  uint8_t *qx, float *sx, hipStream_t st) {
+  static_assert(moe_route_quant_max_assignments == 64 * kWaveSteps, "one wave ranks them all");
+  if (tokens < 1 || n < 1 || n > moe_route_quant_max_assignments || E < 1 || E > 2047 ||
+      k_dim < 8 || k_dim > 2048 || k_dim % 8 != 0 || ldx % 8 != 0)
+    return hipErrorInvalidValue;
+  const unsigned g = (unsigned)((tokens + 3) / 4);
+  const size_t lds = (size_t)4 * E * sizeof(int);
+  const int per = (k_dim / 8 + 63) / 64;
+  if (per <= 1)
+    moe_route_quant_wave_kernel<1><<<g, 256, lds, st>>>(ids, n, E, topk, x, ldx, k_dim, tokens,
+                                                        offsets, dest, src_token, qx, sx);
+  else if (per <= 2)
+    moe_route_quant_wave_kernel<2><<<g, 256, lds, st>>>(ids, n, E, topk, x, ldx, k_dim, tokens,
+                                                        offsets, dest, src_token, qx, sx);
+  else
+    moe_route_quant_wave_kernel<4><<<g, 256, lds, st>>>(ids, n, E, topk, x, ldx, k_dim, tokens,
+                                                        offsets, dest, src_token, qx, sx);
   return hipGetLastError();
 }
 

@@ -13,7 +13,9 @@ GEMM (groups averaging 48 rows or more, K % 128 == 0) the middle two are
 ``moe_quant_tokens`` (codes in token order, scales per sorted row) and
 ``moe_grouped_fp8_gemm``, which reads each sorted row's A through
 ``route.src_token``: the codes are written once per token instead of topk
-times, with the same result bit for bit.  The reference has no MoE glue; its grouped
+times, with the same result bit for bit.  At decode size
+(``tokens * topk <= 1024``, K <= 2048) ``moe_route_quant_tokens`` routes and
+quantizes in one launch, again with the same tables, codes and scales.  The reference has no MoE glue; its grouped
 GEMM takes rows already sorted by group (cuda/gemm/grouped_gemm.cu:26-32,
 :77-104, triton/gemm/gemm_kernels.py:164-182).  Everything runs in
 ``libdsl_gemm.so``; the sorted order is a stable counting sort, so results
@@ -104,6 +106,50 @@ def moe_quant_tokens(x: torch.Tensor, route: Route):
     return qx, sx
 
 
+# one launch for route + per-token quantize (dsl_moe_route_quant_tokens)
+ROUTE_QUANT_MAX_ASSIGNMENTS = 1024
+
+
+def route_quant_applies(tokens: int, topk: int, num_experts: int, k: int) -> bool:
+    """Whether :func:`moe_route_quant_tokens` takes one launch (decode-size
+    batches); otherwise it runs :func:`moe_route` and :func:`moe_quant_tokens`."""
+    return (1 <= tokens and tokens * topk <= ROUTE_QUANT_MAX_ASSIGNMENTS
+            and num_experts <= 2047 and k <= 2048 and k % 8 == 0)
+
+
+def moe_route_quant_tokens(topk_ids: torch.Tensor, x: torch.Tensor, num_experts: int):
+    """:func:`moe_route` then :func:`moe_quant_tokens`: ``(route, qx, sx)``.
+    For decode-size batches (``tokens * topk <= 1024``, K <= 2048) both run in
+    one launch with the same results bit for bit; other sizes take the two
+    calls."""
+    _gpu(topk_ids, "topk_ids")
+    _gpu(x, "x")
+    if topk_ids.dim() != 2 or x.dim() != 2 or x.shape[0] != topk_ids.shape[0]:
+        raise ValueError("topk_ids [tokens, topk] and x [tokens, K] must match")
+    if x.dtype != torch.bfloat16:
+        raise ValueError("x must be bf16 [tokens, K]")
+    T, k = topk_ids.shape
+    K = x.shape[1]
+    if x.stride(1) != 1 or x.stride(0) % 8 != 0:
+        x = x.contiguous()
+    if not route_quant_applies(T, k, num_experts, K):
+        route = moe_route(topk_ids, num_experts)
+        qx, sx = moe_quant_tokens(x, route)
+        return route, qx, sx
+    ids = topk_ids.to(torch.int32).contiguous()
+    dev = ids.device
+    offsets = torch.empty(num_experts + 1, dtype=torch.int32, device=dev)
+    dest = torch.empty(T * k, dtype=torch.int32, device=dev)
+    src = torch.empty(T * k, dtype=torch.int32, device=dev)
+    qx = torch.empty((T, K), dtype=torch.uint8, device=dev)
+    sx = torch.empty(T * k, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        N.call("dsl_moe_route_quant_tokens", N.ptr(ids), T, k, num_experts, N.ptr(x), K,
+               x.stride(0), N.ptr(offsets), N.ptr(dest), N.ptr(src), N.ptr(qx), N.ptr(sx),
+               N.stream_of(dev))
+    return Route(offsets, dest, src, T, k, num_experts), qx, sx
+
+
 def moe_grouped_fp8_gemm(qx: torch.Tensor, sx: torch.Tensor, route: Route, qw: torch.Tensor,
                          sw: torch.Tensor, *, out_dtype=torch.bfloat16) -> torch.Tensor:
     """The grouped GEMM over the routed rows with A read through the row
@@ -176,12 +222,17 @@ def routed_grouped_gemm(x: torch.Tensor, topk_ids: torch.Tensor, topk_weights: t
         wt = w.transpose(1, 2).reshape(E * Nn, K)       # [E*N, K] K-major rows
         qw, sw = Q.quant_fp8_blocks(wt, 1, K)
         qw, sw = qw.reshape(E, Nn, K), sw.reshape(E, Nn)
-    route = moe_route(topk_ids, E)
-    if gather_applies(route.tokens, route.topk, E, qw.shape[2]):
+    _gpu(topk_ids, "topk_ids")
+    if topk_ids.dim() != 2:
+        raise ValueError("topk_ids must be [tokens, topk]")
+    T, topk = topk_ids.shape
+    if gather_applies(T, topk, E, qw.shape[2]):
         # token-major codes, A rows through the row map: no permuted copy
-        qx, sx = moe_quant_tokens(x, route)
+        # (route and quantize in one launch at decode size)
+        route, qx, sx = moe_route_quant_tokens(topk_ids, x, E)
         y = moe_grouped_fp8_gemm(qx, sx, route, qw, sw, out_dtype=torch.bfloat16)
     else:
+        route = moe_route(topk_ids, E)
         qx, sx = moe_permute_quant(x, route)
         y = G.grouped_fp8_gemm_packed(qx, sx, qw, sw, route.offsets, out_dtype=torch.bfloat16)
     return moe_combine(y, route, topk_weights, out_dtype=out_dtype)

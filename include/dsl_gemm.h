@@ -266,6 +266,19 @@ int dsl_moe_quant_tokens(const void *x, int64_t tokens, int64_t k, int64_t ldx,
                          const int32_t *dest, int64_t topk, int64_t rows,
                          uint8_t *qx, float *sx, void *stream);
 
+/* dsl_moe_route followed by dsl_moe_quant_tokens, in one launch, for
+ * decode-size batches: the same offsets [num_experts + 1], dest and
+ * src_token [tokens * topk], token-major codes qx [tokens][k] and scales sx
+ * at the sorted rows, bit for bit.  tokens * topk <= 1024, num_experts <=
+ * 2047 and k <= 2048 (k % 8 == 0, ldx % 8 == 0); other sizes return
+ * DSL_ERR_UNSUPPORTED and take the two calls.  Needs no workspace.  For
+ * the MoE projection at decode size, where each of the two launches is
+ * mostly latency. */
+int dsl_moe_route_quant_tokens(const int32_t *topk_ids, int64_t tokens, int64_t topk,
+                               int64_t num_experts, const void *x, int64_t k, int64_t ldx,
+                               int32_t *offsets, int32_t *dest, int32_t *src_token, uint8_t *qx,
+                               float *sx, void *stream);
+
 /* dsl_grouped_fp8_gemm whose sorted row r reads x row src_token[r]: x is
  * the token-major [tokens][k] E4M3 of dsl_moe_quant_tokens (8x fewer bytes
  * than the permuted copy at topk = 8), sx the per-sorted-row scales it

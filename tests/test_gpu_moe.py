@@ -164,6 +164,59 @@ def test_quant_tokens_matches_oracle(T, k, E, K, pad):
     assert np.array_equal(np_f32(sx)[:n], s_ref)
 
 
+# Route + per-token quantize in one launch (decode sizes, tokens * topk <=
+# 1024, K <= 2048): every table, code and scale equal to the two launches
+# it replaces and to the oracle.  Dropped ids; one token; 1024 assignments
+# (the most one wave ranks); 2000 experts (the scan in 32 runs of 64);
+# padded rows; K of one 8-element chunk and of four chunks per lane; and
+# sizes past the limits, which take the two calls.
+ROUTE_QUANT_CASES = [(32, 8, 64, 2048, 0, True), (1, 8, 64, 2048, 0, False),
+                     (128, 8, 64, 1024, 8, True), (37, 3, 5, 136, 0, True),
+                     (256, 4, 2000, 512, 16, True), (5, 1, 1, 8, 0, False),
+                     (200, 8, 64, 2048, 0, False), (4, 2, 3, 4096, 0, False)]
+
+
+@pytest.mark.parametrize("T,k,E,K,pad,drop", ROUTE_QUANT_CASES)
+def test_route_quant_tokens_matches_two_launches(T, k, E, K, pad, drop):
+    ids = _ids(T, k, E, 470 + T, drop)
+    x = W.randn_bf16((T, K), 471) * 3
+    xd = x.to(DEV)
+    if pad:
+        xd = torch.nn.functional.pad(xd, (0, pad))[:, :K]
+    fused = M.route_quant_applies(T, k, E, K)
+    assert fused == (T * k <= 1024 and K <= 2048)
+    r, qt, sx = M.moe_route_quant_tokens(ids.to(DEV), xd, E)
+    r2 = M.moe_route(ids.to(DEV), E)
+    qt2, sx2 = M.moe_quant_tokens(xd, r2)
+    off, dest, src = OM.route(ids.numpy(), E)
+    n = int(off[-1])
+    assert np.array_equal(r.offsets.cpu().numpy(), off)
+    assert np.array_equal(r.dest.cpu().numpy(), dest)
+    assert np.array_equal(r.src_token.cpu().numpy()[:n], src)
+    assert torch.equal(r.offsets, r2.offsets) and torch.equal(r.dest, r2.dest)
+    assert torch.equal(r.src_token[:n], r2.src_token[:n])
+    assert torch.equal(qt, qt2)
+    assert torch.equal(sx[:n], sx2[:n])
+    q_ref, s_ref = OM.permute_quant(x.float().numpy(), src)
+    assert np.array_equal(np_u8(qt)[src], q_ref)
+    assert np.array_equal(np_f32(sx)[:n], s_ref)
+
+
+def test_route_quant_tokens_unsupported_sizes_report():
+    from dsl_tool_amd import _native as N
+    ids = torch.zeros((300, 4), dtype=torch.int32, device=DEV)
+    x = torch.zeros((300, 256), dtype=torch.bfloat16, device=DEV)
+    off = torch.empty(9, dtype=torch.int32, device=DEV)
+    dest = torch.empty(1200, dtype=torch.int32, device=DEV)
+    src = torch.empty(1200, dtype=torch.int32, device=DEV)
+    qx = torch.empty((300, 256), dtype=torch.uint8, device=DEV)
+    sx = torch.empty(1200, dtype=torch.float32, device=DEV)
+    rc = N.lib().dsl_moe_route_quant_tokens(ids.data_ptr(), 300, 4, 8, x.data_ptr(), 256, 256,
+                                            off.data_ptr(), dest.data_ptr(), src.data_ptr(),
+                                            qx.data_ptr(), sx.data_ptr(), N.stream_of(x.device))
+    assert rc == N.DSL_ERR_UNSUPPORTED
+
+
 def _expert_weights(E, Nn, K, seed):
     from dsl_tool_amd import quant as Q
     w = W.randn_bf16((E * Nn, K), seed, 0.02).to(DEV)
