@@ -145,20 +145,36 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     // the next stage's copies go out after this stage's first fragment
     // reads, so that those are not queued behind the copy burst
     if (ks + NS - 1 < nks) ring.issue(ks + NS - 1, lds0);
+    // Rows are software-pipelined: row i's MFMAs are issued before row
+    // i-1's partials are scaled into the accumulator, so the matrix pipe
+    // works while the VALU folds (issuing each fold right after its own
+    // MFMA left the wave waiting on that MFMA's result).
+    const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    v4f part[2][TN];
+    v4f s4q[2];
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int arow = wm * Cfg::WM + i * 16;
-      const v8i af = afn;
-      if (i + 1 < TM) afn = ld(sA, arow + 16 + r16);
-      const v4f s4 = *reinterpret_cast<const v4f *>(sSa + arow + 4 * g) * sbv;
-      const v4f zero = {0.f, 0.f, 0.f, 0.f};
+    for (int i = 0; i <= TM; ++i) {
+      if (i < TM) {
+        const int arow = wm * Cfg::WM + i * 16;
+        const v8i af = afn;
+        if (i + 1 < TM) afn = ld(sA, arow + 16 + r16);
+        s4q[i & 1] = *reinterpret_cast<const v4f *>(sSa + arow + 4 * g) * sbv;
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const v4f part = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], zero, 0, 0, 0,
-                                                                          0, 0, 0);
-        if constexpr (Cfg::GCOL) acc[i][j] = part * (s4 * sbc[j]) + acc[i][j];
-        else acc[i][j] = part * s4 + acc[i][j];
+        for (int j = 0; j < TN; ++j)
+          part[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], zero, 0, 0,
+                                                                            0, 0, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      if (i > 0) {
+        const int ip = i - 1;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if constexpr (Cfg::GCOL)
+            acc[ip][j] = part[ip & 1][j] * (s4q[ip & 1] * sbc[j]) + acc[ip][j];
+          else acc[ip][j] = part[ip & 1][j] * s4q[ip & 1] + acc[ip][j];
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
 
