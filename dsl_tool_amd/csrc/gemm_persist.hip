@@ -119,6 +119,13 @@ struct TileRef {
 
 namespace pers {
 
+// Pair-slot row swizzle: chunk c of row r lives in slot c ^ pair_swz(r).
+// Its readers (32x32 fragments: lane = row, chunks 4p + 2h and 4p + 2h + 1,
+// or 4h + 2p + kk for MXFP4) are conflict-free with it on gfx950.  It is
+// linear in the row bits and uses only bits 1-3, so the copy plan forms
+// pair_swz(wrow + j*RPI + vsub) as pair_swz(wrow + vsub) ^ pair_swz(j*RPI).
+DSL_DEV int pair_swz(int row) { return (row >> 1) & 7; }
+
 // Direct-to-LDS loads in the saddr form: a wave-uniform 64-bit base (SGPRs)
 // plus a 32-bit per-lane offset (one VGPR).
 DSL_DEV void dma16(const uint8_t *base, uint32_t voff, uint32_t lds) {
@@ -205,7 +212,7 @@ struct Ring {
     vsub = lane / Cfg::CH;
     // DMA j covers tile rows wrow + j*RPI + vsub; RPI is even, so the row
     // swizzle only depends on vsub and the parity of wrow/RPI + j
-    vchunk = (uint32_t)(((lane % Cfg::CH) ^ pipe::swz<Cfg::PKB>(wrow + (int)vsub)) * 16);
+    vchunk = (uint32_t)(((lane % Cfg::CH) ^ pair_swz(wrow + (int)vsub)) * 16);
     sbase = tr.a;
     soff = 0;
   }
@@ -243,7 +250,7 @@ struct Ring {
     r = r < lim ? r : lim;           // rows past the edge re-read the last row
     // swz(wrow + j*RPI + vsub) = swz(wrow + vsub) ^ swz(j*RPI): the row
     // offset j*RPI only flips bit 2 of the swizzle, by the parity of j
-    const uint32_t ch = vchunk ^ (uint32_t)(pipe::swz<Cfg::PKB>(j * Cfg::RPI) * 16);
+    const uint32_t ch = vchunk ^ (uint32_t)(pair_swz(j * Cfg::RPI) * 16);
     // r < 256 and Kb < 2^24 (checked at launch): a full-rate 24-bit multiply
     if constexpr (Cfg::BF16) {
       // pairs from nk1 on come from the second segment (selects, no branch)
@@ -318,7 +325,7 @@ template <class Cfg, int KIND = Cfg::MX ? 1 : (Cfg::NV ? 2 : 0)>
 struct Frag {
   v8i a[Cfg::TM], b[Cfg::TN];
   static DSL_DEV v8i ld(const uint8_t *base, int row, int p, int h) {
-    const int s = pipe::swz<Cfg::PKB>(row), c0 = 4 * p + 2 * h;
+    const int s = pair_swz(row), c0 = 4 * p + 2 * h;
     const v4i lo = *reinterpret_cast<const v4i *>(base + row * Cfg::PKB + ((c0 ^ s) << 4));
     const v4i hi = *reinterpret_cast<const v4i *>(base + row * Cfg::PKB + (((c0 + 1) ^ s) << 4));
     return (v8i){lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
@@ -339,7 +346,7 @@ struct Frag<Cfg, 1> {
   v4i a[Cfg::TM][2], b[Cfg::TN][2];
   int as[Cfg::TM], bs[Cfg::TN];     // scale word h of the row's pair
   static DSL_DEV v4i ld(const uint8_t *base, int row, int c) {
-    return *reinterpret_cast<const v4i *>(base + row * Cfg::PKB + ((c ^ pipe::swz<Cfg::PKB>(row)) << 4));
+    return *reinterpret_cast<const v4i *>(base + row * Cfg::PKB + ((c ^ pair_swz(row)) << 4));
   }
   // sq: quad slot; qw: first scale word of the pair in the row's 16 bytes
   // (2 x quad-local pair index).  The scale word is read with half 0.
