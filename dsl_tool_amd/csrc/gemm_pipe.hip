@@ -108,9 +108,22 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
   sbrow = sbrow > sblim ? sblim : sbrow;
   const float *sbp = static_cast<const float *>(p.sb) + (int64_t)sbrow * nkg;
 
+  // Eight waves (two per SIMD; waves w and w + 4 share one): a wave cannot
+  // issue its MFMAs until its nine copies have gone out, and copies issue at
+  // the L2-to-LDS rate (~16 cycles per 1 KB instruction per CU), so when both
+  // waves of a SIMD issue theirs together after the barrier the matrix pipe
+  // idles.  Waves 4-7 therefore issue after their first row of MFMAs, and
+  // the ring advances its source pointers in place, which leaves no address
+  // temporaries live there.
+  constexpr bool STAGGER = Cfg::NW == 8;
+  const bool late = STAGGER && wave >= 4;
+  auto issue_stage = [&](int s) __attribute__((always_inline)) {
+    if constexpr (STAGGER) ring.issue_next(s, lds0);
+    else ring.issue(s, lds0);
+  };
 #pragma unroll
   for (int s = 0; s < NS - 1; ++s)
-    if (s < nks) ring.issue(s, lds0);
+    if (s < nks) issue_stage(s);
 
   v4f acc[TM][TN];
 #pragma unroll
@@ -144,7 +157,7 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     v8i afn = ld(sA, wm * Cfg::WM + r16);
     // the next stage's copies go out after this stage's first fragment
     // reads, so that those are not queued behind the copy burst
-    if (ks + NS - 1 < nks) ring.issue(ks + NS - 1, lds0);
+    if (!late && ks + NS - 1 < nks) issue_stage(ks + NS - 1);
     // Rows are software-pipelined: row i's MFMAs are issued before row
     // i-1's partials are scaled into the accumulator, so the matrix pipe
     // works while the VALU folds (issuing each fold right after its own
@@ -164,6 +177,8 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
           part[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], zero, 0, 0,
                                                                             0, 0, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      if (i == 0 && late && ks + NS - 1 < nks) issue_stage(ks + NS - 1);
       __builtin_amdgcn_sched_barrier(0);
       if (i > 0) {
         const int ip = i - 1;

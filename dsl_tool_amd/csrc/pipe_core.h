@@ -231,6 +231,23 @@ struct Ring {
     if (j < Cfg::DD) dma16(src[j] + (int64_t)ks * step[j], base + dst[j]);
     else if (has[j]) dma4(src[j] + (int64_t)(ks >> Cfg::SC_SHIFT) * step[j], base + dst[j]);
   }
+  // The same copies for a caller that issues stages strictly in order: the
+  // source pointers advance in place, so no 64-bit `src + ks*step`
+  // temporaries are live where the copies are issued (between MFMA rows).
+  DSL_DEV void issue_next(int ks, uint32_t lds0) {
+    static_assert(Cfg::SC_SHIFT == 0, "one scale step per stage");
+    const uint32_t base = lds0 + (uint32_t)((ks % Cfg::NS) * Cfg::STAGE);
+#pragma unroll
+    for (int j = 0; j < Cfg::D; ++j) {
+      if (j < Cfg::DD) {
+        dma16(src[j], base + dst[j]);
+        src[j] += step[j];
+      } else if (has[j]) {
+        dma4(src[j], base + dst[j]);
+        src[j] += step[j];
+      }
+    }
+  }
   DSL_DEV void issue(int ks, uint32_t lds0) const {
 #pragma unroll
     for (int j = 0; j < Cfg::D; ++j) issue_one(j, ks, lds0);
