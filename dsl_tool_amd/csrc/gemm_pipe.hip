@@ -76,12 +76,15 @@ void gemm_pipe_kernel(const GemmArgs p) {
 // Block-scaled FP8 (1x128 activation groups, 128x128 weight blocks): one
 // 16x16x128 MFMA per output tile per stage yields the group's partial sum,
 // folded at once into the fp32 accumulator as acc += part * sa[m,g] * sb[n/128,g]
-// (the group-partial form of cuda/gemm/fp8_gemm.cu:84-97).  Activation
+// (the group-partial form of cuda/gemm/fp8_gemm.cu:84-97).  The W fragment
+// is the MFMA's first operand, so a lane holds one output row (m = lane % 16)
+// and four consecutive columns (4 * (lane / 16) ..): one row scale per lane,
+// and four adjacent bf16 results that leave as one 8-byte write.  Activation
 // scales travel with the stage; the weight scale of the wave's 128-column
 // block is one scalar load per stage.  With per-column weight scales
 // (MODE_FP8_GCOL, sb[g][n] as fp8_gemm_groupwise_kernel reads them) the
 // stage also carries the tile's BN weight scales of its group, and each
-// lane folds part * (sa[m,g] * sb[g,n]) for its own column.
+// lane folds part * (sa[m,g] * sb[g,n]) for its own four columns.
 template <class Cfg>
 __global__ __launch_bounds__(Cfg::NT) __attribute__((amdgpu_waves_per_eu(Cfg::OCC, Cfg::OCC)))
 void gemm_pipe_block_kernel(const GemmArgs p) {
@@ -139,10 +142,11 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     const uint8_t *st = smem + (ks % NS) * Cfg::STAGE;
     const uint8_t *sA = st, *sB = st + Cfg::A_BYTES;
     const float *sSa = reinterpret_cast<const float *>(st + Cfg::A_BYTES + Cfg::B_BYTES);
-    float sbc[TN];                       // GCOL: the lane's column scale per 16-column tile
+    v4f sbc[TN];                         // GCOL: the lane's four column scales per 16-column tile
     if constexpr (Cfg::GCOL) {
 #pragma unroll
-      for (int t = 0; t < TN; ++t) sbc[t] = sSa[Cfg::BM + wn * Cfg::WN + t * 16 + r16];
+      for (int t = 0; t < TN; ++t)
+        sbc[t] = *reinterpret_cast<const v4f *>(sSa + Cfg::BM + wn * Cfg::WN + t * 16 + 4 * g);
     }
     auto ld = [&](const uint8_t *base, int row) {
       const int s = pipe::swz<SKB>(row);
@@ -164,17 +168,17 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
     // MFMA left the wave waiting on that MFMA's result).
     const v4f zero = {0.f, 0.f, 0.f, 0.f};
     v4f part[2][TN];
-    v4f s4q[2];
+    float srq[2];                        // the lane's row scale (times sb for 128x128 blocks)
 #pragma unroll
     for (int i = 0; i <= TM; ++i) {
       if (i < TM) {
         const int arow = wm * Cfg::WM + i * 16;
         const v8i af = afn;
         if (i + 1 < TM) afn = ld(sA, arow + 16 + r16);
-        s4q[i & 1] = *reinterpret_cast<const v4f *>(sSa + arow + 4 * g) * sbv;
+        srq[i & 1] = sSa[arow + r16] * sbv;
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          part[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(af, bf[j], zero, 0, 0,
+          part[i & 1][j] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(bf[j], af, zero, 0, 0,
                                                                             0, 0, 0, 0);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -185,8 +189,8 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
 #pragma unroll
         for (int j = 0; j < TN; ++j) {
           if constexpr (Cfg::GCOL)
-            acc[ip][j] = part[ip & 1][j] * (s4q[ip & 1] * sbc[j]) + acc[ip][j];
-          else acc[ip][j] = part[ip & 1][j] * s4q[ip & 1] + acc[ip][j];
+            acc[ip][j] = part[ip & 1][j] * (sbc[j] * srq[ip & 1]) + acc[ip][j];
+          else acc[ip][j] = part[ip & 1][j] * srq[ip & 1] + acc[ip][j];
         }
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -201,32 +205,31 @@ void gemm_pipe_block_kernel(const GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = wm * Cfg::WM + i * 16 + 4 * g + r;
-            const int col = wn * Cfg::WN + j * 16 + r16;
-            stg[Out::off(row, col)] = f32_to_bf16(acc[i][j][r]);
-          }
+        for (int j = 0; j < TN; ++j) {
+          const int row = wm * Cfg::WM + i * 16 + r16;
+          const int col = wn * Cfg::WN + j * 16 + 4 * g;   // four columns, 8-byte aligned
+          *reinterpret_cast<uint2 *>(stg + Out::off(row, col)) =
+              make_uint2(pack_bf16x2(acc[i][j][0], acc[i][j][1]), pack_bf16x2(acc[i][j][2], acc[i][j][3]));
+        }
       __syncthreads();
       Out::template store<Cfg::NT>(p, m0, n0, stg);
       return;
     }
   }
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+  for (int i = 0; i < TM; ++i) {
+    const int row = m0 + wm * Cfg::WM + i * 16 + r16;
+    if (row >= p.M) continue;
 #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int col = n0 + wn * Cfg::WN + j * 16 + r16;
-      if (col >= p.N) continue;
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = m0 + wm * Cfg::WM + i * 16 + 4 * g + r;
-        if (row >= p.M) continue;
+        const int col = n0 + wn * Cfg::WN + j * 16 + 4 * g + r;
+        if (col >= p.N) continue;
         if (p.out_f32) static_cast<float *>(p.c)[(int64_t)row * p.ldc + col] = acc[i][j][r];
         else static_cast<uint16_t *>(p.c)[(int64_t)row * p.ldc + col] = f32_to_bf16(acc[i][j][r]);
       }
-    }
+  }
 }
 
 // Block-scaled FP8 (1x128 activation groups, 128x128 weight blocks) on the
