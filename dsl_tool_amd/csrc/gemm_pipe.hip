@@ -7,7 +7,12 @@
 
 namespace dsl {
 
-template <class Cfg>
+// TR (chosen by the launcher for bf16 output staged in LDS): the W tile is
+// the MFMAs' first operand, so a lane holds one output row and, per group of
+// four registers, four adjacent columns; the epilogue packs those into one
+// 8-byte staging write (instead of four 2-byte writes).  The fp32 output
+// keeps the other layout, whose column-contiguous direct stores coalesce.
+template <class Cfg, bool TR>
 __global__ __launch_bounds__(Cfg::NT) __attribute__((amdgpu_waves_per_eu(Cfg::OCC, Cfg::OCC)))
 void gemm_pipe_kernel(const GemmArgs p) {
   __shared__ __align__(16) uint8_t smem[Cfg::LDS];
@@ -20,7 +25,7 @@ void gemm_pipe_kernel(const GemmArgs p) {
   const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
   const int r32 = lane & 31, h = lane >> 5;
   v16f acc[Cfg::TM][Cfg::TN];
-  pipe_mainloop<Cfg>(p, m0, n0, smem, wave, lane, acc);
+  pipe_mainloop<Cfg, TR>(p, m0, n0, smem, wave, lane, acc);
 
   float s1 = 1.f, s2 = 1.f;
   constexpr bool GLOBAL = Cfg::MODE == MODE_FP8_TENSOR || Cfg::MODE == MODE_NVFP4;
@@ -29,6 +34,33 @@ void gemm_pipe_kernel(const GemmArgs p) {
     s2 = *p.gb;
   }
   using Out = pipe::OutStage<Cfg::BM, Cfg::BN>;
+  if constexpr (TR) {
+    static_assert(Cfg::BM * Cfg::BN * 2 <= Cfg::LDS, "TR stages the bf16 tile in LDS");
+    // lane: row 32i + l%32 of the wave's tile; registers 4q..4q+3: columns
+    // 32j + 8q + 4h .. +3
+    uint16_t *stg = reinterpret_cast<uint16_t *>(smem);
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+      for (int j = 0; j < Cfg::TN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int row = wm * Cfg::WM + i * 32 + r32;
+          const int col = wn * Cfg::WN + j * 32 + 8 * q + 4 * h;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = acc[i][j][4 * q + e];
+            if constexpr (GLOBAL) v[e] = (v[e] * s1) * s2;
+          }
+          *reinterpret_cast<uint2 *>(stg + Out::off(row, col)) =
+              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+        }
+    __syncthreads();
+    Out::template store<Cfg::NT>(p, m0, n0, stg);
+    return;
+  }
   if constexpr (Cfg::BM * Cfg::BN * 2 <= Cfg::LDS) {
     if (!p.out_f32) {
       // bf16: stage the tile in the idle ring, then write whole rows
@@ -484,7 +516,12 @@ static hipError_t launch_pipe_cfg(const GemmArgs &p, hipStream_t st) {
   const int tiles = ((p.M + Cfg::BM - 1) / Cfg::BM) * ((p.N + Cfg::BN - 1) / Cfg::BN);
   if constexpr (Cfg::BLOCK && Cfg::PF) gemm_pipe_block_pf_kernel<Cfg><<<tiles, Cfg::NT, 0, st>>>(p);
   else if constexpr (Cfg::BLOCK) gemm_pipe_block_kernel<Cfg><<<tiles, Cfg::NT, 0, st>>>(p);
-  else gemm_pipe_kernel<Cfg><<<tiles, Cfg::NT, 0, st>>>(p);
+  else if constexpr (Cfg::BM * Cfg::BN * 2 <= Cfg::LDS) {
+    if (!p.out_f32) gemm_pipe_kernel<Cfg, true><<<tiles, Cfg::NT, 0, st>>>(p);
+    else gemm_pipe_kernel<Cfg, false><<<tiles, Cfg::NT, 0, st>>>(p);
+  } else {
+    gemm_pipe_kernel<Cfg, false><<<tiles, Cfg::NT, 0, st>>>(p);
+  }
   return hipGetLastError();
 }
 

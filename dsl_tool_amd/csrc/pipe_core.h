@@ -336,7 +336,13 @@ struct KFrag<Cfg, false> {
     c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(x0, y0, c, 0, 0, 0);
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(x1, y1, c, 0, 0, 0);
   }
+  // TR: operands swapped, see mma_row_t
+  template <bool TR = false>
   DSL_DEV void mma_row(int, int i, v16f (&acc)[Cfg::TM][Cfg::TN]) const {
+    if constexpr (TR) {
+      mma_row_t(i, acc);
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < Cfg::TN; ++j) {
       if constexpr (Cfg::BF16)
@@ -359,9 +365,10 @@ struct KFrag<Cfg, false> {
                                                                     0, 0, 0, 0);
     }
   }
+  template <bool TR = false>
   DSL_DEV void mma(int k, v16f (&acc)[Cfg::TM][Cfg::TN]) const {
 #pragma unroll
-    for (int i = 0; i < Cfg::TM; ++i) mma_row(k, i, acc);
+    for (int i = 0; i < Cfg::TM; ++i) mma_row<TR>(k, i, acc);
   }
 };
 
@@ -397,15 +404,23 @@ struct KFrag<Cfg, true> {
 #pragma unroll
     for (int t = 0; t < Cfg::TM; ++t) load_a(st, k, t, wm, r32, h);
   }
+  // TR: W tile (and its scales) in the first operand slot, acc holds C^T
+  template <bool TR = false>
   DSL_DEV void mma_row(int k, int i, v16f (&acc)[Cfg::TM][Cfg::TN]) const {
 #pragma unroll
-    for (int j = 0; j < Cfg::TN; ++j)
-      acc[i][j] = (k & 1) ? pipe::mfma_fp4<1>(a[i], b[j], acc[i][j], as[i], bs[j])
-                          : pipe::mfma_fp4<0>(a[i], b[j], acc[i][j], as[i], bs[j]);
+    for (int j = 0; j < Cfg::TN; ++j) {
+      if constexpr (TR)
+        acc[i][j] = (k & 1) ? pipe::mfma_fp4<1>(b[j], a[i], acc[i][j], bs[j], as[i])
+                            : pipe::mfma_fp4<0>(b[j], a[i], acc[i][j], bs[j], as[i]);
+      else
+        acc[i][j] = (k & 1) ? pipe::mfma_fp4<1>(a[i], b[j], acc[i][j], as[i], bs[j])
+                            : pipe::mfma_fp4<0>(a[i], b[j], acc[i][j], as[i], bs[j]);
+    }
   }
+  template <bool TR = false>
   DSL_DEV void mma(int k, v16f (&acc)[Cfg::TM][Cfg::TN]) const {
 #pragma unroll
-    for (int i = 0; i < Cfg::TM; ++i) mma_row(k, i, acc);
+    for (int i = 0; i < Cfg::TM; ++i) mma_row<TR>(k, i, acc);
   }
 };
 
@@ -419,7 +434,7 @@ struct KFrag<Cfg, true> {
 // u32 after the data tiles, word k holds the quad's four E4M3 bytes.  (A
 // free function with local arrays: as struct members the scale arrays were
 // left in private memory by the compiler.)
-template <class Cfg>
+template <class Cfg, bool TR = false>
 DSL_DEV void nv_kstep(const uint8_t *st, int k, int wm, int wn, int r32, int h,
                       v16f (&acc)[Cfg::TM][Cfg::TN]) {
   constexpr int SKB = Cfg::SKB;
@@ -455,7 +470,8 @@ DSL_DEV void nv_kstep(const uint8_t *st, int k, int wm, int wn, int r32, int h,
     for (int x = 0; x < Cfg::TM; ++x)
 #pragma unroll
       for (int y = 0; y < Cfg::TN; ++y)
-        acc[x][y] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[x], bf[y], acc[x][y], 0, 0, 0);
+        acc[x][y] = TR ? __builtin_amdgcn_mfma_f32_32x32x16_f16(bf[y], af[x], acc[x][y], 0, 0, 0)
+                       : __builtin_amdgcn_mfma_f32_32x32x16_f16(af[x], bf[y], acc[x][y], 0, 0, 0);
   }
 }
 
@@ -467,9 +483,10 @@ struct StageFrag {
 #pragma unroll
     for (int k = 0; k < Cfg::KSTEPS; ++k) f[k].load(st, k, wm, wn, r32, h);
   }
+  template <bool TR = false>
   DSL_DEV void mma(v16f (&acc)[Cfg::TM][Cfg::TN]) const {
 #pragma unroll
-    for (int k = 0; k < Cfg::KSTEPS; ++k) f[k].mma(k, acc);
+    for (int k = 0; k < Cfg::KSTEPS; ++k) f[k].template mma<TR>(k, acc);
   }
   // MFMAs of this stage, with the next stage's fragments read into `nxt`
   // as this stage's registers free up: next B first (its own registers),
@@ -477,6 +494,7 @@ struct StageFrag {
   // When `issue` is set, the DMA instructions of stage `ks_issue` are spread
   // over the MFMA rows, so that the MFMA pipe is already busy while the
   // vector-memory queue accepts them.
+  template <bool TR = false>
   DSL_DEV void mma_prefetch(v16f (&acc)[Cfg::TM][Cfg::TN], StageFrag &nxt, const uint8_t *st_next,
                             int wm, int wn, int r32, int h, const pipe::Ring<Cfg> &ring,
                             bool issue, int ks_issue, uint32_t lds0) const {
@@ -489,7 +507,7 @@ struct StageFrag {
 #pragma unroll
       for (int i = 0; i < Cfg::TM; ++i) {
         const int t = k * Cfg::TM + i;
-        f[k].mma_row(k, i, acc);
+        f[k].template mma_row<TR>(k, i, acc);
         if (issue) {
 #pragma unroll
           for (int j = t * D / R; j < (t + 1) * D / R; ++j) ring.issue_one(j, ks_issue, lds0);
@@ -535,7 +553,7 @@ DSL_DEV void wait_lds() { __builtin_amdgcn_s_waitcnt((15 << 0) | (7 << 4) | (0 <
 // next stage is issued and NS-2 stages follow stage ks+1); without it the
 // step checks at run time.  The steady form has no branch between the MFMA
 // rows, which keeps the compiler from sinking work across them.
-template <class Cfg, bool STEADY>
+template <class Cfg, bool STEADY, bool TR = false>
 DSL_DEV void pf_step(int ks, int nks, const pipe::Ring<Cfg> &ring, uint32_t lds0,
                      const uint8_t *smem, const StageFrag<Cfg> &cur, StageFrag<Cfg> &nxt, int wm,
                      int wn, int r32, int h, v16f (&acc)[Cfg::TM][Cfg::TN]) {
@@ -550,7 +568,7 @@ DSL_DEV void pf_step(int ks, int nks, const pipe::Ring<Cfg> &ring, uint32_t lds0
   }
   pipe::wait_lds();
   __syncthreads();
-  cur.mma_prefetch(acc, nxt, smem + ((ks + 1) % NS) * Cfg::STAGE, wm, wn, r32, h, ring,
+  cur.template mma_prefetch<TR>(acc, nxt, smem + ((ks + 1) % NS) * Cfg::STAGE, wm, wn, r32, h, ring,
                    STEADY || ks + NS < nks, ks + NS, lds0);
 }
 
@@ -572,7 +590,7 @@ DSL_DEV void pf_step(int ks, int nks, const pipe::Ring<Cfg> &ring, uint32_t lds0
 //     ks+NS, issues the LDS reads of stage ks+1 and then the MFMAs of stage
 //     ks, so the LDS latency hides behind the MFMAs and NS-1 stages are in
 //     flight.  Requires an even stage count Kb / SKB >= 2.
-template <class Cfg>
+template <class Cfg, bool TR = false>
 DSL_DEV void pipe_mainloop(const GemmArgs &p, int m0, int n0, uint8_t *smem, int wave, int lane,
                            v16f (&acc)[Cfg::TM][Cfg::TN]) {
   constexpr int NS = Cfg::NS, D = Cfg::D;
@@ -606,11 +624,11 @@ DSL_DEV void pipe_mainloop(const GemmArgs &p, int m0, int n0, uint8_t *smem, int
 #pragma unroll
       for (int k = 0; k < Cfg::KSTEPS; ++k) {
         if constexpr (Cfg::NV) {
-          nv_kstep<Cfg>(st, k, wm, wn, r32, h, acc);
+          nv_kstep<Cfg, TR>(st, k, wm, wn, r32, h, acc);
         } else {
           KFrag<Cfg> f;
           f.load(st, k, wm, wn, r32, h);
-          f.mma(k, acc);
+          f.template mma<TR>(k, acc);
         }
       }
     }
@@ -629,15 +647,15 @@ DSL_DEV void pipe_mainloop(const GemmArgs &p, int m0, int n0, uint8_t *smem, int
     // (nks is even and >= 2: a precondition of this schedule)
     int ks = 0;
     for (; ks + NS + 1 < nks; ks += 2) {
-      pf_step<Cfg, true>(ks, nks, ring, lds0, smem, f0, f1, wm, wn, r32, h, acc);
-      pf_step<Cfg, true>(ks + 1, nks, ring, lds0, smem, f1, f0, wm, wn, r32, h, acc);
+      pf_step<Cfg, true, TR>(ks, nks, ring, lds0, smem, f0, f1, wm, wn, r32, h, acc);
+      pf_step<Cfg, true, TR>(ks + 1, nks, ring, lds0, smem, f1, f0, wm, wn, r32, h, acc);
     }
     for (; ks + 2 < nks; ks += 2) {
-      pf_step<Cfg, false>(ks, nks, ring, lds0, smem, f0, f1, wm, wn, r32, h, acc);
-      pf_step<Cfg, false>(ks + 1, nks, ring, lds0, smem, f1, f0, wm, wn, r32, h, acc);
+      pf_step<Cfg, false, TR>(ks, nks, ring, lds0, smem, f0, f1, wm, wn, r32, h, acc);
+      pf_step<Cfg, false, TR>(ks + 1, nks, ring, lds0, smem, f1, f0, wm, wn, r32, h, acc);
     }
-    pf_step<Cfg, false>(ks, nks, ring, lds0, smem, f0, f1, wm, wn, r32, h, acc);
-    f1.mma(acc);
+    pf_step<Cfg, false, TR>(ks, nks, ring, lds0, smem, f0, f1, wm, wn, r32, h, acc);
+    f1.template mma<TR>(acc);
   }
 }
 
