@@ -7,11 +7,13 @@
 
 namespace dsl {
 
-// TR (chosen by the launcher for bf16 output staged in LDS): the W tile is
-// the MFMAs' first operand, so a lane holds one output row and, per group of
-// four registers, four adjacent columns; the epilogue packs those into one
-// 8-byte staging write (instead of four 2-byte writes).  The fp32 output
-// keeps the other layout, whose column-contiguous direct stores coalesce.
+// TR (chosen by the launcher wherever the output tile can be staged in the
+// idle ring): the W tile is the MFMAs' first operand, so a lane holds one
+// output row and, per group of four registers, four adjacent columns; the
+// epilogue writes those as one packed 8-byte bf16 (or one 16-byte fp32)
+// staging store instead of four scattered ones.  Without staging room the
+// fp32 output keeps the other layout, whose column-contiguous direct stores
+// coalesce.
 template <class Cfg, bool TR>
 __global__ __launch_bounds__(Cfg::NT) __attribute__((amdgpu_waves_per_eu(Cfg::OCC, Cfg::OCC)))
 void gemm_pipe_kernel(const GemmArgs p) {
@@ -38,6 +40,49 @@ void gemm_pipe_kernel(const GemmArgs p) {
     static_assert(Cfg::BM * Cfg::BN * 2 <= Cfg::LDS, "TR stages the bf16 tile in LDS");
     // lane: row 32i + l%32 of the wave's tile; registers 4q..4q+3: columns
     // 32j + 8q + 4h .. +3
+    auto val = [&](int i, int j, int r) __attribute__((always_inline)) {
+      float v = acc[i][j][r];
+      if constexpr (GLOBAL) v = (v * s1) * s2;
+      return v;
+    };
+    if (p.out_f32) {
+      if constexpr (Cfg::BM * Cfg::BN * 4 <= Cfg::LDS) {
+        using OutF = pipe::OutStageF32<Cfg::BM, Cfg::BN>;
+        float *stg = reinterpret_cast<float *>(smem);
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < Cfg::TM; ++i)
+#pragma unroll
+          for (int j = 0; j < Cfg::TN; ++j)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const int row = wm * Cfg::WM + i * 32 + r32;
+              const int col = wn * Cfg::WN + j * 32 + 8 * q + 4 * h;
+              *reinterpret_cast<float4 *>(stg + OutF::off(row, col)) =
+                  make_float4(val(i, j, 4 * q), val(i, j, 4 * q + 1), val(i, j, 4 * q + 2),
+                              val(i, j, 4 * q + 3));
+            }
+        __syncthreads();
+        OutF::template store<Cfg::NT>(p, m0, n0, stg);
+      } else {
+        // no staging room (the launcher does not pick TR then): direct stores
+#pragma unroll
+        for (int i = 0; i < Cfg::TM; ++i) {
+          const int row = m0 + wm * Cfg::WM + i * 32 + r32;
+          if (row >= p.M) continue;
+#pragma unroll
+          for (int j = 0; j < Cfg::TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int col = n0 + wn * Cfg::WN + j * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+              if (col >= p.N) continue;
+              float *d = static_cast<float *>(p.c) + (int64_t)row * p.ldc + col;
+              *d = p.accumulate ? *d + val(i, j, r) : val(i, j, r);
+            }
+        }
+      }
+      return;
+    }
     uint16_t *stg = reinterpret_cast<uint16_t *>(smem);
     __syncthreads();
 #pragma unroll
@@ -48,14 +93,9 @@ void gemm_pipe_kernel(const GemmArgs p) {
         for (int q = 0; q < 4; ++q) {
           const int row = wm * Cfg::WM + i * 32 + r32;
           const int col = wn * Cfg::WN + j * 32 + 8 * q + 4 * h;
-          float v[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            v[e] = acc[i][j][4 * q + e];
-            if constexpr (GLOBAL) v[e] = (v[e] * s1) * s2;
-          }
           *reinterpret_cast<uint2 *>(stg + Out::off(row, col)) =
-              make_uint2(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]));
+              make_uint2(pack_bf16x2(val(i, j, 4 * q), val(i, j, 4 * q + 1)),
+                         pack_bf16x2(val(i, j, 4 * q + 2), val(i, j, 4 * q + 3)));
         }
     __syncthreads();
     Out::template store<Cfg::NT>(p, m0, n0, stg);
@@ -517,7 +557,8 @@ static hipError_t launch_pipe_cfg(const GemmArgs &p, hipStream_t st) {
   if constexpr (Cfg::BLOCK && Cfg::PF) gemm_pipe_block_pf_kernel<Cfg><<<tiles, Cfg::NT, 0, st>>>(p);
   else if constexpr (Cfg::BLOCK) gemm_pipe_block_kernel<Cfg><<<tiles, Cfg::NT, 0, st>>>(p);
   else if constexpr (Cfg::BM * Cfg::BN * 2 <= Cfg::LDS) {
-    if (!p.out_f32) gemm_pipe_kernel<Cfg, true><<<tiles, Cfg::NT, 0, st>>>(p);
+    const bool staged = !p.out_f32 || Cfg::BM * Cfg::BN * 4 <= Cfg::LDS;
+    if (staged) gemm_pipe_kernel<Cfg, true><<<tiles, Cfg::NT, 0, st>>>(p);
     else gemm_pipe_kernel<Cfg, false><<<tiles, Cfg::NT, 0, st>>>(p);
   } else {
     gemm_pipe_kernel<Cfg, false><<<tiles, Cfg::NT, 0, st>>>(p);

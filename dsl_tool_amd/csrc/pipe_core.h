@@ -294,6 +294,48 @@ struct OutStage {
   }
 };
 
+// fp32 output staging (the same idea at 4 bytes per element): a BM x BN fp32
+// tile in LDS, 16-byte chunk c of row r at chunk c ^ (r % CPR), leaving in
+// 16-byte stores; with p.accumulate the store adds to C (one writer per
+// element).
+template <int BM, int BN>
+struct OutStageF32 {
+  static constexpr int CPR = BN / 4;
+  static_assert(CPR >= 8 && (CPR & (CPR - 1)) == 0, "power-of-two chunks per staged row");
+  static DSL_DEV int off(int row, int col) {
+    return row * BN + ((((col >> 2) ^ (row & (CPR - 1))) << 2) | (col & 3));
+  }
+  template <int NT>
+  static DSL_DEV void store(const GemmArgs &p, int m0, int n0, const float *stg) {
+    const bool vec = (p.ldc % 4) == 0 && (reinterpret_cast<uintptr_t>(p.c) & 15) == 0;
+    static_assert((BM * CPR) % NT == 0, "whole passes");
+#pragma unroll
+    for (int it = 0; it < BM * CPR / NT; ++it) {
+      const int idx = it * NT + (int)threadIdx.x;
+      const int row = idx / CPR, ch = idx % CPR;
+      const int grow = m0 + row, gcol = n0 + ch * 4;
+      if (grow >= p.M || gcol >= p.N) continue;
+      float4 v = *reinterpret_cast<const float4 *>(stg + row * BN + ((ch ^ (row & (CPR - 1))) << 2));
+      float *dst = static_cast<float *>(p.c) + (int64_t)grow * p.ldc + gcol;
+      if (vec && gcol + 4 <= p.N) {
+        if (p.accumulate) {
+          const float4 o = *reinterpret_cast<const float4 *>(dst);
+          v.x += o.x;
+          v.y += o.y;
+          v.z += o.z;
+          v.w += o.w;
+        }
+        *reinterpret_cast<float4 *>(dst) = v;
+      } else {
+        const float e4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (gcol + e < p.N) dst[e] = p.accumulate ? dst[e] + e4[e] : e4[e];
+      }
+    }
+  }
+};
+
 }  // namespace pipe
 
 // Operand fragments of one K-step (64 K for FP8, 64 K = 32 bytes for FP4)
