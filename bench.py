@@ -456,6 +456,9 @@ def build_cases(names, dev):
         "fp8_group_m16": lambda: fp8_case("fp8_group_m16", 16, 7168, 4096, False, group=True),
         "fp8_tensor_m4096": lambda: fp8_case("fp8_tensor_m4096", 4096, 7168, 4096, False),
         "fp8_tensor_cfg1": lambda: fp8_case("fp8_tensor_cfg1", 128, 4096, 4096, False),
+        # mid-size shapes on the 128x128 pipelined tiles (one round of tiles)
+        "fp8_tensor_m1024": lambda: fp8_case("fp8_tensor_m1024", 1024, 4096, 4096, False),
+        "fp8_block_m1024": lambda: fp8_case("fp8_block_m1024", 1024, 4096, 4096, True),
         "fp8_tensor_8192": lambda: fp8_case("fp8_tensor_8192", 8192, 8192, 8192, False),
         "mxfp4_8192": lambda: fp4_case("mxfp4_8192", 8192, 8192, 8192, "mxfp4"),
         "mxfp4_m16": lambda: fp4_case("mxfp4_m16", 16, 8192, 8192, "mxfp4"),
@@ -466,6 +469,7 @@ def build_cases(names, dev):
         "bf16_8192": lambda: bf16_case("bf16_8192", 8192, 8192, 8192),
         "bf16_m4096": lambda: bf16_case("bf16_m4096", 4096, 7168, 4096),
         "bf16_m16": lambda: bf16_case("bf16_m16", 16, 7168, 4096),
+        "bf16_m1536": lambda: bf16_case("bf16_m1536", 1536, 2048, 4096),
         "rmsnorm_quant_fp8": lambda: producer_case("rmsnorm_quant_fp8", "rmsnorm", 4096, 7168),
         "rmsnorm_then_quant_fp8": lambda: producer_case("rmsnorm_then_quant_fp8", "rmsnorm", 4096, 7168,
                                                         fused=False),
@@ -502,10 +506,10 @@ def build_cases(names, dev):
 
 
 ALL_CASES = ["fp8_block_m4096", "fp8_block_m16", "fp8_group_m4096", "fp8_group_m16",
-             "fp8_tensor_m4096", "fp8_tensor_cfg1",
+             "fp8_tensor_m4096", "fp8_tensor_cfg1", "fp8_tensor_m1024", "fp8_block_m1024",
              "fp8_tensor_8192",
              "mxfp4_8192", "mxfp4_m16", "nvfp4_m1", "nvfp4_m2048", "grouped_moe", "grouped_moe_decode",
-             "bf16_8192", "bf16_m4096", "bf16_m16",
+             "bf16_8192", "bf16_m4096", "bf16_m16", "bf16_m1536",
              "rmsnorm_quant_fp8", "rmsnorm_then_quant_fp8", "swiglu_quant_fp8", "swiglu_then_quant_fp8",
              "moe_route", "moe_permute_quant", "moe_quant_tokens", "moe_combine", "moe_grouped_permuted",
              "moe_grouped_gather", "moe_layer_cfg5", "moe_layer_decode", "moe_layer_decode_permuted", "lora_m4096", "bf16_4096",
