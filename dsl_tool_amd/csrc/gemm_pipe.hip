@@ -580,7 +580,16 @@ hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_
     if (variant == 0) return launch_pipe_cfg<PipeCfg<MODE_FP8_GCOL, 256, 256, 2, 4, 2, 128>>(p, st);
     return launch_pipe_cfg<PipeCfg<MODE_FP8_GCOL, 128, 128, 2, 2, 2, 128, 2>>(p, st);
   }
-  if (mode == MODE_BF16) return launch_pipe_cfg<PipeCfg<MODE_BF16, 128, 128, 2, 2, 4, 64>>(p, st);
+  // The 128x128 tiles run where one round of them holds the problem: one
+  // workgroup per CU, so with four waves each SIMD holds a single wave and
+  // nothing hides a stage's LDS-read latency.  FP8 per-tensor and bf16 take
+  // the fragment prefetch schedule there (same-box A/B: per-tensor
+  // 1024x4096x4096 23.4 -> 20.6 us, 1536x2048x4096 22.7 -> 19.3; bf16
+  // 1536x2048x4096 38.5 -> 33.5, fp32 out 1024x4096x4096 43.5 -> 40.0);
+  // MXFP4 takes eight waves of 64x32 instead, two per SIMD (768x4096x2048
+  // 10.5 -> 9.3 us; with the prefetch schedule it gained less).
+  if (mode == MODE_BF16)
+    return launch_pipe_cfg<PipeCfg<MODE_BF16, 128, 128, 2, 2, 4, 64, 0, 1>>(p, st);
   if (mode == MODE_FP8_BLOCK) {
     const bool ring_ok = p.K % 512 == 0 && p.K / 128 <= kBlockPfMaxGroups &&
                          (reinterpret_cast<uintptr_t>(p.sa) & 15) == 0;
@@ -602,7 +611,7 @@ hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_
       case 2: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 256, 2, 4, 4, 64>>(p, st);
       case 4: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 256, 2, 2, 4, 64, 1, 1>>(p, st);
       case 3: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 256, 128, 4, 2, 3, 128>>(p, st);
-      default: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 128, 128, 2, 2, 4, 64>>(p, st);
+      default: return launch_pipe_cfg<PipeCfg<MODE_FP8_TENSOR, 128, 128, 2, 2, 4, 64, 0, 1>>(p, st);
     }
   }
   if (mode == MODE_NVFP4) {
@@ -617,7 +626,7 @@ hipError_t launch_gemm_pipe(int mode, const GemmArgs &p, int variant, hipStream_
     case 2: return launch_pipe_cfg<PipeCfg<MODE_MXFP4, 256, 256, 2, 4, 2, 128>>(p, st);
     case 4: return launch_pipe_cfg<PipeCfg<MODE_MXFP4, 256, 256, 2, 2, 4, 64, 1, 1>>(p, st);
     case 5: return launch_pipe_cfg<PipeCfg<MODE_MXFP4, 256, 256, 2, 4, 4, 64, 0, 1>>(p, st);
-    default: return launch_pipe_cfg<PipeCfg<MODE_MXFP4, 128, 128, 2, 2, 4, 64>>(p, st);
+    default: return launch_pipe_cfg<PipeCfg<MODE_MXFP4, 128, 128, 2, 4, 4, 64>>(p, st);
   }
 }
 
