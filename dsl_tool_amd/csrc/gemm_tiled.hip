@@ -232,30 +232,31 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
   // The streaming kernel's time grows with the number of 64-row activation
   // blocks times N (each block streams all of W, and each W slice re-reads
   // its activation rows), while the 128x128 / persistent tiles stay at about
-  // one round up to a few thousand rows.  Measured at K = 4096, N = 4096,
-  // 7168, 14336, 28672, M = 48..1024 (the crossover does not move with K:
-  // both sides scale with it): past ceil(M/64) * N = 8.5 x 4096 (FP8
-  // per-tensor, MXFP4), 7.5 x 4096 (FP8 block) or 18 x 4096 (bf16) the tiles
-  // are faster (FP8 block M=256 N=14336: 31.8 against 58.1 us, M=256 N=7168
-  // streams: 33.1 against 36.4; MXFP4 M=320
-  // N=7168: 19.7 against 23.7; per-tensor M=512 N=4096 streams: 21.5
-  // against 26.7).  NVFP4 (dequantized to fp16 in the tiles) streams up to
-  // 256 rows whatever N, and above that below 15 x 4096 (M=768 N=4096: 61.8
-  // against 76.5 us; M=320 N=14336: 91.4 against 88.1).  bf16 where one
-  // round of the 128x128 pipelined tiles holds the problem: below 10 x 4096
-  // (that round costs ~45-55 us at K = 4096 whatever its size: M=512
-  // N=7168 52.9 against 67.2 us streamed; M=512 N=4096 streams, 34.7 against
-  // 51.7).  Rows of an odd number of 256-byte chunks stream in 32-row
-  // blocks: twice the blocks.
+  // one round up to a few thousand rows.  The edge is a span of
+  // 2 * ceil(M/64) * N (thr2 below, in units of 4096), measured for each
+  // mode (the crossover moves little with K: both sides scale with it).
+  // NVFP4 (dequantized to fp16 in the tiles) streams up to 256 rows whatever
+  // N, and above that below span 30 (M=768 N=4096: 61.8 against 76.5 us;
+  // M=320 N=14336: 91.4 against 88.1).  Rows of an odd number of 256-byte
+  // chunks stream in 32-row blocks: twice the blocks.
   const int64_t t128 = (int64_t)((M + 127) / 128) * ((N + 127) / 128);
   const bool bf16_pipe_round = mode == MODE_BF16 && pipe_forced != -2 && Kb % 128 == 0 && M > 64 &&
                                N > 64 && t128 >= 40 && t128 <= device_cu_count();
   if (streamable && !skinny_stream && M > 32 && (mode != MODE_NVFP4 || M > 256)) {
     const int bm = Kb % 512 == 0 ? 64 : 32;
     const int64_t span2 = 2 * (int64_t)((M + bm - 1) / bm) * N;   // twice the span
-    const int64_t thr2 = mode_grouped_k(mode) ? 15
-                         : (mode == MODE_BF16 ? (bf16_pipe_round ? 20 : 36)
-                                              : (mode == MODE_NVFP4 ? 30 : 17));
+    // crossovers re-measured against the prefetching / eight-wave 128x128
+    // tiles (same-box sweep, M = 256..1024, N = 2048..14336, K = 2048 and
+    // 4096; streamed against the tiles at the first span past the edge):
+    // per-tensor and MXFP4 stream up to span 8 x 4096 (10: 12.5 against
+    // 9.5 us, MXFP4 13.2 against 8.8), FP8 block up to 10 (14: 20.6 against
+    // 14.7), groupwise per-column up to 12 (14: 21.4 against 15.8), bf16
+    // where one round of tiles holds it up to 8 (10: 20.8 against 18.0),
+    // other bf16 below 30 (35: 53.5 against 45.4 on the persistent tiles).
+    const int64_t thr2 = mode == MODE_FP8_GCOL ? 13
+                         : mode_grouped_k(mode) ? 11
+                         : (mode == MODE_BF16 ? (bf16_pipe_round ? 9 : 30)
+                                              : (mode == MODE_NVFP4 ? 30 : 9));
     if (span2 >= thr2 * 4096) streamable = false;
   }
   // Skinny M (measured, graph timing over rotating weights): the streaming
