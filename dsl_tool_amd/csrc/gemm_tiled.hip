@@ -321,10 +321,15 @@ static Route route_for(int mode, int M, int N, int K, int Kb, bool sc4, bool sc1
     // that the 128x128 tiles, down to 40 of them: one round of those beats
     // the register-staged split-K tiles by 1.3-4.6x (M=300 N=5000 K=4096:
     // 24 against 67 us; block 31 against 149).  Measured at N = 512..14336,
-    // K = 4096 and 8192, M = 288..3072.
+    // K = 4096 and 8192, M = 288..3072.  With the prefetching 128x128 tiles
+    // FP8 per-tensor keeps two rounds of them too (same-box, M = 1536..4096,
+    // N = 2048 and 4096, K = 2048 and 4096: 7-12% ahead of the persistent
+    // kernel at six of seven shapes, 2048x4096x4096 41.1 against 42.2 us);
+    // MXFP4 does not (two rounds: 33.9 against 28.1 us at 1536x4096x4096).
     const int64_t cus = device_cu_count();
     const int64_t r128 = (t128 + cus - 1) / cus, r256 = (t256 + cus - 1) / cus;
-    const bool persist_wins = t256 >= 240 || r128 >= (mode_grouped_k(mode) ? 3 : 2) * r256;
+    const int rounds128 = (mode_grouped_k(mode) || mode == MODE_FP8_TENSOR) ? 3 : 2;
+    const bool persist_wins = t256 >= 240 || r128 >= rounds128 * r256;
     if (persist_wins) {
       r.path = PATH_PIPE;
       r.variant = pipe_forced >= 0 ? pipe_forced : (t256 >= 240 ? 0 : 1);
