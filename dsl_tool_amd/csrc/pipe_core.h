@@ -248,6 +248,22 @@ struct Ring {
       }
     }
   }
+  // copies j0 .. j1-1 of stage ks, in place like issue_next (a caller that
+  // spreads a stage over several calls issues every j once per stage)
+  DSL_DEV void issue_range(int ks, uint32_t lds0, int j0, int j1) {
+    const uint32_t base = lds0 + (uint32_t)((ks % Cfg::NS) * Cfg::STAGE);
+#pragma unroll
+    for (int j = 0; j < Cfg::D; ++j) {
+      if (j < j0 || j >= j1) continue;
+      if (j < Cfg::DD) {
+        dma16(src[j], base + dst[j]);
+        src[j] += step[j];
+      } else if (has[j]) {
+        dma4(src[j], base + dst[j]);
+        src[j] += step[j];
+      }
+    }
+  }
   DSL_DEV void issue(int ks, uint32_t lds0) const {
 #pragma unroll
     for (int j = 0; j < Cfg::D; ++j) issue_one(j, ks, lds0);
