@@ -67,6 +67,17 @@ def test_pipelined_128_tiles(m, n, k, mode, out_dtype):
     assert_close(c, ref, what=what)
 
 
+# The shortest K each mode's tiles take: two 64-byte stages (the prefetch
+# schedule's least, and an even count), or one 128-byte stage for block
+# scales.
+MIN_K = {"tensor": 128, "block": 128, "mxfp4": 256, "nvfp4": 256, "bf16": 64}
+
+
+@pytest.mark.parametrize("mode", sorted(MIN_K))
+def test_pipelined_128_tiles_shortest_k(mode):
+    test_pipelined_128_tiles(1100, 3000, MIN_K[mode], mode, torch.bfloat16)
+
+
 def test_pipelined_128_tiles_bf16_repeatable():
     # the packed staging writes leave no lane-order dependence: two runs give
     # the same bytes
