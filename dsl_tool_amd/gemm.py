@@ -359,7 +359,10 @@ def fp8_gemm(A: torch.Tensor, B: torch.Tensor, scale_a=1.0, scale_b=1.0, *,
       [ceil(N/128), ceil(K/128)] (block-scaled); or the reference's groupwise
       layout, scale_a [M, ceil(K/G)] and scale_b [ceil(K/G), N] with G =
       group_size.  2-D scales are told apart by scale_b's shape, or named
-      by granularity="block" / "group".
+      by granularity="block" / "group".  Block-scaled products
+      scale_a[m, g] * scale_b[n // 128, g] must be normal fp32 numbers (the
+      large-M kernels rescale by their ratios); the quantizers floor every
+      scale at 1e-12, as the reference's do (cuda/gemm/fp8_gemm.cu:134).
     group_size must be a multiple of 128 (the FP8 MFMA sums 128 K at a time;
     a larger G is the same sum with its scale repeated over G/128 groups).
     ``out_dtype=torch.float32`` reproduces the reference's fp32 output.

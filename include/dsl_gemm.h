@@ -128,7 +128,15 @@ size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols);
  *   DSL_SCALE_BLOCK128: scale_a [M][ceil(K/128)] (1x128 groups),
  *                       scale_b [ceil(N/128)][ceil(K/128)] (128x128 blocks);
  *                       C = sum_g (sum_{k in g} a*w) * sa[m,g] * sb[n/128,g]
- *                       (cuda/gemm/fp8_gemm.cu:84-97).
+ *                       (cuda/gemm/fp8_gemm.cu:84-97).  The large-M kernels
+ *                       carry the sum in units of the current group's
+ *                       sa*sb and rescale by the ratio of consecutive
+ *                       groups, so every product sa[m,g]*sb[n/128,g] must be
+ *                       a normal fp32 number: a zero or subnormal product
+ *                       makes that row inf/NaN there.  The quantizers here
+ *                       and the reference's floor each scale at 1e-12
+ *                       (cuda/gemm/fp8_gemm.cu:134), whose products are
+ *                       normal.
  *   DSL_SCALE_GROUP128: the reference groupwise layout with G = 128:
  *                       scale_a [M][ceil(K/128)], scale_b [ceil(K/128)][N]
  *                       (one weight scale per output column per group,
