@@ -8,6 +8,12 @@
 
 namespace dsl {
 
+// Floats between consecutive split-K partial slices in the workspace: M*N
+// rounded up to whole float4s, so that every slice starts 16-byte aligned.
+__host__ __device__ inline int64_t splitk_slice(int64_t M, int64_t N) {
+  return (M * N + 3) / 4 * 4;
+}
+
 template <int MODE, class Cfg>
 __global__ __launch_bounds__(Cfg::NT) void gemm_tiled_kernel(const GemmArgs p) {
   __shared__ __align__(16) uint8_t smem[Cfg::LDS];
@@ -74,7 +80,9 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_tiled_kernel(const GemmArgs p) {
           float v = acc[tm][tn][i];
           if constexpr (MODE == MODE_FP8_TENSOR || MODE == MODE_NVFP4) v = (v * s1) * s2;
           if (p.ksplit > 1) {
-            unsafeAtomicAdd(p.ws + (int64_t)row * p.N + col, v);
+            // this K split's own slice of the workspace: the finalize pass
+            // adds the slices in split order, so every run sums alike
+            p.ws[(int64_t)blockIdx.y * splitk_slice(p.M, p.N) + (int64_t)row * p.N + col] = v;
           } else if (p.out_f32) {
             float *d = static_cast<float *>(p.c) + (int64_t)row * p.ldc + col;
             *d = p.accumulate ? *d + v : v;
@@ -86,25 +94,27 @@ __global__ __launch_bounds__(Cfg::NT) void gemm_tiled_kernel(const GemmArgs p) {
     }
 }
 
-__global__ void fill_zero_kernel(float4 *__restrict__ p, int64_t n4) {
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4;
-       i += (int64_t)gridDim.x * blockDim.x)
-    p[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-}
-
-// Split-K finalize: C (bf16, fp32, or fp32 += for accumulate) from the fp32
-// sums in ws [M][N].  Rows over blockIdx.y (grid-stride), four columns per
-// thread; `vec`: N % 4 == 0 and C rows aligned for 16-byte (fp32) / 8-byte
-// (bf16) stores, so a thread moves its four columns with one load and one
-// store (no per-element index division).
-__global__ void splitk_finalize_kernel(const float *__restrict__ ws, void *__restrict__ c, int M,
-                                       int N, int64_t ldc, int out_f32, int accumulate, int vec) {
+// Split-K finalize: C (bf16, fp32, or fp32 += for accumulate) from the
+// ksplit fp32 partial slices in ws ([ksplit][M][N], slice stride
+// splitk_slice(M, N)), added in split order.  Rows over blockIdx.y
+// (grid-stride), four columns per thread; `vec`: N % 4 == 0 and C rows
+// aligned for 16-byte (fp32) / 8-byte (bf16) stores, so a thread moves its
+// four columns with one load per slice and one store (no per-element index
+// division).
+__global__ void splitk_finalize_kernel(const float *__restrict__ ws, int ksplit,
+                                       void *__restrict__ c, int M, int N, int64_t ldc,
+                                       int out_f32, int accumulate, int vec) {
   const int col = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (col >= N) return;
+  const int64_t slice = splitk_slice(M, N);
   for (int r = blockIdx.y; r < M; r += gridDim.y) {
     const float *src = ws + (int64_t)r * N + col;
     if (vec) {
       float4 v = *reinterpret_cast<const float4 *>(src);
+      for (int s = 1; s < ksplit; ++s) {
+        const float4 u = *reinterpret_cast<const float4 *>(src + s * slice);
+        v = make_float4(v.x + u.x, v.y + u.y, v.z + u.z, v.w + u.w);
+      }
       if (out_f32) {
         float4 *d = reinterpret_cast<float4 *>(static_cast<float *>(c) + r * ldc + col);
         if (accumulate) {
@@ -118,11 +128,13 @@ __global__ void splitk_finalize_kernel(const float *__restrict__ ws, void *__res
       }
     } else {
       for (int t = 0; t < 4 && col + t < N; ++t) {
+        float v = src[t];
+        for (int s = 1; s < ksplit; ++s) v += src[s * slice + t];
         if (out_f32) {
           float *d = static_cast<float *>(c) + r * ldc + col + t;
-          *d = accumulate ? *d + src[t] : src[t];
+          *d = accumulate ? *d + v : v;
         } else {
-          static_cast<uint16_t *>(c)[r * ldc + col + t] = f32_to_bf16(src[t]);
+          static_cast<uint16_t *>(c)[r * ldc + col + t] = f32_to_bf16(v);
         }
       }
     }
@@ -358,7 +370,7 @@ size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K, bool accu
   Route r = route_for(mode, (int)M, (int)N, (int)K, Kb, true, true);
   if (accumulate) r.path = PATH_TILED;
   return (r.path == PATH_TILED && r.tiled.ksplit > 1)
-             ? (size_t)((M * N + 3) / 4) * 4 * sizeof(float)
+             ? (size_t)r.tiled.ksplit * (size_t)splitk_slice(M, N) * sizeof(float)
              : 0;
 }
 
@@ -400,15 +412,11 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
   if (r.path == PATH_PIPE) return launch_gemm_pipe(mode, p, r.variant, st);
   if (r.path == PATH_PERSIST) return launch_gemm_persist(mode, p, st);
   const Plan pl = r.tiled;
-  // split-K only into a workspace that holds the whole [M][N] fp32 sum
-  // (rounded up to float4); otherwise one pass over K
-  const size_t need = (size_t)(((int64_t)p.M * p.N + 3) / 4) * 16;
-  p.ksplit = (p.ws && p.ws_bytes >= need) ? pl.ksplit : 1;
-  if (p.ksplit > 1) {
-    const int64_t n4 = ((int64_t)p.M * p.N + 3) / 4;   // workspace is rounded up to float4
-    fill_zero_kernel<<<(unsigned)std::min<int64_t>((n4 + 255) / 256, 4096), 256, 0, st>>>(
-        reinterpret_cast<float4 *>(p.ws), n4);
-  }
+  // split-K into as many [M][N] fp32 slices as the workspace holds (at most
+  // the plan's split count; fewer than two: one pass over K)
+  const size_t slice_bytes = (size_t)splitk_slice(p.M, p.N) * sizeof(float);
+  const size_t fit = p.ws ? p.ws_bytes / slice_bytes : 0;
+  p.ksplit = fit >= 2 ? (int)std::min<size_t>((size_t)pl.ksplit, fit) : 1;
   switch (mode) {
     case MODE_FP8_TENSOR: launch_mode<MODE_FP8_TENSOR>(pl, p, st); break;
     case MODE_FP8_BLOCK: launch_mode<MODE_FP8_BLOCK>(pl, p, st); break;
@@ -425,8 +433,8 @@ hipError_t launch_gemm(int mode, GemmArgs p, hipStream_t st) {
     const int vec = p.N % 4 == 0 && p.ldc % 4 == 0 &&
                     (reinterpret_cast<uintptr_t>(p.c) % (4 * esz)) == 0;
     const dim3 fgrid((unsigned)((p.N + 1023) / 1024), (unsigned)std::min(p.M, 4096));
-    splitk_finalize_kernel<<<fgrid, 256, 0, st>>>(p.ws, p.c, p.M, p.N, p.ldc, p.out_f32,
-                                                  p.accumulate, vec);
+    splitk_finalize_kernel<<<fgrid, 256, 0, st>>>(p.ws, p.ksplit, p.c, p.M, p.N, p.ldc,
+                                                  p.out_f32, p.accumulate, vec);
     e = hipGetLastError();
   }
   return e;

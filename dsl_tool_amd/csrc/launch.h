@@ -54,8 +54,8 @@ struct GemmArgs {
                          // MX/NV as sa for N
   const float *ga;       // FP8_TENSOR: scale_a; NV: global_a
   const float *gb;       // FP8_TENSOR: scale_b; NV: global_b
-  float *ws;             // split-K fp32 [M][N] accumulation buffer (zeroed by the launcher)
-  size_t ws_bytes;       // bytes at ws; split-K runs only when it holds the whole [M][N] sum
+  float *ws;             // split-K: one fp32 [M][N] partial slice per K split
+  size_t ws_bytes;       // bytes at ws; split-K runs only when it holds two slices or more
   int ksplit;            // >= 1
   int out_f32;
   int accumulate;        // fp32 out only: C += result (register-staged kernels)
@@ -103,7 +103,7 @@ bool stream_supported(int mode, int M, int N, int K, int Kb, bool scales16);
 hipError_t launch_gemm_stream(int mode, const GemmArgs &p, hipStream_t st);
 
 // Picks a kernel variant for the shape and launches it (plus the split-K
-// zero-fill / finalize kernels when ksplit > 1).
+// finalize kernel, which adds the slices in split order, when ksplit > 1).
 hipError_t launch_gemm(int mode, GemmArgs args, hipStream_t st);
 // Workspace the launcher will need for this shape (0 if none).
 size_t gemm_workspace_bytes(int mode, int64_t M, int64_t N, int64_t K, bool accumulate = false);

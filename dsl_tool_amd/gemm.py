@@ -83,6 +83,26 @@ def _dev_scalar(v, device) -> torch.Tensor:
     return torch.full((1,), float(v), dtype=torch.float32, device=device)
 
 
+def _out_tensor(out, rows: int, cols: int, out_dtype, device) -> torch.Tensor:
+    """The output matrix: a new [rows, cols] tensor of out_dtype, or the
+    caller's `out`, which the kernels write through (ldc = out.stride(0)), so
+    it must be exactly [rows, cols] with unit column stride, bf16 or fp32,
+    on the operands' device."""
+    if out is None:
+        return torch.empty((rows, cols), dtype=_as_dtype(out_dtype), device=device)
+    if not isinstance(out, torch.Tensor):
+        raise TypeError("out must be a tensor")
+    if out.dim() != 2 or tuple(out.shape) != (rows, cols):
+        raise ValueError(f"out must be [{rows}, {cols}] (got {list(out.shape)})")
+    if out.dtype not in (torch.bfloat16, torch.float32):
+        raise ValueError(f"out must be bfloat16 or float32 (got {out.dtype})")
+    if out.device != device:
+        raise ValueError(f"out is on {out.device}, the operands on {device}")
+    if rows > 0 and cols > 0 and (out.stride(1) != 1 or out.stride(0) < cols):
+        raise ValueError("out needs unit column stride and a row stride >= its columns")
+    return out
+
+
 def _require_gpu(*ts):
     dev = ts[0].device
     for t in ts:
@@ -204,7 +224,7 @@ def fp8_gemm_packed(qa, qw, scale_a, scale_b, *, block: bool = False, group: boo
         if tuple(scale_a.shape) != (M, nkg) or tuple(scale_b.shape) != (nkg, Nn):
             raise ValueError("groupwise scales must be [M, ceil(K/128)] and [ceil(K/128), N]")
     mode = N.SCALE_BLOCK128 if block else (N.SCALE_GROUP128 if group else N.SCALE_TENSOR)
-    c = out if out is not None else torch.empty((M, Nn), dtype=_as_dtype(out_dtype), device=dev)
+    c = _out_tensor(out, M, Nn, out_dtype, dev)
     ws = _gemm_ws(N.OP_FP8, M, Nn, K, dev)
     with torch.cuda.device(dev):
         N.call("dsl_fp8_gemm", N.ptr(qa), N.ptr(qw), N.ptr(c), M, Nn, K, c.stride(0),
@@ -238,7 +258,7 @@ def fp4_gemm_packed(qa, sa, qw, sw, *, fmt: str = "mxfp4", global_a=None, global
         raise ValueError(f"{fmt} scales must be [M, K/{blk}] and [N, K/{blk}]")
     ga = _dev_scalar(global_a, dev) if global_a is not None else None
     gw = _dev_scalar(global_w, dev) if global_w is not None else None
-    c = out if out is not None else torch.empty((M, Nn), dtype=_as_dtype(out_dtype), device=dev)
+    c = _out_tensor(out, M, Nn, out_dtype, dev)
     ws = _gemm_ws(N.OP_FP4, M, Nn, K, dev)
     with torch.cuda.device(dev):
         N.call("dsl_fp4_gemm", N.ptr(qa), N.ptr(qw), N.ptr(c), M, Nn, K, c.stride(0),
@@ -267,7 +287,7 @@ def grouped_fp8_gemm_packed(qx, sx, qw, sw, offsets, *, out_dtype=torch.bfloat16
     sw = sw.reshape(G, Nn).float().contiguous()
     if sx.numel() != T:
         raise ValueError("scale_x must have one entry per row")
-    y = out if out is not None else torch.empty((T, Nn), dtype=_as_dtype(out_dtype), device=dev)
+    y = _out_tensor(out, T, Nn, out_dtype, dev)
     with torch.cuda.device(dev):
         N.call("dsl_grouped_fp8_gemm", N.ptr(qx), N.ptr(qw), N.ptr(y), N.ptr(offsets), G, T, Nn,
                K, y.stride(0), _out_code(y.dtype), N.ptr(sx), N.ptr(sw), N.stream_of(dev))
@@ -296,7 +316,7 @@ def bf16_gemm(A: torch.Tensor, B: torch.Tensor, *, out_dtype: torch.dtype = torc
     dev = _require_gpu(A, B)
     a = A if A.is_contiguous() else A.contiguous()
     w = _k_major_weight(B)
-    c = out if out is not None else torch.empty((M, Nn), dtype=_as_dtype(out_dtype), device=dev)
+    c = _out_tensor(out, M, Nn, out_dtype, dev)
     ws = _gemm_ws(N.OP_BF16, M, Nn, K, dev)
     with torch.cuda.device(dev):
         N.call("dsl_bf16_gemm", N.ptr(a), N.ptr(w), N.ptr(c), M, Nn, K, c.stride(0),

@@ -213,3 +213,26 @@ def test_out_dtype_names_map_to_torch_dtypes():
         G._as_dtype("int8")
     with pytest.raises(ValueError):
         G._out_code(torch.float16)
+
+
+def test_caller_output_must_match_the_product():
+    """`out=` is written through by the kernels (ldc = its row stride), so a
+    wrong shape, dtype, device or column stride is refused before any launch."""
+    cpu = torch.device("cpu")
+    c = G._out_tensor(None, 3, 5, "bf16", cpu)
+    assert c.shape == (3, 5) and c.dtype == torch.bfloat16
+    out = torch.empty(3, 8)[:, :5]                       # padded rows: ldc 8 >= 5
+    assert G._out_tensor(out, 3, 5, torch.bfloat16, cpu) is out
+    bad = [torch.empty(3, 4), torch.empty(5, 3), torch.empty(15),
+           torch.empty(3, 5, dtype=torch.float16),
+           torch.empty(5, 3).t(),                        # column stride 3
+           torch.empty(3, 10)[:, ::2]]                   # column stride 2
+    for b in bad:
+        with pytest.raises(ValueError):
+            G._out_tensor(b, 3, 5, torch.float32, cpu)
+    with pytest.raises(ValueError):
+        G._out_tensor(torch.empty(3, 5), 3, 5, torch.float32, torch.device("cuda", 0))
+    with pytest.raises(TypeError):
+        G._out_tensor([[0.0] * 5] * 3, 3, 5, torch.float32, cpu)
+    # empty products take any [0, n] / [m, 0] tensor of the right shape
+    assert G._out_tensor(torch.empty(0, 5), 0, 5, torch.float32, cpu).shape == (0, 5)
