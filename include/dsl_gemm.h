@@ -181,7 +181,11 @@ int dsl_bf16_gemm(const void *a, const void *b, void *c,
  * multiply w[g] (w is [num_groups][N][K]); y [total_rows][ldy].
  * group_offsets is a device int32 array of num_groups+1 non-decreasing
  * entries, offsets[0] = 0, offsets[num_groups] = total_rows; empty groups
- * are skipped on the device.  Per-row scale_x [total_rows] and per-channel
+ * are skipped on the device.  The kernels clamp each entry into
+ * [0, total_rows] and end a group no earlier than it starts, so a malformed
+ * table never addresses outside x or y: rows no group covers are not
+ * written, and groups that overlap after the clamp write their shared rows
+ * in no defined order.  Per-row scale_x [total_rows] and per-channel
  * scale_w [num_groups][N]: y = acc * sx[r] * sw[g, n].
  * Replaces grouped_gemm (triton/gemm/gemm_kernels.py:164-182, fixed size)
  * and grouped_gemm_variable (cuda/gemm/grouped_gemm.cu:26-32, :150-156). */
