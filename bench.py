@@ -36,7 +36,10 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import shutil
+import subprocess
 import sys
+import threading
 import time
 
 ROOT = os.path.dirname(os.path.abspath(__file__))
@@ -590,6 +593,89 @@ def time_case(case, steps, warmup, dev, graph):
     return start.elapsed_time(end) / steps
 
 
+def _smi_sample(exe: str) -> list:
+    """One amd-smi reading per GPU: socket power (W), mean GFX clock over the
+    XCDs and the memory clock (MHz)."""
+    r = subprocess.run([exe, "metric", "-p", "-c", "--json"], capture_output=True, text=True,
+                       timeout=20)
+    d = json.loads(r.stdout[r.stdout.index("{"):])
+
+    def num(v):
+        v = v.get("value") if isinstance(v, dict) else None
+        return float(v) if isinstance(v, (int, float)) else None
+
+    out = []
+    for g in d.get("gpu_data", []):
+        clk = g.get("clock", {}) or {}
+        gfx = [num(v.get("clk")) for k, v in clk.items() if k.startswith("gfx_") and isinstance(v, dict)]
+        gfx = [x for x in gfx if x is not None]
+        mem = clk.get("mem_0")
+        out.append({"power_w": num((g.get("power", {}) or {}).get("socket_power")),
+                    "gfx_mhz": sum(gfx) / len(gfx) if gfx else None,
+                    "mem_mhz": num(mem.get("clk")) if isinstance(mem, dict) else None})
+    return out
+
+
+def telemetry(case, dev, seconds: float = 3.0):
+    """Socket power and clocks while `case` runs back to back (amd-smi sampled
+    from a second thread), or None where amd-smi is missing or unreadable.
+    Taken after every timed region, so it changes no timing.  With several
+    GPUs in the node, the one drawing the most power is reported."""
+    import torch
+
+    exe = shutil.which("amd-smi") or "/opt/rocm/bin/amd-smi"
+    if not os.path.exists(exe):
+        return None
+    stream = torch.cuda.Stream(device=dev)          # default priority
+    sp = stream.cuda_stream
+
+    def burst(i0, n):
+        with torch.cuda.stream(stream):
+            for i in range(i0, i0 + n):
+                if case.launch(i, sp) != 0:
+                    raise RuntimeError(f"telemetry: {case.name} launch failed")
+        torch.cuda.synchronize(dev)
+
+    t_warm = time.time() + WARM_MS / 1000.0
+    i = 0
+    while time.time() < t_warm:                       # settle the clock first
+        burst(i, 20)
+        i += 20
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            try:
+                samples.append(_smi_sample(exe))
+            except Exception:                         # unreadable: report what was read
+                return
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    t_end = time.time() + seconds
+    while th.is_alive() and (time.time() < t_end or len(samples) < 3) and time.time() < t_end + 20:
+        burst(i, 20)
+        i += 20
+    stop.set()
+    th.join(timeout=30)
+    samples = [s_ for s_ in samples if s_]
+    if not samples:
+        return None
+    ng = min(len(s_) for s_ in samples)
+
+    def mean(vals):
+        vals = [v for v in vals if v is not None]
+        return round(sum(vals) / len(vals), 1) if vals else None
+
+    per_gpu = [{k: mean([s_[g][k] for s_ in samples]) for k in ("power_w", "gfx_mhz", "mem_mhz")}
+               for g in range(ng)]
+    busy = max(per_gpu, key=lambda x: x["power_w"] or 0.0)
+    return {"case": case.name, "samples": len(samples), "socket_power_w": busy["power_w"],
+            "gfx_clock_mhz": busy["gfx_mhz"], "mem_clock_mhz": busy["mem_mhz"],
+            "source": "amd-smi metric -p -c --json, sampled while the case runs back to back "
+                      "after the timed regions"}
+
+
 TRACE_FILE = os.path.join(ROOT, "profiles", "bench_default_kernel_trace.txt")
 
 
@@ -977,6 +1063,8 @@ def main(argv=None):
     ap.add_argument("--cases", default="all",
                     help="comma list of extra cases, 'all' or 'none' (headline always runs)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-telemetry", action="store_true",
+                    help="skip the amd-smi power / clock samples of the headline case")
     ap.add_argument("--cpu-rows", type=int, default=4096)
     ap.add_argument("--profile-traffic", action="store_true",
                     help="run only the copy calibration and headline launches for rocprofv3 --pmc")
@@ -1022,7 +1110,7 @@ def main(argv=None):
 
     results = {}
     traced = read_trace_medians()
-    head_ms = None
+    head_ms, head = None, None
     for nm in names:
         log(f"case {nm}: build")
         case = build_cases([nm], dev)[nm]
@@ -1047,6 +1135,17 @@ def main(argv=None):
         del case
         torch.cuda.empty_cache()
 
+    tele = None
+    if not args.no_telemetry and not args.trace_windows and head_ms is not None:
+        log("telemetry")
+        try:
+            tele = telemetry(head, dev)
+        except Exception as e:                        # the measurement stands without it
+            log(f"telemetry unavailable: {e}")
+        log(f"telemetry: {tele}")
+    del head
+    torch.cuda.empty_cache()
+
     cpu = None
     if not args.no_cpu:
         log("cpu baseline")
@@ -1069,6 +1168,7 @@ def main(argv=None):
                      "unit": "TFLOP/s", "frac": round(h["tflops"] / PEAK_FP8_TFLOPS, 4),
                      "traffic": read_traffic()},
         "cpu_baseline": cpu,
+        "telemetry": tele,
         "cases": results,
     }
     print(json.dumps(line), flush=True)
