@@ -40,3 +40,9 @@ def test_gpus_above_one_exit_with_a_message():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"],
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2 and "one GPU" in r.stderr and r.stdout == ""
+
+
+def test_telemetry_is_null_without_amd_smi(monkeypatch):
+    monkeypatch.setattr(bench.shutil, "which", lambda name: None)
+    monkeypatch.setattr(bench.os.path, "exists", lambda p: False)
+    assert bench.telemetry(case=None, dev=None) is None
