@@ -240,6 +240,11 @@ int dsl_fp8_gemm(const uint8_t *a, const uint8_t *b, void *c, int64_t m, int64_t
   const char *fn = "dsl_fp8_gemm";
   int rc = check_gemm_dims(fn, m, n, k, ldc, 16, out_dtype);
   if (rc) return rc;
+  if (scale_mode != DSL_SCALE_TENSOR && scale_mode != DSL_SCALE_BLOCK128 &&
+      scale_mode != DSL_SCALE_GROUP128)
+    return fail(DSL_ERR_ARG, "%s: unknown scale_mode %d", fn, scale_mode);
+  // an empty product reads nothing (its block scale arrays may be empty, i.e. NULL)
+  if (m == 0 || n == 0) return ok();
   if (!scale_a || !scale_b) return fail(DSL_ERR_ARG, "%s: scale pointers must not be NULL", fn);
   if (scale_mode == DSL_SCALE_TENSOR)
     return run_gemm(fn, dsl::MODE_FP8_TENSOR, a, b, c, m, n, k, ldc, out_dtype, nullptr, nullptr,
@@ -263,6 +268,10 @@ int dsl_fp4_gemm(const uint8_t *a, const uint8_t *b, void *c, int64_t m, int64_t
   const char *fn = "dsl_fp4_gemm";
   int rc = check_gemm_dims(fn, m, n, k, ldc, 32, out_dtype);
   if (rc) return rc;
+  if (fmt != DSL_FMT_MXFP4 && fmt != DSL_FMT_NVFP4)
+    return fail(DSL_ERR_ARG, "%s: unknown fmt %d", fn, fmt);
+  // an empty product reads nothing (its scale arrays may be empty, i.e. NULL)
+  if (m == 0 || n == 0) return ok();
   if (!scale_a || !scale_b) return fail(DSL_ERR_ARG, "%s: scale pointers must not be NULL", fn);
   if (fmt == DSL_FMT_MXFP4)
     return run_gemm(fn, dsl::MODE_MXFP4, a, b, c, m, n, k, ldc, out_dtype, scale_a, scale_b,

@@ -120,6 +120,8 @@ size_t dsl_quant_workspace_bytes(int64_t rows, int64_t cols);
 /* --------------------------------------------------------------- GEMMs --
  * C[m, n] = sum_k A[m, k] * W[n, k] (the reference's A @ B with B = W^T),
  * A [M][K] and W [N][K] packed K-major, C [M][ldc] in bf16 or fp32.
+ * m == 0 or n == 0 succeeds without reading any pointer (an empty scale
+ * array may be NULL); the dimensions and mode are still checked.
  */
 
 /* FP8 E4M3 GEMM.

@@ -52,8 +52,18 @@ def test_fp8_gemm_argument_validation(lib):
     # misaligned operand
     rc = lib.dsl_fp8_gemm(fake + 1, fake, fake, 16, 16, 16, 16, 0, 0, fake, fake, None, 0, None)
     assert rc == N.DSL_ERR_ARG and "aligned" in _err(lib)
-    # empty problem is a no-op success
+    # empty problem is a no-op success, also with the empty (NULL) scale
+    # arrays of an empty block-scaled or FP4 operand; the mode is still checked
     assert lib.dsl_fp8_gemm(None, None, None, 0, 16, 16, 16, 0, 0, fake, fake, None, 0, None) == 0
+    for mode in (N.SCALE_BLOCK128, N.SCALE_GROUP128):
+        assert lib.dsl_fp8_gemm(None, None, None, 0, 16, 256, 16, 0, mode, None, None, None, 0,
+                                None) == 0
+        assert lib.dsl_fp8_gemm(None, None, None, 16, 0, 256, 0, 0, mode, None, None, None, 0,
+                                None) == 0
+    assert lib.dsl_fp4_gemm(None, None, None, 0, 16, 256, 16, 0, N.FMT_MXFP4, None, None, None,
+                            None, None, 0, None) == 0
+    rc = lib.dsl_fp8_gemm(None, None, None, 0, 16, 16, 16, 0, 7, None, None, None, 0, None)
+    assert rc == N.DSL_ERR_ARG and "scale_mode" in _err(lib)
     # groupwise (per-column weight scales): 4-byte aligned scale arrays
     rc = lib.dsl_fp8_gemm(fake, fake, fake, 16, 16, 16, 16, 0, N.SCALE_GROUP128, fake + 2, fake,
                           None, 0, None)
