@@ -97,7 +97,9 @@ int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols, int64_t sr, 
   const char *fn = "dsl_quant_fp8_tensor";
   int rc = check_input(fn, x, rows, cols, sr, sc, x_dtype);
   if (rc) return rc;
-  if (rows == 0 || cols == 0) return ok();
+  if (rows == 0 || cols == 0)   // no codes; the scale of amax 0, as the reference's
+    return scale ? hip_status(dsl::launch_empty_scale(scale, static_cast<hipStream_t>(stream)), fn)
+                 : ok();
   if ((rc = check_out(fn, q, "q"))) return rc;
   if (!scale) return fail(DSL_ERR_ARG, "%s: scale is NULL", fn);
   if (!ws || ws_bytes < dsl_quant_workspace_bytes(rows, cols))
@@ -115,7 +117,9 @@ int dsl_quant_fp8_tensor_noalloc(const void *x, int64_t rows, int64_t cols, int6
   const char *fn = "dsl_quant_fp8_tensor_noalloc";
   int rc = check_input(fn, x, rows, cols, sr, sc, x_dtype);
   if (rc) return rc;
-  if (rows == 0 || cols == 0) return ok();
+  if (rows == 0 || cols == 0)   // no codes; the scale of amax 0, as the reference's
+    return scale ? hip_status(dsl::launch_empty_scale(scale, static_cast<hipStream_t>(stream)), fn)
+                 : ok();
   if ((rc = check_out(fn, q, "q"))) return rc;
   if (!scale) return fail(DSL_ERR_ARG, "%s: scale is NULL", fn);
   if (dsl_quant_workspace_bytes(rows, cols) > dsl::quant_scratch_bytes())
@@ -169,7 +173,9 @@ int dsl_quant_nvfp4(const void *x, int64_t rows, int64_t cols, int64_t sr, int64
   if (rc) return rc;
   if (cols % 16 != 0)
     return fail(DSL_ERR_ARG, "%s: cols=%lld must be a multiple of 16", fn, (long long)cols);
-  if (rows == 0 || cols == 0) return ok();
+  if (rows == 0 || cols == 0)   // no codes; the global scale of amax 0
+    return gscale ? hip_status(dsl::launch_empty_scale(gscale, static_cast<hipStream_t>(stream)), fn)
+                  : ok();
   if ((rc = check_out(fn, q, "q_packed"))) return rc;
   if (!e4m3s || !gscale) return fail(DSL_ERR_ARG, "%s: scale output is NULL", fn);
   if (!ws || ws_bytes < dsl_quant_workspace_bytes(rows, cols))

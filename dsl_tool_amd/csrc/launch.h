@@ -22,6 +22,9 @@ hipError_t launch_quant_mxfp4(const void *x, bool f32, int64_t rows, int64_t col
 hipError_t launch_quant_nvfp4(const void *x, bool f32, int64_t rows, int64_t cols, int64_t sr,
                               int64_t sc, uint8_t *q, uint8_t *e4m3s, float *gscale,
                               float *partial, hipStream_t st);
+// The scale an empty tensor quantizes to (amax 0: the 1e-12 floor), written
+// to *scale by one thread.
+hipError_t launch_empty_scale(float *scale, hipStream_t st);
 // Device address of the library-held amax partials on the current device
 // (looked up once per device); nullptr and *err set on failure.
 float *quant_scratch(hipError_t *err);

@@ -713,6 +713,13 @@ float *quant_scratch(hipError_t *err) {
 
 size_t quant_scratch_bytes() { return sizeof(scratch); }
 
+__global__ void empty_scale_kernel(float *scale) { *scale = kScaleFloor; }
+
+hipError_t launch_empty_scale(float *scale, hipStream_t st) {
+  empty_scale_kernel<<<1, 1, 0, st>>>(scale);
+  return hipGetLastError();
+}
+
 hipError_t launch_quant_fp8_tensor(const void *xv, bool f32, int64_t rows, int64_t cols,
                                    int64_t sr, int64_t sc, uint8_t *q, float *scale,
                                    float *partial, hipStream_t st) {

@@ -63,7 +63,8 @@ int dsl_abi_version(void);
 
 /* Per-tensor E4M3.  scale = max(amax/448, 1e-12); q = e4m3(x / scale).
  * Replaces quantize_to_fp8_kernel (cuda/gemm/fp8_gemm.cu:118-144).
- * Writes one float to *scale.  Needs dsl_quant_workspace_bytes(R, C). */
+ * Writes one float to *scale (1e-12 for an empty tensor, when scale is not
+ * NULL).  Needs dsl_quant_workspace_bytes(R, C). */
 int dsl_quant_fp8_tensor(const void *x, int64_t rows, int64_t cols,
                          int64_t stride_row, int64_t stride_col, int x_dtype,
                          uint8_t *q, float *scale,
@@ -107,7 +108,8 @@ int dsl_quant_mxfp4(const void *x, int64_t rows, int64_t cols,
 /* NVFP4: s_g = max(amax_T/2688, 1e-12); per row and 16 K elements
  * s_b = e4m3((amax_16/6)/s_g); codes = e2m1_rne_sat(x / (f32(s_b)*s_g)),
  * all-zero codes where that denominator is 0.  q_packed [R][C/2],
- * e4m3_scales [R][C/16], *global_scale = s_g.  C % 16 == 0.
+ * e4m3_scales [R][C/16], *global_scale = s_g (1e-12 for an empty tensor,
+ * when global_scale is not NULL).  C % 16 == 0.
  * Same reference function replaced as dsl_quant_mxfp4. */
 int dsl_quant_nvfp4(const void *x, int64_t rows, int64_t cols,
                     int64_t stride_row, int64_t stride_col, int x_dtype,

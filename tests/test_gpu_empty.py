@@ -36,6 +36,13 @@ def test_quantizers_with_no_rows():
     assert tuple(q.shape) == (0, 256) and tuple(s.shape) == (0, 2)
     q, e = Q.quant_mxfp4(x)
     assert tuple(q.shape) == (0, 128) and tuple(e.shape) == (0, 8)
+    # the per-tensor and NVFP4 global scales of an empty tensor are those of
+    # amax 0: the 1e-12 floor (cuda/gemm/fp8_gemm.cu:133-134), not left unset
+    q, s = Q.quant_fp8_tensor(x)
+    assert tuple(q.shape) == (0, 256) and s.item() == torch.tensor(1e-12, dtype=torch.float32).item()
+    q, sb, sg = Q.quant_nvfp4(x)
+    assert tuple(q.shape) == (0, 128) and tuple(sb.shape) == (0, 16)
+    assert sg.item() == torch.tensor(1e-12, dtype=torch.float32).item()
 
 
 def test_grouped_with_every_group_empty():
