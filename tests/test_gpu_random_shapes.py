@@ -94,3 +94,15 @@ def test_random_shape(mode, m, n, k):
             ref = OF.round_to_bf16(ref)
     assert c.dtype == out_dtype and tuple(c.shape) == (m, n)
     assert_close(c, ref, what=what)
+
+
+# The smallest K each mode accepts (one MFMA step or less), at row counts that
+# take the decode, streaming, 128x128 and persistent routes (or their
+# short-K fallbacks).
+MIN_K_CASES = [(mode, m, 512, {"bf16": 8, "mxfp4": 32, "nvfp4": 32}.get(mode, 16))
+               for mode in sorted(UNIT) for m in (1, 16, 300, 4096)]
+
+
+@pytest.mark.parametrize("mode,m,n,k", MIN_K_CASES, ids=lambda v: str(v))
+def test_minimum_k(mode, m, n, k):
+    test_random_shape(mode, m, n, k)
