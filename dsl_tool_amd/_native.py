@@ -134,3 +134,22 @@ def ptr(t) -> int | None:
 
 def stream_of(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+def vec_rows(t: torch.Tensor, ld_mult: int | None = None) -> torch.Tensor:
+    """``t`` in a layout the kernels read in 16-byte vectors: a 16-byte
+    aligned start and either row-major contiguous storage (``ld_mult=None``,
+    for entry points that take no row stride) or unit column stride with a
+    row stride of at least one row and a multiple of ``ld_mult`` elements.
+    The C ABI refuses anything else, so any other view (an odd storage
+    offset, a transposed or padded one) is copied into fresh row-major
+    storage, which the allocator aligns."""
+    if ld_mult is None:
+        ok = t.is_contiguous()
+    else:
+        ok = t.stride(-1) == 1 and t.stride(0) >= t.shape[-1] and t.stride(0) % ld_mult == 0
+    if ok and t.data_ptr() % 16 == 0:
+        return t
+    out = torch.empty(t.shape, dtype=t.dtype, device=t.device)
+    out.copy_(t)
+    return out

@@ -32,9 +32,7 @@ def _rows2d(x: torch.Tensor, name: str) -> torch.Tensor:
         raise ValueError(f"{name}: tensor must be on a GPU device (got {x.device})")
     if x.dtype != torch.bfloat16:
         raise TypeError(f"{name}: input must be bfloat16 (got {x.dtype})")
-    if x.stride(1) != 1:
-        x = x.contiguous()
-    return x
+    return N.vec_rows(x, 8)
 
 
 def _outputs(rows: int, cols: int, fmt: str, dev, return_y: bool):

@@ -167,6 +167,7 @@ def _u8(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.uint8 else t.view(torch.uint8)
 
 
+
 def _gemm_ws(op: int, m: int, n: int, k: int, device) -> torch.Tensor | None:
     nbytes = N.lib().dsl_gemm_workspace_bytes(op, m, n, k)
     return torch.empty(nbytes // 4, dtype=torch.float32, device=device) if nbytes else None
@@ -209,7 +210,7 @@ def fp8_gemm_packed(qa, qw, scale_a, scale_b, *, block: bool = False, group: boo
     if block and group:
         raise ValueError("block and group scales are exclusive")
     dev = _require_gpu(qa, qw, scale_a, scale_b)
-    qa, qw = _u8(qa).contiguous(), _u8(qw).contiguous()
+    qa, qw = N.vec_rows(_u8(qa)), N.vec_rows(_u8(qw))
     M, K = qa.shape
     Nn, K2 = qw.shape
     if K != K2:
@@ -239,7 +240,7 @@ def fp4_gemm_packed(qa, sa, qw, sw, *, fmt: str = "mxfp4", global_a=None, global
     even K).  MXFP4: sa [M, K/32], sw [N, K/32] E8M0 bytes.  NVFP4: sa [M, K/16],
     sw [N, K/16] E4M3 bytes plus 1-element float32 global scales."""
     dev = _require_gpu(qa, qw, sa, sw)
-    qa, qw = _u8(qa).contiguous(), _u8(qw).contiguous()
+    qa, qw = N.vec_rows(_u8(qa)), N.vec_rows(_u8(qw))
     sa, sw = _u8(sa).contiguous(), _u8(sw).contiguous()
     M, Kh = qa.shape
     Nn, Kh2 = qw.shape
@@ -275,7 +276,7 @@ def grouped_fp8_gemm_packed(qx, sx, qw, sw, offsets, *, out_dtype=torch.bfloat16
     scales, sw [G, N] per-channel scales.  Returns y [T, N].
     """
     dev = _require_gpu(qx, qw, sx, sw, offsets)
-    qx, qw = _u8(qx).contiguous(), _u8(qw).contiguous()
+    qx, qw = N.vec_rows(_u8(qx)), N.vec_rows(_u8(qw))
     T, K = qx.shape
     G, Nn, K2 = qw.shape
     if K != K2:
@@ -314,8 +315,8 @@ def bf16_gemm(A: torch.Tensor, B: torch.Tensor, *, out_dtype: torch.dtype = torc
     if K != K2:
         raise ValueError(f"K mismatch: A is [{M}, {K}], B is [{K2}, {Nn}]")
     dev = _require_gpu(A, B)
-    a = A if A.is_contiguous() else A.contiguous()
-    w = _k_major_weight(B)
+    a = N.vec_rows(A)
+    w = N.vec_rows(_k_major_weight(B))
     c = _out_tensor(out, M, Nn, out_dtype, dev)
     ws = _gemm_ws(N.OP_BF16, M, Nn, K, dev)
     with torch.cuda.device(dev):
@@ -344,10 +345,10 @@ def lora_fused_gemm(X: torch.Tensor, W: torch.Tensor, loraA: torch.Tensor, loraB
     if K != K2 or K != K3 or tuple(loraB.shape) != (L, R, Nn):
         raise ValueError("lora_fused_gemm: shapes do not match")
     dev = _require_gpu(X, W, loraA, loraB)
-    x = X if X.is_contiguous() else X.contiguous()
-    w = _k_major(W)                                                 # [N, K]
-    a_t = loraA.permute(0, 2, 1).reshape(L * R, K).contiguous()     # row l*R + r = A_l[:, r]
-    b_t = loraB.permute(2, 0, 1).reshape(Nn, L * R).contiguous()    # col l*R + r = B_l[r, :]
+    x = N.vec_rows(X)
+    w = N.vec_rows(_k_major(W))                                     # [N, K]
+    a_t = N.vec_rows(loraA.permute(0, 2, 1).reshape(L * R, K))      # row l*R + r = A_l[:, r]
+    b_t = N.vec_rows(loraB.permute(2, 0, 1).reshape(Nn, L * R))     # col l*R + r = B_l[r, :]
     if isinstance(scales, torch.Tensor):
         s = scales.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
     else:

@@ -73,8 +73,7 @@ def moe_permute_quant(x: torch.Tensor, route: Route):
     _gpu(x, "x")
     if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] != route.tokens:
         raise ValueError("x must be bf16 [tokens, K]")
-    if x.stride(1) != 1:
-        x = x.contiguous()
+    x = N.vec_rows(x, 8)
     T, K = x.shape
     rows = T * route.topk
     qx = torch.empty((rows, K), dtype=torch.uint8, device=x.device)
@@ -94,8 +93,7 @@ def moe_quant_tokens(x: torch.Tensor, route: Route):
     _gpu(x, "x")
     if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[0] != route.tokens:
         raise ValueError("x must be bf16 [tokens, K]")
-    if x.stride(1) != 1:
-        x = x.contiguous()
+    x = N.vec_rows(x, 8)
     T, K = x.shape
     rows = T * route.topk
     qx = torch.empty((T, K), dtype=torch.uint8, device=x.device)
@@ -130,8 +128,7 @@ def moe_route_quant_tokens(topk_ids: torch.Tensor, x: torch.Tensor, num_experts:
         raise ValueError("x must be bf16 [tokens, K]")
     T, k = topk_ids.shape
     K = x.shape[1]
-    if x.stride(1) != 1 or x.stride(0) % 8 != 0:
-        x = x.contiguous()
+    x = N.vec_rows(x, 8)
     if not route_quant_applies(T, k, num_experts, K):
         route = moe_route(topk_ids, num_experts)
         qx, sx = moe_quant_tokens(x, route)
@@ -158,7 +155,7 @@ def moe_grouped_fp8_gemm(qx: torch.Tensor, sx: torch.Tensor, route: Route, qw: t
     expert's ``qw [E, N, K]``; ``y [T*topk, N]`` in sorted order, as
     ``grouped_fp8_gemm_packed`` over the permuted copy gives."""
     dev = G._require_gpu(qx, qw, sx, sw)
-    qx, qw = G._u8(qx).contiguous(), G._u8(qw).contiguous()
+    qx, qw = N.vec_rows(G._u8(qx)), N.vec_rows(G._u8(qw))
     T, K = qx.shape
     E, Nn, K2 = qw.shape
     if K != K2 or T != route.tokens or E != route.num_experts:
