@@ -963,7 +963,10 @@ void gemm_persist_kernel(const Args p) {
     bool quad;
     int qq;
     uint32_t islot;
-    issue_next(0, quad, qq, islot);
+    // grouped: the whole of pair gp+2 is issued here, right after the
+    // barrier, so its copies get the most lead over the misses that a
+    // group's W panels take (dense: spread over the MFMA rows below)
+    issue_next(GR ? -1 : 0, quad, qq, islot);
     // the compute cursor moves to pair gp+1 (the next tile's first pair
     // after KIND 2)
     cq = KIND == 2 ? 0 : cq + 1;
@@ -985,7 +988,7 @@ void gemm_persist_kernel(const Args p) {
         issue_part(i, qq, islot, quad);
       } else {
         pers::mma_row<Cfg, 1>(fa, fb[1], i, acc);
-        issue_part(i, qq, islot, quad);
+        if constexpr (!GR) issue_part(i, qq, islot, quad);
         if constexpr (KIND != 2) fa.load_a(stn, sqn, sw, 0, i, wm, r32, h);
       }
       __builtin_amdgcn_sched_barrier(0);
